@@ -1,0 +1,194 @@
+"""Benchmark: one step of the continuous-batching decode path on one MI355X.
+
+A step is the slot-mapped write of the 256 new K/V rows followed by ragged
+paged GQA decode attention over 256 sequences (context
+log-uniform in [128, 32768], 16 q / 2 kv heads, head_dim 128, block 128,
+random block tables over a 65536-block bf16 pool). Inputs are resident in HBM
+before the timed region. Prints one JSON line (rank 0).
+
+value  = algorithmic bytes of the step / step time  (GB/s)
+roofline: the attention operator's algorithmic bytes / its average duration
+          measured with HIP events on the launch stream, against 8 TB/s.
+cpu_baseline: the C++ CPU oracle (a restatement of the reference's CPU
+          algorithm) timed on this host over a bounded sample of the workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-seqs", type=int, default=64)
+    return ap.parse_args()
+
+
+def gpu_workload(seed):
+    import torch
+    from ironpangu_amd import workloads as W
+    kw = dict(W.CONFIGS["decode"])
+    case = W.decode_meta(seed, **kw)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    nslot = case.pool_blocks * case.block_size
+    shape = (case.pool_blocks, case.block_size, case.kv_heads, case.head_dim)
+
+    def randn(*s):
+        return torch.randn(*s, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+
+    k_cache = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    v_cache = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    # fill in slabs to bound the fp32 temporary
+    for t in (k_cache, v_cache):
+        flat = t.view(-1)
+        step = 1 << 28
+        for i in range(0, flat.numel(), step):
+            n = min(step, flat.numel() - i)
+            flat[i:i + n] = randn(n)
+    q = randn(case.num_seqs, case.q_heads, case.head_dim)
+    k_new = randn(case.num_seqs, case.kv_heads, case.head_dim)
+    v_new = randn(case.num_seqs, case.kv_heads, case.head_dim)
+    t = {
+        "q": q, "k_new": k_new, "v_new": v_new, "k_cache": k_cache, "v_cache": v_cache,
+        "tables": torch.from_numpy(case.block_tables).to(dev),
+        "lens": torch.from_numpy(case.seq_lens).to(dev),
+        "slots": torch.from_numpy(case.slot_mapping.astype(np.int64)).to(dev),
+    }
+    del nslot
+    return case, t
+
+
+def cpu_baseline(seed, sample_seqs):
+    """Time the CPU oracle on the first `sample_seqs` sequences of the same
+    length distribution (bounded sample), with this host's CPU share."""
+    import oracle
+    from ironpangu_amd import workloads as W
+    kw = dict(W.CONFIGS["decode"])
+    full = W.decode_meta(seed, **kw)
+    lens = full.seq_lens[:sample_seqs].copy()
+    bs, hkv, hd, hq = full.block_size, full.kv_heads, full.head_dim, full.q_heads
+    rng = np.random.default_rng(seed + 7)
+    need = int(((lens + bs - 1) // bs).sum())
+    table = W.block_tables_for(rng, lens, bs, need, full.block_tables.shape[1])
+    nslot = need * bs
+    k = W.bf16_randn(rng, (nslot, hkv, hd))
+    v = W.bf16_randn(rng, (nslot, hkv, hd))
+    q = W.bf16_randn(rng, (len(lens), hq, hd))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.paged_decode(q, k, v, table, np.minimum(lens, 64), hq, hkv, hd, bs, full.scale,
+                        threads=threads)  # warm
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.paged_decode(q, k, v, table, lens, hq, hkv, hd, bs, full.scale, threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 20:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    b = W.decode_bytes(lens, hq, hkv, hd, bs, with_write=False)["attention"]
+    return {"value": round(b / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "tokens_per_s": round(len(lens) / dt, 1), "seconds_per_pass": round(dt, 4),
+            "sample": f"oracle_paged_decode (fp32 C++ restatement) over the first {len(lens)} of "
+                      f"the 256 config-2 sequences ({int(lens.sum())} context tokens), "
+                      f"{reps} passes"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (each GPU box "
+                                   "has a single MI355X, and the decode path shards by sequence "
+                                   "with no cross-GPU exchange)"}))
+        sys.exit(2)
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+
+    case, t = gpu_workload(args.seed)
+    ws = ops.decode_workspace(case.num_seqs, case.q_heads, case.head_dim, case.max_context)
+    out = torch.empty_like(t["q"])
+    stream = torch.cuda.current_stream()
+
+    def step(ev=None):
+        ops.kv_cache_write(t["k_new"], t["v_new"], t["k_cache"], t["v_cache"], t["slots"])
+        if ev is not None:
+            ev[0].record(stream)
+        ops.paged_decode(t["q"], t["k_cache"], t["v_cache"], t["tables"], t["lens"],
+                         case.max_context, case.scale, out=out, workspace=ws)
+        if ev is not None:
+            ev[1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(args.steps):
+        step(evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(end) / args.steps
+    attn_ms = [a.elapsed_time(b) for a, b in evs]
+    attn_avg = float(np.mean(attn_ms))
+
+    nbytes = W.decode_bytes(case.seq_lens, case.q_heads, case.kv_heads, case.head_dim,
+                            case.block_size)
+    value = nbytes["total"] / (ms_step * 1e-3) / 1e9
+    achieved = nbytes["attention"] / (attn_avg * 1e-3) / 1e9
+    res = {
+        "metric": "paged-decode attention GB/s (% of 8 TB/s HBM) + decode tokens/s, 256 ragged seqs",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 caches, random block tables)",
+        "config": {"workload": "ragged_paged_decode_256 (BASELINE config 2)",
+                   "num_seqs": case.num_seqs, "context": "log-uniform [128, 32768]",
+                   "total_context_tokens": int(case.seq_lens.sum()),
+                   "q_heads": case.q_heads, "kv_heads": case.kv_heads,
+                   "head_dim": case.head_dim, "block_size": case.block_size,
+                   "pool_blocks": case.pool_blocks, "parallelism": "none (1 GPU)"},
+        "tokens_per_s": round(case.num_seqs / (ms_step * 1e-3), 1),
+        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes_per_step": nbytes["total"],
+        "roofline": {"bound": "hbm", "kernel": "paged_decode (decode + split-K merge launches)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "avg_ms": round(attn_avg, 5),
+                     "algorithmic_bytes": nbytes["attention"]},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_sample_seqs)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

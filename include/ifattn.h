@@ -1,0 +1,163 @@
+/* ifattn — MI355X (gfx950) continuous-batching attention path, C ABI.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t passed
+ * as void*. Nothing here allocates device memory, synchronizes, or changes the
+ * caller's stream; calls are asynchronous on `stream` and safe to record into a
+ * HIP graph (all control data is read on the device). Functions return an
+ * int32 status (0 = OK, negative = error) and leave a thread-local message in
+ * ifattn_last_error(), the boundary convention of the reference
+ * (native/src/inferfabric_acl.cpp:46-58, native/src/program_engine.cpp:274-278).
+ *
+ * Layouts (row-major, contiguous):
+ *   GQA caches     K, V : [num_blocks * block_size, kv_heads, head_dim]  (bf16 or int8)
+ *                  this is the reference's flattened slot-row cache [slots, kv_heads*head_dim]
+ *                  (native/src/inferfabric_acl.cpp:1359-1362); slot = block*block_size + offset.
+ *   C8 scales           : [num_blocks * block_size, kv_heads] fp32
+ *   MLA cache (bf16)    : [num_blocks * block_size, 576]       (token_executor.h:749)
+ *   MLA cache (C8)      : [num_blocks * block_size, 656] bytes (docs/packed-mla-cache.md:27-43)
+ *   block tables        : [num_seqs, table_stride] int32        (page_binding.h:132-160)
+ *   q / out (decode)    : [num_seqs, q_heads, head_dim] bf16
+ *   q / out (prefill)   : [total_q_rows, q_heads, head_dim] bf16, packed by cu_seqlens_q
+ */
+#ifndef IFATTN_H
+#define IFATTN_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFATTN_OK 0
+#define IFATTN_EINVAL (-1)  /* argument / contract violation, nothing launched */
+#define IFATTN_ELAUNCH (-2) /* HIP launch error */
+#define IFATTN_EWORKSPACE (-3)
+
+/* Dtype codes: 1..3 are the reference's IFKernelTensorV1 codes
+ * (native/include/inferfabric_kernel_v1.h:7); 4 and 5 are additive. */
+#define IFATTN_DTYPE_I8 1
+#define IFATTN_DTYPE_BF16 2
+#define IFATTN_DTYPE_F32 3
+#define IFATTN_DTYPE_I32 4
+#define IFATTN_DTYPE_I64 5
+
+#define IFATTN_ABI_VERSION 1
+
+int32_t ifattn_abi_version(void);
+const char *ifattn_last_error(void);
+
+/* ---- slot-mapped cache writes ------------------------------------------------ */
+
+/* cache[slot_mapping[r]] = rows[r] for K and (optionally) V. Rows are row_bytes
+ * each (a multiple of 16: 1024 B for 2 kv heads x 128 bf16, 1152 B for an MLA
+ * latent row). slot_mapping holds int32 or int64 physical slots; negative or
+ * >= num_slots entries are skipped. Bit copy.
+ * Replaces aclnnScatterNdUpdate x2 in inferfabric_acl_paged_attention_prepare
+ * (native/src/inferfabric_acl.cpp:1364-1376) and aclnnInplaceIndexCopy of the
+ * MLA cache (native/src/token_executor.h:733-757). */
+int32_t ifattn_kv_cache_write(const void *k_rows, const void *v_rows, void *k_cache,
+                              void *v_cache, const void *slot_mapping, int32_t slot_dtype,
+                              int64_t rows, int64_t row_bytes, int64_t num_slots, void *stream);
+
+/* Quantizing write, int8 with one fp32 scale per (token, kv head):
+ * scale = max|x|/127 (1.0 for an all-zero row), q = round-half-even(x/scale)
+ * clamped to +-127. Rows bf16 [rows, kv_heads, head_dim].
+ * Replaces the row-quantized cache write (native/kernels/cache_quantization.cpp:12-38,
+ * token_executor.h:795-810) at the per_token_head granularity of
+ * crates/inferfabric-authoring/src/execution.rs:65-66. */
+int32_t ifattn_kv_cache_write_c8(const void *k_rows, const void *v_rows, void *k_cache,
+                                 void *v_cache, void *k_scale, void *v_scale,
+                                 const void *slot_mapping, int32_t slot_dtype, int64_t rows,
+                                 int32_t kv_heads, int32_t head_dim, int64_t num_slots,
+                                 void *stream);
+
+/* Packed C8 MLA latent write: 576 bf16 (512 latent + 64 rope) per row ->
+ * 656-byte row {int8[512], bf16 rope[64], f32 scale[4]}, scale per 128-value
+ * tile = max/127 (0 for a zero tile), nearest-even codes. Replaces the cache
+ * storage half of aclnnAiInfraKvRmsNormRopeCache pertile128
+ * (native/src/resident_cache_writer.h:5-20; docs/packed-mla-cache.md:27-43). */
+int32_t ifattn_mla_cache_write_c8(const void *rows, void *cache, const void *slot_mapping,
+                                  int32_t slot_dtype, int64_t rows_count, int64_t num_slots,
+                                  void *stream);
+
+/* ---- paged decode (one query row per sequence) --------------------------------- */
+
+/* Workspace bytes for the split-K partials of the decode kernels. */
+uint64_t ifattn_paged_decode_workspace_size(int32_t num_seqs, int32_t q_heads, int32_t head_dim,
+                                            int32_t max_context);
+
+/* Ragged paged GQA decode, bf16 caches. For each sequence b and q head h
+ * (kv head h / (q_heads/kv_heads)): softmax(scale * q.K[0..len_b)) . V with fp32
+ * accumulation; len_b = seq_lens[b] (>= 1, clamped to max_context).
+ * head_dim 64/128/256, q_heads/kv_heads <= 16, block_size a multiple of 32,
+ * table_stride*block_size >= max_context.
+ * Replaces the gather + matmul + fp32 softmax + matmul sequence of
+ * inferfabric_acl_paged_attention_prepare (native/src/inferfabric_acl.cpp:1377-1428)
+ * without the gather copy; CPU oracle crates/inferfabric-cli/src/npu_probe/attention.rs:221-253. */
+int32_t ifattn_paged_decode_bf16(const void *q, const void *k_cache, const void *v_cache,
+                                 const int32_t *block_tables, int32_t table_stride,
+                                 const int32_t *seq_lens, void *out, int32_t num_seqs,
+                                 int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                 int32_t block_size, int64_t num_blocks, int32_t max_context,
+                                 float scale, void *workspace, uint64_t workspace_bytes,
+                                 void *stream);
+
+/* Same over an int8 cache with fp32 scales per (token, kv head), dequantized in
+ * registers (replaces cache_dequantize + bf16 attention, token_executor.h:812-822). */
+int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, const void *v_cache,
+                               const void *k_scale, const void *v_scale,
+                               const int32_t *block_tables, int32_t table_stride,
+                               const int32_t *seq_lens, void *out, int32_t num_seqs,
+                               int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                               int32_t block_size, int64_t num_blocks, int32_t max_context,
+                               float scale, void *workspace, uint64_t workspace_bytes,
+                               void *stream);
+
+/* ---- packed varlen chunked prefill -------------------------------------------- */
+
+uint64_t ifattn_varlen_prefill_workspace_size(int32_t num_seqs, int32_t total_q, int32_t q_heads,
+                                              int32_t head_dim, int32_t max_kv_len);
+
+/* Packed TND batch: sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1])
+ * and kv_lens[s] cached keys (prior context + this chunk, already written).
+ * Row t of a chunk of `count` rows sees keys [0, kv_len - count + t]
+ * (causal rule of native/src/openpangu_attention_metadata.h:20-22; writes precede
+ * queries, native/include/sliding_window_layout.h:7). Sequences with one row are
+ * decode rows. Replaces the TND attention call of token_executor.h:863-906 /
+ * resident_window_attention.h:17-31 (without window/sinks). */
+int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache, const void *v_cache,
+                                   const int32_t *block_tables, int32_t table_stride,
+                                   const int32_t *cu_seqlens_q, const int32_t *kv_lens, void *out,
+                                   int32_t num_seqs, int32_t total_q, int32_t max_q_len,
+                                   int32_t max_kv_len, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, int32_t block_size, int64_t num_blocks,
+                                   float scale, void *workspace, uint64_t workspace_bytes,
+                                   void *stream);
+
+/* ---- packed MLA latent decode -------------------------------------------------- */
+
+uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads, int32_t max_context);
+
+/* q [num_seqs, heads, 576] bf16 (512 absorbed latent + 64 rope); cache rows of
+ * 576 bf16; s_j = scale * q.row_j, o = softmax(s) . row_j[0:512];
+ * out [num_seqs, heads, 512] bf16. heads <= 16 per call.
+ * Replaces the BF16 latent attention (token_executor.h:863-906); CPU oracle
+ * native/probes/sliding_window_probe.cpp:144-163 without sinks/window. */
+int32_t ifattn_mla_decode_bf16(const void *q, const void *cache, const int32_t *block_tables,
+                               int32_t table_stride, const int32_t *seq_lens, void *out,
+                               int32_t num_seqs, int32_t heads, int32_t block_size,
+                               int64_t num_blocks, int32_t max_context, float scale,
+                               void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* Same over the packed 656-byte C8 rows: latent = int8 * scale[d/128], rope bf16
+ * (native/probes/packed_cache_probe.cpp:57); replaces
+ * aclnnAiInfraKvQuantSparseFlashAttention on dense causal candidates
+ * (token_executor.h:841-852) without learned sinks. */
+int32_t ifattn_mla_decode_c8(const void *q, const void *cache, const int32_t *block_tables,
+                             int32_t table_stride, const int32_t *seq_lens, void *out,
+                             int32_t num_seqs, int32_t heads, int32_t block_size,
+                             int64_t num_blocks, int32_t max_context, float scale,
+                             void *workspace, uint64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IFATTN_H */

@@ -1,0 +1,73 @@
+// Shared device helpers for the gfx950 attention-path kernels.
+//
+// bf16 rounding is round-to-nearest-even on the fp32 bit pattern, the rule the
+// reference uses everywhere it narrows to bf16
+// (crates/inferfabric-cli/src/npu_probe.rs:151-154,
+//  native/kernels/cache_quantization.cpp:9-12). NaN inputs stay quiet NaN here
+// (the reference rule would also produce a NaN pattern, but not a canonical one).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifattn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+// Two fp32 -> packed bf16 pair (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// v_perm_b32 byte select: result byte i = byte sel[i] of {hi:lo} (lo = bytes 0-3).
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// Low bf16 halves of two dwords -> one dword {a.lo, b.lo}.
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x05040100u);
+}
+// High bf16 halves of two dwords -> one dword {a.hi, b.hi}.
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return perm_b32(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+__device__ __forceinline__ float wave_sum_xor(float v, int mask) {
+  return v + __shfl_xor(v, mask, 64);
+}
+
+template <typename T>
+__device__ __forceinline__ T uniform(T v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+__device__ __forceinline__ u32x4 load_u32x4(const void *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ void store_u32x4(void *p, u32x4 v) {
+  *reinterpret_cast<u32x4 *>(p) = v;
+}
+
+}  // namespace ifattn

@@ -1,0 +1,266 @@
+"""Torch-tensor wrappers over the C ABI (device memory and streams come from
+torch; every kernel is the native gfx950 code in ``libifattn_hip.so``).
+
+Shapes are validated on the host before any launch so that a kernel never
+runs on operands that disagree with its grid. Each call is asynchronous on
+torch's current stream (or ``stream`` when given).
+
+Cache layouts (see include/ifattn.h):
+  GQA K/V cache  [num_blocks, block_size, kv_heads, head_dim]   bf16 or int8
+  C8 scales      [num_blocks, block_size, kv_heads]             fp32
+  MLA cache      [num_blocks, block_size, 576] bf16 or [num_blocks, block_size, 656] uint8
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from ._native import check, lib
+
+I32, I64 = 4, 5
+
+
+def _stream(stream):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _req(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _req(t.is_cuda, "all tensors must be on the GPU")
+        _req(t.is_contiguous(), "all tensors must be contiguous")
+        dev = dev or t.device
+        _req(t.device == dev, "all tensors must be on one device")
+
+
+def _slot_dtype(slots):
+    _req(slots.dtype in (torch.int32, torch.int64), "slot_mapping must be int32 or int64")
+    return I32 if slots.dtype == torch.int32 else I64
+
+
+# ---------------------------------------------------------------- cache writes
+
+def kv_cache_write(k, v, k_cache, v_cache, slot_mapping, stream=None):
+    """cache[slot_mapping[r]] = rows[r] (bit copy) for K and, if given, V.
+
+    k, v: [rows, ...]; caches: [num_blocks, block_size, ...] with the same
+    per-token row; slot_mapping: [rows] int32/int64 physical token rows.
+    """
+    _dev(k, v, k_cache, v_cache, slot_mapping)
+    rows = k.shape[0]
+    row_bytes = k[0].numel() * k.element_size() if rows else 0
+    _req(slot_mapping.numel() == rows, "one slot per row")
+    _req(k_cache.dtype == k.dtype, "row and cache dtypes differ")
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
+    _req(k_cache.numel() * k_cache.element_size() == num_slots * row_bytes or rows == 0,
+         "cache row width differs from input row width")
+    if v is not None:
+        _req(v.shape == k.shape and v_cache.shape == k_cache.shape, "K/V shapes differ")
+    check(lib().ifattn_kv_cache_write(_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+                                      _ptr(slot_mapping), _slot_dtype(slot_mapping), rows,
+                                      max(row_bytes, 16), num_slots, _stream(stream)),
+          "ifattn_kv_cache_write")
+
+
+def kv_cache_write_c8(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping, stream=None):
+    """Quantizing write: bf16 [rows, kv_heads, head_dim] -> int8 caches
+    [blocks, block_size, kv_heads, head_dim] and fp32 scales [blocks, block_size, kv_heads]."""
+    _dev(k, v, k_cache, v_cache, k_scale, v_scale, slot_mapping)
+    _req(k.dtype == torch.bfloat16 and k.dim() == 3, "k rows: bf16 [rows, kv_heads, head_dim]")
+    rows, kvh, hd = k.shape
+    _req(k_cache.dtype == torch.int8 and k_cache.dim() == 4 and tuple(k_cache.shape[2:]) == (kvh, hd),
+         "k cache: int8 [blocks, block_size, kv_heads, head_dim]")
+    _req(k_scale.dtype == torch.float32 and tuple(k_scale.shape) == tuple(k_cache.shape[:3]),
+         "k scale: fp32 [blocks, block_size, kv_heads]")
+    if v is not None:
+        _req(v.shape == k.shape and v_cache.shape == k_cache.shape and v_scale.shape == k_scale.shape,
+             "K/V shapes differ")
+    _req(slot_mapping.numel() == rows, "one slot per row")
+    num_slots = k_cache.shape[0] * k_cache.shape[1]
+    check(lib().ifattn_kv_cache_write_c8(_ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+                                         _ptr(k_scale), _ptr(v_scale), _ptr(slot_mapping),
+                                         _slot_dtype(slot_mapping), rows, kvh, hd, num_slots,
+                                         _stream(stream)),
+          "ifattn_kv_cache_write_c8")
+
+
+def mla_cache_write_c8(rows, cache, slot_mapping, stream=None):
+    """bf16 [rows, 576] -> packed 656-byte rows of a uint8 [blocks, block_size, 656] cache."""
+    _dev(rows, cache, slot_mapping)
+    _req(rows.dtype == torch.bfloat16 and rows.dim() == 2 and rows.shape[1] == 576,
+         "rows: bf16 [rows, 576]")
+    _req(cache.dtype == torch.uint8 and cache.dim() == 3 and cache.shape[2] == 656,
+         "cache: uint8 [blocks, block_size, 656]")
+    _req(slot_mapping.numel() == rows.shape[0], "one slot per row")
+    check(lib().ifattn_mla_cache_write_c8(_ptr(rows), _ptr(cache), _ptr(slot_mapping),
+                                          _slot_dtype(slot_mapping), rows.shape[0],
+                                          cache.shape[0] * cache.shape[1], _stream(stream)),
+          "ifattn_mla_cache_write_c8")
+
+
+# ---------------------------------------------------------------- decode
+
+def decode_workspace(num_seqs, q_heads, head_dim, max_context, device="cuda"):
+    n = lib().ifattn_paged_decode_workspace_size(num_seqs, q_heads, head_dim, max_context)
+    return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
+
+
+def _check_tables(block_tables, seq_lens, num_seqs, block_size, max_context):
+    _req(block_tables.dtype == torch.int32 and block_tables.dim() == 2
+         and block_tables.shape[0] >= num_seqs, "block_tables: int32 [num_seqs, entries]")
+    _req(block_tables.shape[1] * block_size >= max_context,
+         "block_tables do not cover max_context")
+    _req(seq_lens.dtype == torch.int32 and seq_lens.numel() >= num_seqs, "seq_lens: int32 [num_seqs]")
+
+
+def paged_decode(q, k_cache, v_cache, block_tables, seq_lens, max_context, scale=None,
+                 out=None, workspace=None, k_scale=None, v_scale=None, stream=None):
+    """Ragged paged GQA decode. q [num_seqs, q_heads, head_dim] bf16.
+
+    bf16 caches, or int8 caches with fp32 k_scale/v_scale. Returns out
+    [num_seqs, q_heads, head_dim] bf16.
+    """
+    c8 = k_cache.dtype == torch.int8
+    _dev(q, k_cache, v_cache, block_tables, seq_lens, out, workspace, k_scale, v_scale)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3, "q: bf16 [num_seqs, q_heads, head_dim]")
+    ns, hq, hd = q.shape
+    _req(k_cache.dim() == 4 and k_cache.shape == v_cache.shape and k_cache.shape[3] == hd,
+         "caches: [num_blocks, block_size, kv_heads, head_dim]")
+    nb, bs, hkv, _ = k_cache.shape
+    _req(k_cache.dtype == (torch.int8 if c8 else torch.bfloat16) and v_cache.dtype == k_cache.dtype,
+         "cache dtype must be bf16 or int8 (both caches)")
+    if c8:
+        _req(k_scale is not None and v_scale is not None and k_scale.dtype == torch.float32
+             and tuple(k_scale.shape) == (nb, bs, hkv) and v_scale.shape == k_scale.shape,
+             "int8 caches need fp32 scales [num_blocks, block_size, kv_heads]")
+    _check_tables(block_tables, seq_lens, ns, bs, max_context)
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty_like(q)
+    _req(out.shape == q.shape and out.dtype == torch.bfloat16, "out: bf16 like q")
+    if workspace is None:
+        workspace = decode_workspace(ns, hq, hd, max_context, q.device)
+    stride = block_tables.shape[1]
+    if c8:
+        st = lib().ifattn_paged_decode_c8(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_scale), _ptr(v_scale),
+            _ptr(block_tables), stride, _ptr(seq_lens), _ptr(out), ns, hq, hkv, hd, bs, nb,
+            max_context, float(scale), _ptr(workspace), workspace.numel(), _stream(stream))
+        check(st, "ifattn_paged_decode_c8")
+    else:
+        st = lib().ifattn_paged_decode_bf16(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), stride, _ptr(seq_lens),
+            _ptr(out), ns, hq, hkv, hd, bs, nb, max_context, float(scale), _ptr(workspace),
+            workspace.numel(), _stream(stream))
+        check(st, "ifattn_paged_decode_bf16")
+    return out
+
+
+# ---------------------------------------------------------------- varlen prefill
+
+def prefill_workspace(num_seqs, total_q, q_heads, head_dim, max_kv_len, device="cuda"):
+    n = lib().ifattn_varlen_prefill_workspace_size(num_seqs, total_q, q_heads, head_dim, max_kv_len)
+    return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
+
+
+def varlen_prefill(q, k_cache, v_cache, block_tables, cu_seqlens_q, kv_lens, max_q_len,
+                   max_kv_len, scale=None, out=None, workspace=None, stream=None):
+    """Packed chunked prefill (+ decode rows). q [total_q, q_heads, head_dim] bf16."""
+    _dev(q, k_cache, v_cache, block_tables, cu_seqlens_q, kv_lens, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3, "q: bf16 [total_q, q_heads, head_dim]")
+    tq, hq, hd = q.shape
+    _req(k_cache.dtype == torch.bfloat16 and k_cache.dim() == 4 and k_cache.shape == v_cache.shape
+         and k_cache.shape[3] == hd, "caches: bf16 [num_blocks, block_size, kv_heads, head_dim]")
+    nb, bs, hkv, _ = k_cache.shape
+    _req(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.dim() == 1, "cu_seqlens_q: int32")
+    ns = cu_seqlens_q.numel() - 1
+    _check_tables(block_tables, kv_lens, ns, bs, max_kv_len)
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = prefill_workspace(ns, tq, hq, hd, max_kv_len, q.device)
+    st = lib().ifattn_varlen_prefill_bf16(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), block_tables.shape[1],
+        _ptr(cu_seqlens_q), _ptr(kv_lens), _ptr(out), ns, tq, max_q_len, max_kv_len, hq, hkv, hd,
+        bs, nb, float(scale), _ptr(workspace), workspace.numel(), _stream(stream))
+    check(st, "ifattn_varlen_prefill_bf16")
+    return out
+
+
+# ---------------------------------------------------------------- MLA decode
+
+def mla_workspace(num_seqs, heads, max_context, device="cuda"):
+    n = lib().ifattn_mla_decode_workspace_size(num_seqs, heads, max_context)
+    return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
+
+
+def mla_decode(q, cache, block_tables, seq_lens, max_context, scale=None, out=None,
+               workspace=None, stream=None):
+    """q [num_seqs, heads, 576] bf16; cache bf16 [blocks, bs, 576] or uint8 [blocks, bs, 656]."""
+    c8 = cache.dtype == torch.uint8
+    _dev(q, cache, block_tables, seq_lens, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == 576,
+         "q: bf16 [num_seqs, heads, 576]")
+    ns, h, _ = q.shape
+    _req(cache.dim() == 3 and cache.shape[2] == (656 if c8 else 576)
+         and cache.dtype in (torch.uint8, torch.bfloat16), "cache: bf16 [.., 576] or uint8 [.., 656]")
+    nb, bs, _ = cache.shape
+    _check_tables(block_tables, seq_lens, ns, bs, max_context)
+    if scale is None:
+        scale = 1.0 / math.sqrt(192.0)
+    if out is None:
+        out = torch.empty((ns, h, 512), dtype=torch.bfloat16, device=q.device)
+    _req(tuple(out.shape) == (ns, h, 512) and out.dtype == torch.bfloat16, "out: bf16 [n, heads, 512]")
+    if workspace is None:
+        workspace = mla_workspace(ns, h, max_context, q.device)
+    fn = lib().ifattn_mla_decode_c8 if c8 else lib().ifattn_mla_decode_bf16
+    st = fn(_ptr(q), _ptr(cache), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
+            _ptr(out), ns, h, bs, nb, max_context, float(scale), _ptr(workspace),
+            workspace.numel(), _stream(stream))
+    check(st, "ifattn_mla_decode")
+    return out
+
+
+# ---------------------------------------------------------------- legacy launchers
+
+def cache_quantize(row, packed, scales, position, bits=8, stream=None):
+    """if_cache_quantize: row bf16 [width]; packed uint8 [capacity * width*bits/8];
+    scales fp32 [capacity]; position int64 [1] on the device."""
+    _dev(row, packed, scales, position)
+    width = row.numel()
+    capacity = scales.numel()
+    _req(packed.numel() >= capacity * width * bits // 8, "packed storage too small")
+    lib().if_cache_quantize(_ptr(row), _ptr(packed), _ptr(scales), _ptr(position), width,
+                            capacity, bits, _stream(stream))
+
+
+def cache_dequantize(packed, scales, output, position, width, bits=8, stream=None):
+    _dev(packed, scales, output, position)
+    capacity = scales.numel()
+    _req(output.numel() >= capacity * width, "output too small")
+    lib().if_cache_dequantize(_ptr(packed), _ptr(scales), _ptr(output), _ptr(position), width,
+                              capacity, bits, _stream(stream))
+
+
+def packed_attention_metadata(positions, indices, lengths, capacity, stream=None):
+    _dev(positions, indices, lengths)
+    rows = positions.numel()
+    _req(indices.numel() >= rows * capacity and lengths.numel() >= rows, "outputs too small")
+    lib().if_packed_attention_metadata_batch(_ptr(positions), _ptr(indices), _ptr(lengths),
+                                             capacity, rows, _stream(stream))

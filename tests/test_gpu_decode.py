@@ -1,0 +1,98 @@
+"""GPU parity: slot-mapped KV write (bit-exact) and ragged paged GQA decode
+(bf16 output within 1e-2 abs/rel of the fp32 oracle) through the C ABI."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_close, bf16_host, bits_host, to_dev
+from ironpangu_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(case, max_context=None):
+    """Upload the pools, run write + decode on the GPU and on the oracle."""
+    import torch
+    from ironpangu_amd import ops
+    h = case.host
+    nb, bs, hkv, hd = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim
+    kc = to_dev(h["k_pool"]).view(nb, bs, hkv, hd)
+    vc = to_dev(h["v_pool"]).view(nb, bs, hkv, hd)
+    slots = to_dev(case.slot_mapping.astype(np.int64))
+    ops.kv_cache_write(to_dev(h["k_new"]), to_dev(h["v_new"]), kc, vc, slots)
+    out = ops.paged_decode(to_dev(h["q"]), kc, vc, to_dev(case.block_tables),
+                           to_dev(case.seq_lens), max_context or case.max_context, case.scale)
+    torch.cuda.synchronize()
+    k_ref, v_ref = h["k_pool"].copy(), h["v_pool"].copy()
+    oracle.kv_write(h["k_new"], k_ref, case.slot_mapping)
+    oracle.kv_write(h["v_new"], v_ref, case.slot_mapping)
+    exp = oracle.paged_decode(h["q"], k_ref, v_ref, case.block_tables, case.seq_lens,
+                              case.q_heads, hkv, hd, bs, case.scale)
+    return kc, vc, k_ref, v_ref, out, exp
+
+
+def test_config1_write_and_decode():
+    case = W.config_case("cpu_ref", seed=1)
+    kc, vc, k_ref, v_ref, out, exp = _step(case)
+    assert np.array_equal(bits_host(kc).reshape(k_ref.shape), k_ref), "K cache not bit-exact"
+    assert np.array_equal(bits_host(vc).reshape(v_ref.shape), v_ref), "V cache not bit-exact"
+    assert_close(bf16_host(out), exp)
+
+
+@pytest.mark.parametrize("hq,hkv,hd,bs", [(16, 2, 128, 128), (16, 2, 128, 32), (8, 2, 256, 64),
+                                          (8, 8, 64, 32), (32, 2, 128, 64)])
+def test_decode_shapes(hq, hkv, hd, bs):
+    case = W.decode_host_case(7, num_seqs=6, lo=1, hi=1100, dist="uniform", q_heads=hq,
+                              kv_heads=hkv, head_dim=hd, block_size=bs,
+                              pool_blocks=6 * ((1100 + bs - 1) // bs) + 3)
+    case.seq_lens[:4] = [1, 256, 257, 1100][:4]
+    # keep the slot mapping consistent with the edited lengths
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(6), bs)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
+def test_decode_partition_edges_and_long():
+    # lengths around the 256-token split-K partition and 32-token tile edges
+    lens = [31, 32, 33, 255, 256, 257, 511, 512, 513, 4095, 8193]
+    case = W.decode_host_case(3, num_seqs=len(lens), lo=1, hi=8193, dist="uniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=128, pool_blocks=720)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(5), case.seq_lens, 128, 720,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(len(lens)), 128)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
+def test_decode_zero_length_gives_zero():
+    import torch
+    from ironpangu_amd import ops
+    case = W.decode_host_case(11, num_seqs=3, lo=5, hi=40, dist="uniform", q_heads=16, kv_heads=2,
+                              head_dim=128, block_size=32, pool_blocks=8)
+    lens = case.seq_lens.copy()
+    lens[1] = 0
+    h = case.host
+    kc = to_dev(h["k_pool"]).view(8, 32, 2, 128)
+    vc = to_dev(h["v_pool"]).view(8, 32, 2, 128)
+    out = ops.paged_decode(to_dev(h["q"]), kc, vc, to_dev(case.block_tables), to_dev(lens), 40)
+    torch.cuda.synchronize()
+    o = bf16_host(out)
+    assert np.all(o[1] == 0)
+    exp = oracle.paged_decode(h["q"], h["k_pool"], h["v_pool"], case.block_tables, lens, 16, 2,
+                              128, 32, case.scale)
+    assert_close(o, exp)
+
+
+def test_decode_rejects_bad_contracts():
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd._native import IfattnError
+    q = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros(4, 16, 2, 128, dtype=torch.bfloat16, device="cuda")  # block 16 unsupported
+    bt = torch.zeros(2, 8, dtype=torch.int32, device="cuda")
+    sl = torch.ones(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(IfattnError):
+        ops.paged_decode(q, kc, kc, bt, sl, 64)
