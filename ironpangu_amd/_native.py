@@ -12,8 +12,11 @@ from __future__ import annotations
 import ctypes as C
 from pathlib import Path
 
+import os
+
 PKG = Path(__file__).resolve().parent
-LIB_PATH = PKG / "libifattn_hip.so"
+# IFATTN_LIBRARY may point at another build of the same C ABI (e.g. a tuning build).
+LIB_PATH = Path(os.environ.get("IFATTN_LIBRARY", str(PKG / "libifattn_hip.so")))
 
 _lib = None
 

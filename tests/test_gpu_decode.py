@@ -96,3 +96,39 @@ def test_decode_rejects_bad_contracts():
     sl = torch.ones(2, dtype=torch.int32, device="cuda")
     with pytest.raises(IfattnError):
         ops.paged_decode(q, kc, kc, bt, sl, 64)
+
+
+def test_graph_replay_matches_eager():
+    """Write + decode captured once into a HIP graph: every replay (with eager
+    work and synchronisation in between) reproduces the eager result bit for bit."""
+    import torch
+    from ironpangu_amd import ops
+    case = W.config_case("cpu_ref", seed=4)
+    h = case.host
+    nb, bs, hkv, hd = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim
+    kc = to_dev(h["k_pool"]).view(nb, bs, hkv, hd)
+    vc = to_dev(h["v_pool"]).view(nb, bs, hkv, hd)
+    k_new, v_new, q = to_dev(h["k_new"]), to_dev(h["v_new"]), to_dev(h["q"])
+    slots = to_dev(case.slot_mapping.astype(np.int64))
+    tables, lens = to_dev(case.block_tables), to_dev(case.seq_lens)
+    ws = ops.decode_workspace(case.num_seqs, case.q_heads, hd, case.max_context)
+    out = torch.empty_like(q)
+
+    def step():
+        ops.kv_cache_write(k_new, v_new, kc, vc, slots)
+        ops.paged_decode(q, kc, vc, tables, lens, case.max_context, case.scale, out=out,
+                         workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for i in range(3):
+        out.fill_(0)
+        ws.fill_(255)  # scheduling words must be rebuilt by the replay itself
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from eager"
