@@ -1,0 +1,226 @@
+// Split-K scheduling shared by the paged decode kernels (GQA and MLA):
+// per-call device work list in longest-processing-time order, a work queue
+// drained by persistent workgroups, (m, l, O) partials per (sequence,
+// partition, head) and the merge kernel that combines them.
+#pragma once
+#include <cstdlib>
+
+#include "common.h"
+
+namespace ifattn {
+
+struct DecodeParams {
+  const uint16_t *q;
+  const uint8_t *k_cache;
+  const uint8_t *v_cache;
+  const float *k_scale;
+  const float *v_scale;
+  const int32_t *block_tables;
+  const int32_t *seq_lens;
+  uint16_t *out;
+  int32_t *queue;    // [0] next item (atomic), [1] item count; set by the plan kernel
+  uint32_t *items;   // (seq << 12 | part) per (sequence, partition), in sequence order
+  float *part_o;     // [num_seqs, max_parts, q_heads, D]
+  float *part_ml;    // [num_seqs, max_parts, q_heads, 2]
+  // Packed varlen batches: when set, sequence s reads/writes q/out row
+  // cu_seqlens[s+1]-1 and only sequences with exactly one query row are
+  // scheduled here (longer chunks go to the prefill kernel).
+  const int32_t *cu_seqlens;
+  int64_t num_blocks;
+  int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_context, max_parts,
+      part_tokens;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ int clamp_len(const DecodeParams &p, int seq) {
+  const int len = p.seq_lens[seq];
+  return len > p.max_context ? p.max_context : len;
+}
+__device__ __forceinline__ int parts_of(int len, int pt) { return len > 0 ? (len + pt - 1) / pt : 1; }
+// q / out row of a sequence (identity for plain decode batches).
+__device__ __forceinline__ int64_t q_row_of(const DecodeParams &p, int seq) {
+  return p.cu_seqlens ? int64_t(p.cu_seqlens[seq + 1]) - 1 : int64_t(seq);
+}
+__device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
+  return !p.cu_seqlens || p.cu_seqlens[seq + 1] - p.cu_seqlens[seq] == 1;
+}
+
+// Builds the compact work list on the device (graph-safe: lengths are read at
+// run time) and resets the work queue. Longest-processing-time order: every
+// full partition first, then the partial tail partitions by decreasing length
+// (a counting sort over 32-token buckets), so the last items pulled from the
+// queue are the shortest and the persistent workgroups finish together.
+// Sequences with no visible key get one zero-length item at the very end.
+// One workgroup of 1024 threads.
+template <int Unused = 0>
+__global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
+  constexpr int kBuckets = 257;  // 32-token buckets of PT <= 8192, plus empty rows
+  __shared__ int scan[1024];
+  __shared__ int bucket[kBuckets];
+  __shared__ int carry;
+  const int tid = threadIdx.x;
+  const int PT = p.part_tokens;
+  const int nb = PT / 32;  // bucket b holds remainders in (PT - 32(b+1), PT - 32b]
+  for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  // Pass 1: full partitions in sequence order; histogram of partial ones.
+  for (int base = 0; base < p.num_seqs; base += 1024) {
+    const int seq = base + tid;
+    int nfull = 0, bk = -1;
+    if (seq < p.num_seqs && decode_seq(p, seq)) {
+      const int len = clamp_len(p, seq);
+      nfull = len > 0 ? len / PT : 0;
+      const int rem = len > 0 ? len - nfull * PT : 0;
+      bk = len <= 0 ? nb : (rem > 0 ? (PT - rem) / 32 : -1);
+      if (bk >= 0) atomicAdd(&bucket[bk], 1);
+    }
+    scan[tid] = nfull;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int v = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += v;
+      __syncthreads();
+    }
+    const int start = carry + scan[tid] - nfull;
+    for (int k = 0; k < nfull; ++k) p.items[start + k] = (uint32_t(seq) << 12) | uint32_t(k);
+    __syncthreads();
+    if (tid == 1023) carry += scan[1023];
+    __syncthreads();
+  }
+  // Exclusive scan of the bucket counts, offset by the full-item count.
+  if (tid == 0) {
+    int run = carry;
+    for (int b = 0; b <= nb; ++b) {
+      const int c = bucket[b];
+      bucket[b] = run;
+      run += c;
+    }
+    p.queue[0] = 0;
+    p.queue[1] = run;
+  }
+  __syncthreads();
+  // Pass 2: place each partial / empty item in its bucket.
+  for (int base = 0; base < p.num_seqs; base += 1024) {
+    const int seq = base + tid;
+    if (seq < p.num_seqs && decode_seq(p, seq)) {
+      const int len = clamp_len(p, seq);
+      const int nfull = len > 0 ? len / PT : 0;
+      const int rem = len > 0 ? len - nfull * PT : 0;
+      const int bk = len <= 0 ? nb : (rem > 0 ? (PT - rem) / 32 : -1);
+      if (bk >= 0) p.items[atomicAdd(&bucket[bk], 1)] = (uint32_t(seq) << 12) | uint32_t(nfull);
+    }
+  }
+}
+
+// Merge split-K partials: one wave per (sequence, q head); lane l owns dims
+// [l*D/64, (l+1)*D/64).
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(DecodeParams p) {
+  const int seq = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  if (!decode_seq(p, seq)) return;
+  const int nparts = parts_of(clamp_len(p, seq), p.part_tokens);
+  if (nparts <= 1) return;
+  constexpr int V = D / 64;
+  const int64_t row0 = int64_t(seq) * p.max_parts * p.q_heads + h;
+  const int64_t pstride = p.q_heads;
+  float mmax = -INFINITY;
+  for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, p.part_ml[(row0 + k * pstride) * 2]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+  float lsum = 0.0f;
+  for (int k = lane; k < nparts; k += 64) {
+    const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + k * pstride) * 2);
+    lsum += fast_exp2(ml.x - mmax) * ml.y;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll 4
+  for (int k = 0; k < nparts; ++k) {
+    const int64_t row = row0 + k * pstride;
+    const float w = fast_exp2(p.part_ml[row * 2] - mmax);
+    const float *src = p.part_o + row * D + lane * V;
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] += w * src[i];
+  }
+  const float inv = 1.0f / lsum;
+  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + lane * V;
+  if constexpr (V == 1) {
+    op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; i += 2)
+      *reinterpret_cast<uint32_t *>(op + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
+  }
+}
+
+constexpr uint64_t kQueueBytes = 64;
+
+// Tokens per split-K partition (a multiple of the 32-token tile). The
+// IFATTN_DECODE_PART_TOKENS environment variable overrides it for tuning.
+inline int part_tokens() {
+  static int v = [] {
+    const char *e = getenv("IFATTN_DECODE_PART_TOKENS");
+    int x = e ? atoi(e) : 0;
+    return (x >= 32 && x <= 8192 && x % 32 == 0) ? x : 2048;
+  }();
+  return v;
+}
+
+inline int max_parts_for(int max_context) { return (max_context + part_tokens() - 1) / part_tokens(); }
+
+inline uint64_t align16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Persistent workgroups per CU. Fewer concurrent row streams keep HBM pages
+// open longer; IFATTN_DECODE_WGS_PER_CU overrides the default for tuning.
+inline int wgs_per_cu() {
+  static int v = [] {
+    const char *e = getenv("IFATTN_DECODE_WGS_PER_CU");
+    int x = e ? atoi(e) : 0;
+    return (x >= 1 && x <= 16) ? x : 2;
+  }();
+  return v;
+}
+
+
+// Workspace layout: queue words | items | partial O | partial (m, l).
+inline uint64_t split_k_workspace_bytes(int num_seqs, int heads, int dims, int max_context) {
+  const uint64_t items = uint64_t(num_seqs) * uint64_t(max_parts_for(max_context));
+  const uint64_t partials = items > uint64_t(num_seqs)  // single-partition calls keep no partials
+                                ? items * heads * (uint64_t(dims) + 2) * sizeof(float)
+                                : 0;
+  return kQueueBytes + align16(items * 4) + partials;
+}
+inline void split_k_bind_workspace(DecodeParams &p, void *workspace, int heads, int dims) {
+  uint8_t *w = static_cast<uint8_t *>(workspace);
+  const uint64_t items = uint64_t(p.num_seqs) * p.max_parts;
+  p.queue = reinterpret_cast<int32_t *>(w);
+  p.items = reinterpret_cast<uint32_t *>(w + kQueueBytes);
+  p.part_o = reinterpret_cast<float *>(w + kQueueBytes + align16(items * 4));
+  p.part_ml = p.part_o + items * heads * dims;
+}
+
+// Launches plan + decode + merge for the single-row sequences of a packed
+// varlen batch (defined with the GQA decode kernels).
+void launch_varlen_decode_rows(const DecodeParams &p, int head_dim, hipStream_t s);
+
+}  // namespace ifattn

@@ -1,0 +1,434 @@
+// Packed varlen chunked-prefill attention over paged bf16 caches (gfx950).
+//
+// Sequence s owns query rows [cu[s], cu[s+1]) (count rows) and kv_len cached
+// keys, this chunk's rows already written (writes precede queries,
+// native/include/sliding_window_layout.h:7). Row t of the chunk sees keys
+// [0, kv_len - count + t] — the causal rule of
+// native/src/openpangu_attention_metadata.h:20-22 — with GQA grouping
+// kh = h / (q_heads/kv_heads). fp32 accumulation, bf16 in/out. This replaces the
+// TND attention call of native/src/token_executor.h:863-906 (without window
+// or sinks).
+//
+// Work split:
+//  * single-row sequences (decode rows of a mixed batch) go to the split-K
+//    paged decode kernels through a q-row indirection;
+//  * longer chunks are cut into query tiles of 256/G rows (G = q heads per kv
+//    head); a workgroup (4 waves) owns one (sequence, query tile, kv head).
+//    The MFMA N dimension packs (query row, grouped head) columns, so all G
+//    heads of a kv head reuse every K/V tile. Each wave owns 4 column blocks
+//    of 16 (2 for head_dim 256).
+//  * K/V 32-token tiles stream through double-buffered LDS (rows padded by
+//    16 B so the 16-byte MFMA operand reads are bank-conflict free), fetched
+//    with buffer loads one tile ahead. QK^T runs transposed (tokens in M,
+//    columns in N) so the score tile is already the B operand of the PV MFMA;
+//    V^T operands come from 16-byte LDS reads split with v_perm.
+//  * tiles wholly above the diagonal are never visited; only tiles crossing a
+//    column's limit apply the causal mask.
+//  * query tiles are scheduled longest-first by a device plan kernel.
+#include <cstdlib>
+
+#include "common.h"
+#include "ifattn_internal.h"
+#include "split_k.h"
+
+namespace ifattn {
+
+struct PrefillParams {
+  const uint16_t *q;
+  const uint8_t *k_cache;
+  const uint8_t *v_cache;
+  const int32_t *block_tables;
+  const int32_t *cu;
+  const int32_t *kv_lens;
+  uint16_t *out;
+  uint32_t *items;   // (seq << 12 | query tile), longest first
+  int32_t *n_items;
+  int64_t num_blocks;
+  int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_kv, q_tile;
+  float scale_log2;
+};
+
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillTile = 32;
+constexpr int prefill_nb(int d) { return d > 128 ? 2 : 4; }        // column blocks per wave
+constexpr int prefill_q_tile(int d, int g) { return kPrefillWaves * prefill_nb(d) * 16 / g; }
+
+// Work list for the multi-row sequences, sorted by the number of key tokens
+// the query tile visits (descending, 256-token buckets).
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
+  constexpr int kBuckets = 1025;
+  __shared__ int bucket[kBuckets];
+  const int tid = threadIdx.x;
+  const int QT = p.q_tile;
+  const int nbk = (p.max_kv + 255) / 256 + 1;  // <= kBuckets (host-checked)
+  for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
+  __syncthreads();
+  auto cost_bucket = [&](int seq, int qt, int count) {
+    int kv = p.kv_lens[seq];
+    kv = kv > p.max_kv ? p.max_kv : kv;
+    const int rows_end = (qt + 1) * QT < count ? (qt + 1) * QT : count;
+    int reach = kv - count + rows_end;
+    reach = reach < 0 ? 0 : (reach > p.max_kv ? p.max_kv : reach);
+    return nbk - 1 - reach / 256;  // most work first
+  };
+  for (int seq = tid; seq < p.num_seqs; seq += 1024) {
+    const int count = p.cu[seq + 1] - p.cu[seq];
+    if (count <= 1) continue;
+    for (int qt = 0; qt * QT < count; ++qt) atomicAdd(&bucket[cost_bucket(seq, qt, count)], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int b = 0; b < nbk; ++b) {
+      const int c = bucket[b];
+      bucket[b] = run;
+      run += c;
+    }
+    *p.n_items = run;
+  }
+  __syncthreads();
+  for (int seq = tid; seq < p.num_seqs; seq += 1024) {
+    const int count = p.cu[seq + 1] - p.cu[seq];
+    if (count <= 1) continue;
+    for (int qt = 0; qt * QT < count; ++qt)
+      p.items[atomicAdd(&bucket[cost_bucket(seq, qt, count)], 1)] =
+          (uint32_t(seq) << 12) | uint32_t(qt);
+  }
+}
+
+__device__ __forceinline__ int pf_tile_token(int g, int j) {
+  return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+}
+
+template <int D>
+struct PrefillLds {
+  static constexpr int ROW = D + 8;  // bf16 elements per padded row
+  uint16_t k[2][kPrefillTile][ROW];
+  uint16_t v[2][kPrefillTile][ROW];
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p) {
+  constexpr int NB = prefill_nb(D);
+  constexpr int QT = prefill_q_tile(D, G);
+  constexpr int VPL = D / 16;                        // V dims per lane
+  constexpr int CHUNKS = kPrefillTile * D / 8;       // 16-byte pieces per K (or V) tile
+  constexpr int CPT = CHUNKS / (64 * kPrefillWaves);  // pieces per thread
+  __shared__ __align__(16) PrefillLds<D> lds;
+
+  if (int(blockIdx.x) >= *p.n_items) return;
+  const uint32_t e = p.items[blockIdx.x];
+  const int seq = int(e >> 12), qt = int(e & 0xfffu);
+  const int kvh = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = uniform(int(tid >> 6));
+  const int c = lane & 15, g = lane >> 4;
+  const int q0 = p.cu[seq];
+  const int count = p.cu[seq + 1] - q0;
+  int kv_len = p.kv_lens[seq];
+  kv_len = kv_len > p.max_kv ? p.max_kv : kv_len;
+  const int row0 = qt * QT;
+  const int rows_here = count - row0 < QT ? count - row0 : QT;
+  const int base_lim = kv_len - count;  // row t sees keys [0, base_lim + t]
+  int range_end = base_lim + row0 + rows_here;
+  range_end = range_end < 0 ? 0 : range_end;
+
+  // Columns of this lane: block nb -> (row, head).
+  int lim[NB];
+  int64_t qrow[NB];
+  int head[NB];
+  bool live[NB];
+  u32x4 qv[NB][D / 32];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int col = (w * NB + nb) * 16 + c;
+    const int r = col / G;
+    live[nb] = r < rows_here;
+    const int t = row0 + (live[nb] ? r : rows_here - 1);
+    lim[nb] = base_lim + t;
+    qrow[nb] = int64_t(q0) + t;
+    head[nb] = kvh * G + col % G;
+    const uint16_t *qp = p.q + (qrow[nb] * p.q_heads + head[nb]) * D + (D / 4) * g;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) qv[nb][s] = live[nb] ? load_u32x4(qp + 8 * s) : u32x4{0, 0, 0, 0};
+  }
+
+  const int32_t *table_row = p.block_tables + int64_t(seq) * p.table_stride;
+  const uint32_t row_bytes = uint32_t(p.kv_heads) * D * 2;
+  // Global -> register prefetch of one K/V tile (CPT 16-byte pieces each).
+  u32x4 pk[CPT], pv[CPT];
+  auto fetch = [&](int t0) {
+    int blk = uniform(table_row[t0 / p.block_size]);
+    blk = blk < 0 ? 0 : (blk >= p.num_blocks ? int(p.num_blocks - 1) : blk);
+    const int64_t tok0 = int64_t(blk) * p.block_size + (t0 & (p.block_size - 1));
+    const int n_live = range_end - t0 < kPrefillTile ? range_end - t0 : kPrefillTile;
+    const uint32_t extent = uint32_t(n_live - 1) * row_bytes + D * 2;
+    const int64_t first = (tok0 * p.kv_heads + kvh) * D * 2;
+    const auto rk = make_rsrc(p.k_cache + first, extent);
+    const auto rv = make_rsrc(p.v_cache + first, extent);
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = tid + k * 64 * kPrefillWaves;
+      const uint32_t off = uint32_t(i / (D / 8)) * row_bytes + uint32_t(i % (D / 8)) * 16;
+      pk[k] = buf_load_x4(rk, off);
+      pv[k] = buf_load_x4(rv, off);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int i = tid + k * 64 * kPrefillWaves;
+      *reinterpret_cast<u32x4 *>(&lds.k[buf][i / (D / 8)][(i % (D / 8)) * 8]) = pk[k];
+      *reinterpret_cast<u32x4 *>(&lds.v[buf][i / (D / 8)][(i % (D / 8)) * 8]) = pv[k];
+    }
+  };
+
+  f32x4 oacc[NB][VPL];
+  float m_run[NB], l_run[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    m_run[nb] = -INFINITY;
+    l_run[nb] = 0.0f;
+#pragma unroll
+    for (int b = 0; b < VPL; ++b) oacc[nb][b] = f32x4{0, 0, 0, 0};
+  }
+  const int lim_min = base_lim + row0;  // smallest limit among this tile's rows
+
+  auto compute = [&](int buf, int t0) {
+    u32x4 ka[2][D / 32];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s)
+        ka[mt][s] = *reinterpret_cast<const u32x4 *>(&lds.k[buf][16 * mt + c][(D / 4) * g + 8 * s]);
+    u32x4 pb[NB];
+    const bool masked = t0 + kPrefillTile - 1 > lim_min;  // tile crosses some column's limit
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < D / 32; ++s) {
+        s0 = mfma16x16x32(ka[0][s], qv[nb][s], s0);
+        s1 = mfma16x16x32(ka[1][s], qv[nb][s], s1);
+      }
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s0[r] * p.scale_log2;
+        x[4 + r] = s1[r] * p.scale_log2;
+      }
+      if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = t0 + pf_tile_token(g, j) <= lim[nb] ? x[j] : -INFINITY;
+      }
+      float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                         fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      tmax = wave_max_xor(tmax, 16);
+      tmax = wave_max_xor(tmax, 32);
+      if (__any(tmax > m_run[nb] + 8.0f)) {
+        const float m_new = fmaxf(m_run[nb], tmax);
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run[nb] - m_new);
+        m_run[nb] = m_new;
+        l_run[nb] *= alpha;
+#pragma unroll
+        for (int b = 0; b < VPL; ++b) oacc[nb][b] *= alpha;
+      }
+      const float m_use = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
+      float pr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(x[j] - m_use);
+      l_run[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+      pb[nb] = u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                     pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+    }
+    // V^T operands: lane c holds dims c*VPL .. +VPL of its eight tokens.
+    uint32_t vr[8][VPL / 2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint16_t *src = &lds.v[buf][pf_tile_token(g, j)][c * VPL];
+      if constexpr (VPL == 4) {
+        const u32x2 x = *reinterpret_cast<const u32x2 *>(src);
+        vr[j][0] = x[0];
+        vr[j][1] = x[1];
+      } else {
+#pragma unroll
+        for (int qd = 0; qd < VPL / 2; qd += 4) {
+          const u32x4 x = *reinterpret_cast<const u32x4 *>(src + 2 * qd);
+          vr[j][qd] = x[0];
+          vr[j][qd + 1] = x[1];
+          vr[j][qd + 2] = x[2];
+          vr[j][qd + 3] = x[3];
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < VPL; ++b) {
+      const int wd = b >> 1;
+      u32x4 a;
+      if (b & 1)
+        a = u32x4{pack_hi16(vr[0][wd], vr[1][wd]), pack_hi16(vr[2][wd], vr[3][wd]),
+                  pack_hi16(vr[4][wd], vr[5][wd]), pack_hi16(vr[6][wd], vr[7][wd])};
+      else
+        a = u32x4{pack_lo16(vr[0][wd], vr[1][wd]), pack_lo16(vr[2][wd], vr[3][wd]),
+                  pack_lo16(vr[4][wd], vr[5][wd]), pack_lo16(vr[6][wd], vr[7][wd])};
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) oacc[nb][b] = mfma16x16x32(a, pb[nb], oacc[nb][b]);
+    }
+  };
+
+  if (range_end > 0) {
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    int buf = 0;
+    for (int t0 = 0; t0 < range_end; t0 += kPrefillTile) {
+      const bool more = t0 + kPrefillTile < range_end;
+      if (more) fetch(t0 + kPrefillTile);
+      compute(buf, t0);
+      if (more) stash(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    float l_tot = wave_sum_xor(l_run[nb], 16);
+    l_tot = wave_sum_xor(l_tot, 32);
+    if (!live[nb]) continue;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t *op = p.out + (qrow[nb] * p.q_heads + head[nb]) * D + 4 * g * VPL;
+    // lane holds dims (4g + r)*VPL + b
+#pragma unroll
+    for (int k = 0; k < D / 32; ++k) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int idx = 8 * k + i;  // = r*VPL + b
+        v[i] = oacc[nb][idx % VPL][idx / VPL] * inv;
+      }
+      store_u32x4(op + 8 * k, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                    pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])});
+    }
+  }
+}
+
+namespace {
+
+template <int D>
+void launch_prefill(const PrefillParams &p, int grid, hipStream_t s) {
+  const dim3 g(grid, p.kv_heads);
+  switch (p.group) {
+    case 1: varlen_prefill_kernel<D, 1><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
+    case 2: varlen_prefill_kernel<D, 2><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
+    case 4: varlen_prefill_kernel<D, 4><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
+    case 8: varlen_prefill_kernel<D, 8><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
+    default: varlen_prefill_kernel<D, 16><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
+  }
+}
+
+uint64_t prefill_items_bound(int num_seqs, int total_q, int q_tile) {
+  return uint64_t(total_q) / q_tile + uint64_t(num_seqs) + 1;
+}
+
+}  // namespace
+}  // namespace ifattn
+
+using namespace ifattn;
+
+extern "C" uint64_t ifattn_varlen_prefill_workspace_size(int32_t num_seqs, int32_t total_q,
+                                                         int32_t q_heads, int32_t head_dim,
+                                                         int32_t max_kv_len) {
+  if (num_seqs <= 0 || total_q <= 0 || q_heads <= 0 || head_dim <= 0 || max_kv_len <= 0) return 0;
+  const uint64_t dec = split_k_workspace_bytes(num_seqs, q_heads, head_dim, max_kv_len);
+  return align16(dec) + 16 + 4 * prefill_items_bound(num_seqs, total_q, 1);
+}
+
+extern "C" int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache, const void *v_cache,
+                                              const int32_t *block_tables, int32_t table_stride,
+                                              const int32_t *cu_seqlens_q, const int32_t *kv_lens,
+                                              void *out, int32_t num_seqs, int32_t total_q,
+                                              int32_t max_q_len, int32_t max_kv_len,
+                                              int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                              int32_t block_size, int64_t num_blocks, float scale,
+                                              void *workspace, uint64_t workspace_bytes,
+                                              void *stream) {
+  if (!q || !k_cache || !v_cache || !block_tables || !cu_seqlens_q || !kv_lens || !out)
+    return fail(IFATTN_EINVAL, "varlen prefill: null pointer");
+  if (num_seqs <= 0 || total_q <= 0 || max_q_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+      q_heads % kv_heads)
+    return fail(IFATTN_EINVAL, "varlen prefill: bad sequence or head counts");
+  const int group = q_heads / kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8 && group != 16)
+    return fail(IFATTN_EINVAL, "varlen prefill: q_heads / kv_heads must be 1, 2, 4, 8 or 16");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(IFATTN_EINVAL, "varlen prefill: head_dim must be 64, 128 or 256");
+  if (block_size < 32 || (block_size & (block_size - 1)))
+    return fail(IFATTN_EINVAL, "varlen prefill: block_size must be a power of two >= 32");
+  if (max_kv_len <= 0 || max_kv_len > 262144 || num_blocks <= 0 || table_stride <= 0 ||
+      int64_t(table_stride) * block_size < max_kv_len)
+    return fail(IFATTN_EINVAL, "varlen prefill: max_kv_len in [1, 262144] covered by the tables");
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
+    return fail(IFATTN_EINVAL, "varlen prefill: q, out and caches must be 16-byte aligned");
+  const uint64_t need = ifattn_varlen_prefill_workspace_size(num_seqs, total_q, q_heads, head_dim,
+                                                             max_kv_len);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(IFATTN_EWORKSPACE, "varlen prefill: workspace missing, short or misaligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  // Decode rows: split-K decode kernels with the q-row indirection.
+  DecodeParams d{};
+  d.q = (const uint16_t *)q;
+  d.k_cache = (const uint8_t *)k_cache;
+  d.v_cache = (const uint8_t *)v_cache;
+  d.block_tables = block_tables;
+  d.seq_lens = kv_lens;
+  d.out = (uint16_t *)out;
+  d.cu_seqlens = cu_seqlens_q;
+  d.num_blocks = num_blocks;
+  d.num_seqs = num_seqs;
+  d.q_heads = q_heads;
+  d.kv_heads = kv_heads;
+  d.group = group;
+  d.table_stride = table_stride;
+  d.block_size = block_size;
+  d.max_context = max_kv_len;
+  d.part_tokens = part_tokens();
+  d.max_parts = max_parts_for(max_kv_len);
+  d.scale_log2 = scale * kLog2e;
+  if (d.part_tokens > 64 * block_size)
+    return fail(IFATTN_EINVAL, "varlen prefill: decode partition spans more than 64 blocks");
+  split_k_bind_workspace(d, workspace, q_heads, head_dim);
+
+  PrefillParams p{};
+  p.q = d.q;
+  p.k_cache = d.k_cache;
+  p.v_cache = d.v_cache;
+  p.block_tables = block_tables;
+  p.cu = cu_seqlens_q;
+  p.kv_lens = kv_lens;
+  p.out = d.out;
+  {
+    uint8_t *w = static_cast<uint8_t *>(workspace) +
+                 align16(split_k_workspace_bytes(num_seqs, q_heads, head_dim, max_kv_len));
+    p.n_items = reinterpret_cast<int32_t *>(w);
+    p.items = reinterpret_cast<uint32_t *>(w + 16);
+  }
+  p.num_blocks = num_blocks;
+  p.num_seqs = num_seqs;
+  p.q_heads = q_heads;
+  p.kv_heads = kv_heads;
+  p.group = group;
+  p.table_stride = table_stride;
+  p.block_size = block_size;
+  p.max_kv = max_kv_len;
+  p.q_tile = prefill_q_tile(head_dim, group);
+  p.scale_log2 = d.scale_log2;
+  const int grid = int(prefill_items_bound(num_seqs, total_q, p.q_tile));
+
+  launch_varlen_decode_rows(d, head_dim, s);
+  prefill_plan_kernel<<<1, 1024, 0, s>>>(p);
+  if (head_dim == 64) launch_prefill<64>(p, grid, s);
+  else if (head_dim == 128) launch_prefill<128>(p, grid, s);
+  else launch_prefill<256>(p, grid, s);
+  return launch_status("varlen prefill");
+}
