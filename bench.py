@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=64)
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip configs 3-5 (reported under 'secondary')")
     return ap.parse_args()
 
 
@@ -110,6 +112,218 @@ def cpu_baseline(seed, sample_seqs):
             "sample": f"oracle_paged_decode (fp32 C++ restatement) over the first {len(lens)} of "
                       f"the 256 config-2 sequences ({int(lens.sum())} context tokens), "
                       f"{reps} passes"}
+
+
+def timed(fn, steps, warmup, graph=True):
+    """Average ms of fn() over `steps` runs (HIP graph replay by default)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    run = fn
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        run = g.replay
+        for _ in range(2):
+            run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def fill_randn(t, gen, std=1.0, clip=None):
+    import torch
+    flat = t.view(-1)
+    step = 1 << 27
+    for i in range(0, flat.numel(), step):
+        n = min(step, flat.numel() - i)
+        x = torch.randn(n, generator=gen, device=t.device, dtype=torch.float32) * std
+        if clip is not None:
+            x.clamp_(-clip, clip)
+        flat[i:i + n] = x.to(t.dtype)
+
+
+def bench_c8(seed, steps, warmup):
+    """Config 4: C8 paged decode, 256 seqs, L ~ U[1024,16384]; the pool is
+    quantized by the C8 write from N(0,1) clipped to +-4."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    kw = dict(W.CONFIGS["c8"])
+    case = W.decode_meta(seed, c8=True, **kw)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 4)
+    nb, bs, hkv, hd = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim
+    kc = torch.empty((nb, bs, hkv, hd), dtype=torch.int8, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((nb, bs, hkv), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    rows = 1 << 18
+    src_k = torch.empty((rows, hkv, hd), dtype=torch.bfloat16, device=dev)
+    src_v = torch.empty_like(src_k)
+    for r0 in range(0, nb * bs, rows):
+        fill_randn(src_k, g, clip=4.0)
+        fill_randn(src_v, g, clip=4.0)
+        sl = torch.arange(r0, r0 + rows, dtype=torch.int64, device=dev)
+        ops.kv_cache_write_c8(src_k, src_v, kc, vc, ks, vs, sl)
+    del src_k, src_v
+    q = torch.randn((case.num_seqs, case.q_heads, hd), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((case.num_seqs, hkv, hd), generator=g, device=dev).clamp_(-4, 4).to(torch.bfloat16)
+    vn = torch.randn((case.num_seqs, hkv, hd), generator=g, device=dev).clamp_(-4, 4).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    slots = torch.from_numpy(case.slot_mapping.astype(np.int64)).to(dev)
+    ws = ops.decode_workspace(case.num_seqs, case.q_heads, hd, case.max_context)
+    out = torch.empty_like(q)
+
+    def attn():
+        ops.paged_decode(q, kc, vc, tables, lens, case.max_context, case.scale, out=out,
+                         workspace=ws, k_scale=ks, v_scale=vs)
+
+    def step():
+        ops.kv_cache_write_c8(kn, vn, kc, vc, ks, vs, slots)
+        attn()
+
+    ms_step = timed(step, steps, warmup)
+    ms_attn = timed(attn, steps, warmup, graph=False)
+    b = W.decode_bytes(case.seq_lens, case.q_heads, hkv, hd, bs, elem_bytes=1, scale_bytes=4)
+    res = {"workload": "C8 paged decode, 256 seqs, L~U[1024,16384] (BASELINE config 4)",
+           "value": round(b["total"] / ms_step / 1e6, 2), "unit": "GB/s",
+           "ms_per_step": round(ms_step, 5), "tokens_per_s": round(case.num_seqs / ms_step * 1e3, 1),
+           "total_context_tokens": int(case.seq_lens.sum()),
+           "roofline": {"bound": "hbm", "kernel": "paged_decode c8 operator",
+                        "achieved": round(b["attention"] / ms_attn / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(b["attention"] / ms_attn / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms_attn, 5), "algorithmic_bytes": b["attention"]}}
+    del kc, vc, ks, vs
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_mla(seed, steps, warmup):
+    """Config 5: packed-MLA latent decode, 128 seqs, L log-uniform [1024,65536],
+    16 heads, 576-wide bf16 rows, block 64, N(0,0.5)."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    case = W.mla_meta(seed)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 5)
+    cache = torch.empty((case.pool_blocks, case.block_size, 576), dtype=torch.bfloat16, device=dev)
+    fill_randn(cache, g, std=0.5)
+    q = (torch.randn((case.num_seqs, case.heads, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    rows = (torch.randn((case.num_seqs, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    slots = torch.from_numpy(case.slot_mapping.astype(np.int64)).to(dev)
+    ws = ops.mla_workspace(case.num_seqs, case.heads, case.max_context)
+    out = torch.empty((case.num_seqs, case.heads, 512), dtype=torch.bfloat16, device=dev)
+
+    def attn():
+        ops.mla_decode(q, cache, tables, lens, case.max_context, case.scale, out=out, workspace=ws)
+
+    def step():
+        ops.kv_cache_write(rows, None, cache, None, slots)
+        attn()
+
+    ms_step = timed(step, steps, warmup)
+    ms_attn = timed(attn, steps, warmup, graph=False)
+    L = case.seq_lens.astype(np.int64)
+    attn_b = int(L.sum()) * 1152 + case.num_seqs * case.heads * (576 + 512) * 2 + \
+        int(((L + 63) // 64).sum()) * 4 + case.num_seqs * 4
+    total_b = attn_b + case.num_seqs * (1152 * 2 + 8)
+    flops = int(L.sum()) * case.heads * (576 + 512) * 2
+    res = {"workload": "packed-MLA latent decode, 128 seqs, L log-uniform [1024,65536] (BASELINE config 5)",
+           "value": round(total_b / ms_step / 1e6, 2), "unit": "GB/s",
+           "ms_per_step": round(ms_step, 5), "tokens_per_s": round(case.num_seqs / ms_step * 1e3, 1),
+           "total_context_tokens": int(L.sum()), "tflops": round(flops / ms_attn / 1e9, 2),
+           "roofline": {"bound": "hbm", "kernel": "mla_decode bf16 operator",
+                        "achieved": round(attn_b / ms_attn / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(attn_b / ms_attn / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms_attn, 5), "algorithmic_bytes": attn_b}}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_mixed(seed, steps, warmup):
+    """Config 3: 8 prefill chunks (U[64,2048] rows after U[0,8192] cached) +
+    192 decode rows (U[256,16384]) in one packed varlen call."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    case = W.mixed_meta(seed)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 3)
+    nb, bs, hkv, hd, hq = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim, case.q_heads
+    kc = torch.empty((nb, bs, hkv, hd), dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    fill_randn(kc, g)
+    fill_randn(vc, g)
+    tq = int(case.cu_seqlens[-1])
+    q = torch.randn((tq, hq, hd), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((tq, hkv, hd), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((tq, hkv, hd), generator=g, device=dev).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    cu = torch.from_numpy(case.cu_seqlens).to(dev)
+    kv = torch.from_numpy(case.kv_lens).to(dev)
+    slots = torch.from_numpy(case.slot_mapping.astype(np.int64)).to(dev)
+    ws = ops.prefill_workspace(len(case.q_lens), tq, hq, hd, case.max_kv_len)
+    out = torch.empty_like(q)
+    nchunk = int((case.q_lens > 1).sum())
+    # prefill-only view: the chunk sequences alone
+    cu_p = cu[: nchunk + 1].contiguous()
+    tq_p = int(case.cu_seqlens[nchunk])
+    ws_p = ops.prefill_workspace(nchunk, tq_p, hq, hd, case.max_kv_len)
+
+    def attn():
+        ops.varlen_prefill(q, kc, vc, tables, cu, kv, case.max_q_len, case.max_kv_len, case.scale,
+                           out=out, workspace=ws)
+
+    def prefill_only():
+        ops.varlen_prefill(q[:tq_p], kc, vc, tables[:nchunk], cu_p, kv[:nchunk], case.max_q_len,
+                           case.max_kv_len, case.scale, out=out[:tq_p], workspace=ws_p)
+
+    def step():
+        ops.kv_cache_write(kn, vn, kc, vc, slots)
+        attn()
+
+    ms_step = timed(step, steps, warmup)
+    ms_pf = timed(prefill_only, steps, warmup, graph=False)
+    flops = 0
+    kv_bytes = 0
+    for s in range(len(case.q_lens)):
+        L, K = int(case.q_lens[s]), int(case.kv_lens[s])
+        vis = np.arange(K - L + 1, K + 1, dtype=np.int64)
+        if L > 1:
+            flops += int(vis.sum()) * hq * hd * 4
+        kv_bytes += K * hkv * hd * 2 * 2
+    ms_attn = timed(attn, steps, warmup, graph=False)
+    tf = flops / ms_pf / 1e9
+    res = {"workload": "mixed chunked prefill + decode packed batch (BASELINE config 3)",
+           "value": round(flops / ms_step / 1e9, 2), "unit": "TFLOP/s (prefill flops / step time)",
+           "ms_per_step": round(ms_step, 5), "ms_attention": round(ms_attn, 5),
+           "prefill_rows": tq_p, "decode_rows": int((case.q_lens == 1).sum()),
+           "prefill_flops": flops, "kv_bytes": kv_bytes,
+           "roofline": {"bound": "mfma", "kernel": "varlen_prefill (8 chunks, prefill kernel)",
+                        "achieved": round(tf, 2), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tf / BF16_MFMA_PEAK_TFLOPS, 4), "avg_ms": round(ms_pf, 5)}}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -202,6 +416,12 @@ def main():
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_sample_seqs)
+    if not args.no_secondary:
+        del t
+        torch.cuda.empty_cache()
+        res["secondary"] = {"c8_decode": bench_c8(args.seed, args.steps, args.warmup),
+                            "mla_decode": bench_mla(args.seed, args.steps, args.warmup),
+                            "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup)}
     print(json.dumps(res), flush=True)
 
 

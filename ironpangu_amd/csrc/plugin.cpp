@@ -1,0 +1,344 @@
+// IFKernelV1-layout operator plug-ins (abi_version 2) over the ifattn C ABI.
+// prepare: descriptor validation in the manner of the reference loader
+// (native/src/compiled_kernel.cpp:20-41,71-83) plus per-contract shape checks,
+// host state only. enqueue: one call into the launchers, no allocation, no
+// synchronization, no device reads on the host.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/ifattn.h"
+#include "../../include/inferfabric_kernel_v1.h"
+#include "ifattn_internal.h"
+
+namespace {
+
+enum Op : int {
+  kWriteBf16 = 0,
+  kWriteC8,
+  kDecodeBf16,
+  kDecodeC8,
+  kPrefillBf16,
+  kMlaBf16,
+  kMlaC8,
+  kMlaWriteC8,
+  kOpCount
+};
+
+const char *const kContract[kOpCount] = {
+    "inferfabric.kv_cache_write.bf16.v2",   "inferfabric.kv_cache_write.c8.v2",
+    "inferfabric.paged_decode.gqa.bf16.v2", "inferfabric.paged_decode.gqa.c8.v2",
+    "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
+    "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
+};
+constexpr const char *kTarget = "gfx950";
+
+struct State {
+  int op;
+  IFKernelTensorV1 inputs[8], outputs[4];
+  uint64_t workspace;
+  int32_t slot_dtype;
+  int64_t rows, row_bytes, num_slots, num_blocks;
+  int32_t n, q_heads, kv_heads, head_dim, block_size, stride, max_ctx, total_q;
+  float scale;
+};
+
+struct Reject {
+  const char *what;
+};
+void require(bool ok, const char *what) {
+  if (!ok) throw Reject{what};
+}
+
+uint64_t elem_bytes(uint32_t dtype) {
+  switch (dtype) {
+    case IF_KERNEL_DTYPE_I8: return 1;
+    case IF_KERNEL_DTYPE_BF16: return 2;
+    case IF_KERNEL_DTYPE_F32: return 4;
+    case IF_KERNEL_DTYPE_I32: return 4;
+    case IF_KERNEL_DTYPE_I64: return 8;
+    default: return 0;
+  }
+}
+
+void check_tensor(const IFKernelTensorV1 &t, uint32_t dtype, uint32_t access, uint32_t rank) {
+  require(t.struct_bytes == sizeof(IFKernelTensorV1), "tensor descriptor size");
+  require(t.data != nullptr, "tensor data pointer");
+  require(t.rank == rank, "tensor rank");
+  require(t.dtype == dtype, "tensor dtype");
+  require(t.access == access, "tensor access");
+  uint64_t stride = 1;
+  for (uint32_t i = t.rank; i-- > 0;) {
+    require(t.shape[i] > 0, "tensor extent must be positive");
+    require(t.strides[i] == int64_t(stride), "tensor must be contiguous");
+    require(uint64_t(t.shape[i]) <= UINT64_MAX / stride, "tensor shape overflow");
+    stride *= uint64_t(t.shape[i]);
+  }
+  const uint64_t eb = elem_bytes(dtype);
+  require(stride <= UINT64_MAX / eb && stride * eb <= t.allocation_bytes, "tensor allocation bound");
+}
+
+uint64_t nbytes(const IFKernelTensorV1 &t) {
+  uint64_t n = elem_bytes(t.dtype);
+  for (uint32_t i = 0; i < t.rank; ++i) n *= uint64_t(t.shape[i]);
+  return n;
+}
+
+bool overlap(const IFKernelTensorV1 &a, const IFKernelTensorV1 &b) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a.data), y = reinterpret_cast<uintptr_t>(b.data);
+  return x < y + nbytes(b) && y < x + nbytes(a);
+}
+
+void check_slots(const IFKernelTensorV1 &t, int64_t rows, State &s) {
+  require(t.struct_bytes == sizeof(IFKernelTensorV1) && t.data && t.rank == 1 &&
+              t.access == IF_KERNEL_ACCESS_READ &&
+              (t.dtype == IF_KERNEL_DTYPE_I64 || t.dtype == IF_KERNEL_DTYPE_I32),
+          "slot_mapping: I64 or I32 [rows], read");
+  check_tensor(t, t.dtype, IF_KERNEL_ACCESS_READ, 1);
+  require(t.shape[0] == rows, "slot_mapping length differs from rows");
+  s.slot_dtype = t.dtype == IF_KERNEL_DTYPE_I64 ? IFATTN_DTYPE_I64 : IFATTN_DTYPE_I32;
+}
+
+bool same_shape(const IFKernelTensorV1 &a, const IFKernelTensorV1 &b) {
+  if (a.rank != b.rank) return false;
+  for (uint32_t i = 0; i < a.rank; ++i)
+    if (a.shape[i] != b.shape[i]) return false;
+  return true;
+}
+
+void prepare_op(State &s, const IFKernelTensorV1 *in, uint32_t nin, const IFKernelTensorV1 *out,
+                uint32_t nout) {
+  constexpr uint32_t R = IF_KERNEL_ACCESS_READ, W = IF_KERNEL_ACCESS_WRITE,
+                     RW = IF_KERNEL_ACCESS_READ_WRITE;
+  constexpr uint32_t BF = IF_KERNEL_DTYPE_BF16, I8 = IF_KERNEL_DTYPE_I8, F32 = IF_KERNEL_DTYPE_F32,
+                     I32 = IF_KERNEL_DTYPE_I32;
+  switch (s.op) {
+    case kWriteBf16:
+    case kWriteC8: {
+      const bool c8 = s.op == kWriteC8;
+      require(nin == 3 && nout == (c8 ? 4u : 2u), "write: 3 inputs, 2 (bf16) or 4 (c8) outputs");
+      check_tensor(in[0], BF, R, 3);
+      check_tensor(in[1], BF, R, 3);
+      require(same_shape(in[0], in[1]), "k/v rows differ");
+      s.rows = in[0].shape[0];
+      check_slots(in[2], s.rows, s);
+      check_tensor(out[0], c8 ? I8 : BF, RW, 4);
+      check_tensor(out[1], c8 ? I8 : BF, RW, 4);
+      require(same_shape(out[0], out[1]), "k/v caches differ");
+      require(out[0].shape[2] == in[0].shape[1] && out[0].shape[3] == in[0].shape[2],
+              "cache row differs from input row");
+      s.kv_heads = int32_t(in[0].shape[1]);
+      s.head_dim = int32_t(in[0].shape[2]);
+      s.num_slots = out[0].shape[0] * out[0].shape[1];
+      s.row_bytes = int64_t(s.kv_heads) * s.head_dim * 2;
+      require(c8 || s.row_bytes % 16 == 0, "bf16 row must be a multiple of 16 bytes");
+      if (c8) {
+        check_tensor(out[2], F32, RW, 3);
+        check_tensor(out[3], F32, RW, 3);
+        require(out[2].shape[0] == out[0].shape[0] && out[2].shape[1] == out[0].shape[1] &&
+                    out[2].shape[2] == out[0].shape[2] && same_shape(out[2], out[3]),
+                "scales must be [blocks, block_size, kv_heads]");
+        require(s.head_dim % 8 == 0 && s.head_dim <= 512, "c8 head_dim: multiple of 8, <= 512");
+      }
+      return;
+    }
+    case kDecodeBf16:
+    case kDecodeC8: {
+      const bool c8 = s.op == kDecodeC8;
+      require(nin == (c8 ? 7u : 5u) && nout == 1, "decode: 5 (bf16) or 7 (c8) inputs, 1 output");
+      check_tensor(in[0], BF, R, 3);
+      check_tensor(in[1], c8 ? I8 : BF, R, 4);
+      check_tensor(in[2], c8 ? I8 : BF, R, 4);
+      require(same_shape(in[1], in[2]), "k/v caches differ");
+      const int t = c8 ? 5 : 3;
+      if (c8) {
+        check_tensor(in[3], F32, R, 3);
+        check_tensor(in[4], F32, R, 3);
+        require(same_shape(in[3], in[4]) && in[3].shape[0] == in[1].shape[0] &&
+                    in[3].shape[1] == in[1].shape[1] && in[3].shape[2] == in[1].shape[2],
+                "scales must be [blocks, block_size, kv_heads]");
+      }
+      check_tensor(in[t], I32, R, 2);
+      check_tensor(in[t + 1], I32, R, 1);
+      check_tensor(out[0], BF, W, 3);
+      s.n = int32_t(in[0].shape[0]);
+      s.q_heads = int32_t(in[0].shape[1]);
+      s.head_dim = int32_t(in[0].shape[2]);
+      s.num_blocks = in[1].shape[0];
+      s.block_size = int32_t(in[1].shape[1]);
+      s.kv_heads = int32_t(in[1].shape[2]);
+      require(in[1].shape[3] == s.head_dim, "cache head_dim differs from q");
+      require(in[t].shape[0] >= s.n && in[t + 1].shape[0] >= s.n, "tables/lengths shorter than q");
+      s.stride = int32_t(in[t].shape[1]);
+      require(int64_t(s.stride) * s.block_size <= (int64_t(1) << 20), "max_context above 1M");
+      s.max_ctx = s.stride * s.block_size;
+      require(same_shape(out[0], in[0]), "out must match q");
+      s.scale = 1.0f / std::sqrt(float(s.head_dim));
+      s.workspace = ifattn_paged_decode_workspace_size(s.n, s.q_heads, s.head_dim, s.max_ctx);
+      return;
+    }
+    case kPrefillBf16: {
+      require(nin == 6 && nout == 1, "prefill: 6 inputs, 1 output");
+      check_tensor(in[0], BF, R, 3);
+      check_tensor(in[1], BF, R, 4);
+      check_tensor(in[2], BF, R, 4);
+      require(same_shape(in[1], in[2]), "k/v caches differ");
+      check_tensor(in[3], I32, R, 2);
+      check_tensor(in[4], I32, R, 1);
+      check_tensor(in[5], I32, R, 1);
+      check_tensor(out[0], BF, W, 3);
+      s.total_q = int32_t(in[0].shape[0]);
+      s.q_heads = int32_t(in[0].shape[1]);
+      s.head_dim = int32_t(in[0].shape[2]);
+      s.num_blocks = in[1].shape[0];
+      s.block_size = int32_t(in[1].shape[1]);
+      s.kv_heads = int32_t(in[1].shape[2]);
+      require(in[1].shape[3] == s.head_dim, "cache head_dim differs from q");
+      s.n = int32_t(in[4].shape[0] - 1);
+      require(s.n >= 1 && in[5].shape[0] >= s.n && in[3].shape[0] >= s.n,
+              "cu_seqlens [n+1], kv_lens [n], tables [n, entries]");
+      s.stride = int32_t(in[3].shape[1]);
+      require(int64_t(s.stride) * s.block_size <= 262144, "max_kv_len above 262144");
+      s.max_ctx = s.stride * s.block_size;
+      require(same_shape(out[0], in[0]), "out must match q");
+      s.scale = 1.0f / std::sqrt(float(s.head_dim));
+      s.workspace = ifattn_varlen_prefill_workspace_size(s.n, s.total_q, s.q_heads, s.head_dim,
+                                                         s.max_ctx);
+      return;
+    }
+    case kMlaBf16:
+    case kMlaC8: {
+      const bool c8 = s.op == kMlaC8;
+      require(nin == 4 && nout == 1, "mla decode: 4 inputs, 1 output");
+      check_tensor(in[0], BF, R, 3);
+      require(in[0].shape[2] == 576, "q must be [n, heads, 576]");
+      check_tensor(in[1], c8 ? I8 : BF, R, 3);
+      require(in[1].shape[2] == (c8 ? 656 : 576), "cache row width 576 (bf16) or 656 (c8)");
+      check_tensor(in[2], I32, R, 2);
+      check_tensor(in[3], I32, R, 1);
+      check_tensor(out[0], BF, W, 3);
+      s.n = int32_t(in[0].shape[0]);
+      s.q_heads = int32_t(in[0].shape[1]);
+      s.num_blocks = in[1].shape[0];
+      s.block_size = int32_t(in[1].shape[1]);
+      require(in[2].shape[0] >= s.n && in[3].shape[0] >= s.n, "tables/lengths shorter than q");
+      s.stride = int32_t(in[2].shape[1]);
+      require(int64_t(s.stride) * s.block_size <= (int64_t(1) << 20), "max_context above 1M");
+      s.max_ctx = s.stride * s.block_size;
+      require(out[0].shape[0] == s.n && out[0].shape[1] == s.q_heads && out[0].shape[2] == 512,
+              "out must be [n, heads, 512]");
+      s.scale = 1.0f / std::sqrt(192.0f);
+      s.workspace = ifattn_mla_decode_workspace_size(s.n, s.q_heads, s.max_ctx);
+      return;
+    }
+    case kMlaWriteC8: {
+      require(nin == 2 && nout == 1, "mla write: 2 inputs, 1 output");
+      check_tensor(in[0], BF, R, 2);
+      require(in[0].shape[1] == 576, "rows must be [rows, 576]");
+      s.rows = in[0].shape[0];
+      check_slots(in[1], s.rows, s);
+      check_tensor(out[0], I8, RW, 3);
+      require(out[0].shape[2] == 656, "cache must be [blocks, block_size, 656]");
+      s.num_slots = out[0].shape[0] * out[0].shape[1];
+      return;
+    }
+    default:
+      require(false, "unknown operator");
+  }
+}
+
+template <int OP>
+int32_t prepare(const IFKernelTensorV1 *inputs, uint32_t input_count,
+                const IFKernelTensorV1 *outputs, uint32_t output_count, IFKernelPreparedV1 *out) {
+  if (!out) return ifattn::fail(IFATTN_EINVAL, "prepare: null output");
+  *out = IFKernelPreparedV1{};
+  if (!inputs || !outputs || input_count > 8 || output_count > 4)
+    return ifattn::fail(IFATTN_EINVAL, "prepare: port count");
+  State *s = new (std::nothrow) State{};
+  if (!s) return ifattn::fail(IFATTN_EINVAL, "prepare: host allocation");
+  s->op = OP;
+  try {
+    prepare_op(*s, inputs, input_count, outputs, output_count);
+    for (uint32_t i = 0; i < output_count; ++i) {
+      for (uint32_t j = 0; j < input_count; ++j)
+        require(!overlap(outputs[i], inputs[j]), "output aliases an input");
+      for (uint32_t j = 0; j < i; ++j) require(!overlap(outputs[i], outputs[j]), "outputs alias");
+    }
+  } catch (const Reject &r) {
+    delete s;
+    return ifattn::fail(IFATTN_EINVAL, r.what);
+  }
+  std::memcpy(s->inputs, inputs, sizeof(IFKernelTensorV1) * input_count);
+  std::memcpy(s->outputs, outputs, sizeof(IFKernelTensorV1) * output_count);
+  out->state = s;
+  out->workspace_bytes = s->workspace;
+  out->workspace_alignment = 256;
+  return IFATTN_OK;
+}
+
+int32_t enqueue(void *state, void *workspace, uint64_t bytes, void *stream) {
+  State *s = static_cast<State *>(state);
+  if (!s) return ifattn::fail(IFATTN_EINVAL, "enqueue: null state");
+  if (bytes < s->workspace || (s->workspace && !workspace))
+    return ifattn::fail(IFATTN_EWORKSPACE, "enqueue: workspace smaller than prepared");
+  const IFKernelTensorV1 *in = s->inputs, *out = s->outputs;
+  switch (s->op) {
+    case kWriteBf16:
+      return ifattn_kv_cache_write(in[0].data, in[1].data, out[0].data, out[1].data, in[2].data,
+                                   s->slot_dtype, s->rows, s->row_bytes, s->num_slots, stream);
+    case kWriteC8:
+      return ifattn_kv_cache_write_c8(in[0].data, in[1].data, out[0].data, out[1].data,
+                                      out[2].data, out[3].data, in[2].data, s->slot_dtype, s->rows,
+                                      s->kv_heads, s->head_dim, s->num_slots, stream);
+    case kDecodeBf16:
+      return ifattn_paged_decode_bf16(in[0].data, in[1].data, in[2].data,
+                                      static_cast<const int32_t *>(in[3].data), s->stride,
+                                      static_cast<const int32_t *>(in[4].data), out[0].data, s->n,
+                                      s->q_heads, s->kv_heads, s->head_dim, s->block_size,
+                                      s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
+    case kDecodeC8:
+      return ifattn_paged_decode_c8(in[0].data, in[1].data, in[2].data, in[3].data, in[4].data,
+                                    static_cast<const int32_t *>(in[5].data), s->stride,
+                                    static_cast<const int32_t *>(in[6].data), out[0].data, s->n,
+                                    s->q_heads, s->kv_heads, s->head_dim, s->block_size,
+                                    s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
+    case kPrefillBf16:
+      return ifattn_varlen_prefill_bf16(
+          in[0].data, in[1].data, in[2].data, static_cast<const int32_t *>(in[3].data), s->stride,
+          static_cast<const int32_t *>(in[4].data), static_cast<const int32_t *>(in[5].data),
+          out[0].data, s->n, s->total_q, s->total_q, s->max_ctx, s->q_heads, s->kv_heads,
+          s->head_dim, s->block_size, s->num_blocks, s->scale, workspace, bytes, stream);
+    case kMlaBf16:
+    case kMlaC8:
+      return (s->op == kMlaC8 ? ifattn_mla_decode_c8 : ifattn_mla_decode_bf16)(
+          in[0].data, in[1].data, static_cast<const int32_t *>(in[2].data), s->stride,
+          static_cast<const int32_t *>(in[3].data), out[0].data, s->n, s->q_heads, s->block_size,
+          s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
+    case kMlaWriteC8:
+      return ifattn_mla_cache_write_c8(in[0].data, out[0].data, in[1].data, s->slot_dtype, s->rows,
+                                       s->num_slots, stream);
+    default:
+      return ifattn::fail(IFATTN_EINVAL, "enqueue: unknown operator");
+  }
+}
+
+void release(void *state) { delete static_cast<State *>(state); }
+
+template <int OP>
+IFKernelV1 table() {
+  return IFKernelV1{sizeof(IFKernelV1), 2, kContract[OP], kTarget, &prepare<OP>, &enqueue, &release};
+}
+
+const IFKernelV1 kTables[kOpCount] = {table<0>(), table<1>(), table<2>(), table<3>(),
+                                      table<4>(), table<5>(), table<6>(), table<7>()};
+
+}  // namespace
+
+extern "C" const IFKernelV1 *ifattn_kernel_v1_contract(const char *contract,
+                                                       uint32_t requested_version) {
+  if (!contract || requested_version != 2) return nullptr;
+  for (int i = 0; i < kOpCount; ++i)
+    if (std::strcmp(contract, kContract[i]) == 0) return &kTables[i];
+  return nullptr;
+}
