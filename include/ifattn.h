@@ -100,6 +100,21 @@ int32_t ifattn_paged_decode_bf16(const void *q, const void *k_cache, const void 
                                  float scale, void *workspace, uint64_t workspace_bytes,
                                  void *stream);
 
+/* One decode step as the reference's paged attention operator runs it
+ * (native/src/inferfabric_acl.cpp:1343-1430): the slot-mapped write of `rows`
+ * new K/V rows (as ifattn_kv_cache_write, row = kv_heads*head_dim bf16) followed
+ * by ifattn_paged_decode_bf16 over the updated caches. The write is folded into
+ * the decode prologue launch, so the step is two kernel launches. */
+int32_t ifattn_paged_decode_step_bf16(const void *q, const void *k_rows, const void *v_rows,
+                                      void *k_cache, void *v_cache, const void *slot_mapping,
+                                      int32_t slot_dtype, int64_t rows,
+                                      const int32_t *block_tables, int32_t table_stride,
+                                      const int32_t *seq_lens, void *out, int32_t num_seqs,
+                                      int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                      int32_t block_size, int64_t num_blocks, int32_t max_context,
+                                      float scale, void *workspace, uint64_t workspace_bytes,
+                                      void *stream);
+
 /* Same over an int8 cache with fp32 scales per (token, kv head), dequantized in
  * registers (replaces cache_dequantize + bf16 attention, token_executor.h:812-822). */
 int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, const void *v_cache,

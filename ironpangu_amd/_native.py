@@ -38,6 +38,8 @@ SIGNATURES = {
     "ifattn_paged_decode_workspace_size": (u64, [i32, i32, i32, i32]),
     "ifattn_paged_decode_bf16": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i64,
                                        i32, f32, vp, u64, vp]),
+    "ifattn_paged_decode_step_bf16": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, vp, i32, vp, vp, i32,
+                                            i32, i32, i32, i32, i64, i32, f32, vp, u64, vp]),
     "ifattn_paged_decode_c8": (i32, [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32,
                                      i64, i32, f32, vp, u64, vp]),
     "ifattn_varlen_prefill_workspace_size": (u64, [i32, i32, i32, i32, i32]),

@@ -324,7 +324,8 @@ __global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_decode_kernel(DecodePar
     __syncthreads();
     if (it >= p.queue[1]) break;
     const uint32_t e = uniform(p.items[it]);
-    mla_item<C8>(p, cache, xbuf, int(e >> 12), int(e & 0xfffu), w, lane);
+    const int seq = int(e >> 12);
+    mla_item<C8>(p, cache, xbuf, seq, int(e & 0xfffu), w, lane);
   }
 }
 
@@ -372,12 +373,12 @@ int32_t mla_common(bool c8, const void *q, const void *cache, const int32_t *blo
     return fail(IFATTN_EWORKSPACE, "mla decode: workspace missing, short or misaligned");
   split_k_bind_workspace(p, workspace, heads, 512);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  decode_plan_kernel<><<<1, 1024, 0, s>>>(p);
+  launch_prologue(p, RowWrite{}, s);
   if (c8)
     mla_decode_kernel<true><<<device_cus() * 2, 64 * kMlaWaves, 0, s>>>(p);
   else
     mla_decode_kernel<false><<<device_cus() * 2, 64 * kMlaWaves, 0, s>>>(p);
-  if (p.max_parts > 1) paged_decode_reduce_kernel<512><<<dim3(num_seqs, heads), 64, 0, s>>>(p);
+  launch_merge<512>(p, s);
   return launch_status("mla decode");
 }
 

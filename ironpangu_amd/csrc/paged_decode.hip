@@ -363,7 +363,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 }
 
 // Persistent decode: each workgroup pulls (sequence, partition, kv-head group)
-// items from the queue built by decode_plan_kernel until it is exhausted. The
+// items from the queue built by the prologue kernel until it is exhausted. The
 // waves of a workgroup take the kv heads of one item, so the halves of every
 // cache row are fetched by sibling waves at the same time (whole rows stay
 // DRAM-page friendly; measured ~40% more bandwidth than independent waves).
@@ -371,7 +371,7 @@ template <int D, bool C8>
 __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kernel(
     DecodeParams p, int waves_per_wg) {
   __shared__ int item_slot;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = uniform(int(threadIdx.x >> 6));
   const int groups = (p.kv_heads + waves_per_wg - 1) / waves_per_wg;
   const int total = p.queue[1] * groups;
   while (true) {
@@ -381,26 +381,29 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
     __syncthreads();
     if (it >= total) break;
     const uint32_t e = uniform(p.items[it / groups]);
+    const int seq = int(e >> 12);
     const int kvh = uniform((it % groups) * waves_per_wg + wave);  // wave-uniform for SGPR descriptors
-    if (kvh < p.kv_heads) decode_item<D, C8>(p, int(e >> 12), int(e & 0xfffu), kvh, lane);
+    if (kvh < p.kv_heads) decode_item<D, C8>(p, seq, int(e & 0xfffu), kvh, lane);
   }
 }
 
 namespace {
 template <int D, bool C8>
-void launch_decode(const DecodeParams &p, hipStream_t s) {
-  decode_plan_kernel<><<<1, 1024, 0, s>>>(p);
+void launch_decode(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
+  launch_prologue(p, wr, s);
   const int waves = p.kv_heads < max_decode_waves(D) ? p.kv_heads : max_decode_waves(D);
   paged_decode_kernel<D, C8><<<device_cus() * wgs_per_cu(), 64 * waves, 0, s>>>(p, waves);
-  if (p.max_parts > 1) paged_decode_reduce_kernel<D><<<dim3(p.num_seqs, p.q_heads), 64, 0, s>>>(p);
+  launch_merge<D>(p, s);
 }
+
 }  // namespace
 
 // Decode rows of a packed varlen batch (p.cu_seqlens set), bf16 caches.
 void launch_varlen_decode_rows(const DecodeParams &p, int head_dim, hipStream_t s) {
-  if (head_dim == 64) launch_decode<64, false>(p, s);
-  else if (head_dim == 128) launch_decode<128, false>(p, s);
-  else launch_decode<256, false>(p, s);
+  const RowWrite none{};
+  if (head_dim == 64) launch_decode<64, false>(p, none, s);
+  else if (head_dim == 128) launch_decode<128, false>(p, none, s);
+  else launch_decode<256, false>(p, none, s);
 }
 
 namespace {
@@ -410,7 +413,7 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
                       int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs,
                       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t block_size,
                       int64_t num_blocks, int32_t max_context, float scale, void *workspace,
-                      uint64_t workspace_bytes, void *stream) {
+                      uint64_t workspace_bytes, void *stream, const RowWrite &wr) {
   if (!q || !k_cache || !v_cache || !block_tables || !seq_lens || !out ||
       (c8 && (!k_scale || !v_scale)))
     return fail(IFATTN_EINVAL, "paged decode: null pointer");
@@ -458,13 +461,13 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   split_k_bind_workspace(p, workspace, q_heads, head_dim);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (c8) {
-    if (head_dim == 64) launch_decode<64, true>(p, s);
-    else if (head_dim == 128) launch_decode<128, true>(p, s);
-    else launch_decode<256, true>(p, s);
+    if (head_dim == 64) launch_decode<64, true>(p, wr, s);
+    else if (head_dim == 128) launch_decode<128, true>(p, wr, s);
+    else launch_decode<256, true>(p, wr, s);
   } else {
-    if (head_dim == 64) launch_decode<64, false>(p, s);
-    else if (head_dim == 128) launch_decode<128, false>(p, s);
-    else launch_decode<256, false>(p, s);
+    if (head_dim == 64) launch_decode<64, false>(p, wr, s);
+    else if (head_dim == 128) launch_decode<128, false>(p, wr, s);
+    else launch_decode<256, false>(p, wr, s);
   }
   return launch_status("paged decode");
 }
@@ -488,7 +491,7 @@ extern "C" int32_t ifattn_paged_decode_bf16(const void *q, const void *k_cache, 
                                             uint64_t workspace_bytes, void *stream) {
   return decode_common(false, q, k_cache, v_cache, nullptr, nullptr, block_tables, table_stride,
                        seq_lens, out, num_seqs, q_heads, kv_heads, head_dim, block_size, num_blocks,
-                       max_context, scale, workspace, workspace_bytes, stream);
+                       max_context, scale, workspace, workspace_bytes, stream, RowWrite{});
 }
 
 extern "C" int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, const void *v_cache,
@@ -501,5 +504,34 @@ extern "C" int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, co
                                           uint64_t workspace_bytes, void *stream) {
   return decode_common(true, q, k_cache, v_cache, k_scale, v_scale, block_tables, table_stride,
                        seq_lens, out, num_seqs, q_heads, kv_heads, head_dim, block_size, num_blocks,
-                       max_context, scale, workspace, workspace_bytes, stream);
+                       max_context, scale, workspace, workspace_bytes, stream, RowWrite{});
+}
+
+extern "C" int32_t ifattn_paged_decode_step_bf16(
+    const void *q, const void *k_rows, const void *v_rows, void *k_cache, void *v_cache,
+    const void *slot_mapping, int32_t slot_dtype, int64_t rows, const int32_t *block_tables,
+    int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs, int32_t q_heads,
+    int32_t kv_heads, int32_t head_dim, int32_t block_size, int64_t num_blocks,
+    int32_t max_context, float scale, void *workspace, uint64_t workspace_bytes, void *stream) {
+  if (rows < 0 || (rows > 0 && (!k_rows || !v_rows || !slot_mapping)))
+    return fail(IFATTN_EINVAL, "decode step: rows >= 0 with k/v rows and slot mapping");
+  if (slot_dtype != IFATTN_DTYPE_I32 && slot_dtype != IFATTN_DTYPE_I64)
+    return fail(IFATTN_EINVAL, "decode step: slot mapping dtype must be I32 (4) or I64 (5)");
+  if (rows > 0 && (!aligned16(k_rows) || !aligned16(v_rows)))
+    return fail(IFATTN_EINVAL, "decode step: k/v rows must be 16-byte aligned");
+  RowWrite wr{};
+  if (rows > 0) {
+    wr.k_rows = static_cast<const uint8_t *>(k_rows);
+    wr.v_rows = static_cast<const uint8_t *>(v_rows);
+    wr.k_cache = static_cast<uint8_t *>(k_cache);
+    wr.v_cache = static_cast<uint8_t *>(v_cache);
+    wr.slots = slot_mapping;
+    wr.slot_i64 = slot_dtype == IFATTN_DTYPE_I64;
+    wr.rows = rows;
+    wr.row_vecs = int64_t(kv_heads) * head_dim * 2 / 16;
+    wr.num_slots = num_blocks * block_size;
+  }
+  return decode_common(false, q, k_cache, v_cache, nullptr, nullptr, block_tables, table_stride,
+                       seq_lens, out, num_seqs, q_heads, kv_heads, head_dim, block_size, num_blocks,
+                       max_context, scale, workspace, workspace_bytes, stream, wr);
 }

@@ -1,7 +1,9 @@
 // Split-K scheduling shared by the paged decode kernels (GQA and MLA):
 // per-call device work list in longest-processing-time order, a work queue
 // drained by persistent workgroups, (m, l, O) partials per (sequence,
-// partition, head) and the merge kernel that combines them.
+// partition, head) combined by a merge launch. The prologue kernel that builds
+// the work list also performs the step's slot-mapped row writes, so a decode
+// step is prologue -> decode -> merge from one host call.
 #pragma once
 #include <cstdlib>
 
@@ -52,10 +54,40 @@ __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
 // queue are the shortest and the persistent workgroups finish together.
 // Sequences with no visible key get one zero-length item at the very end.
 // One workgroup of 1024 threads.
+// Slot-mapped row writes folded into the prologue (cache[slot[r]] = rows[r]).
+struct RowWrite {
+  const uint8_t *k_rows, *v_rows;
+  uint8_t *k_cache, *v_cache;
+  const void *slots;
+  int slot_i64;
+  int64_t rows, row_vecs, num_slots;
+};
+
+__device__ __forceinline__ void prologue_write(const RowWrite &w) {
+  const int64_t total = w.rows * w.row_vecs * (w.v_rows ? 2 : 1);
+  for (int64_t i = int64_t(blockIdx.x - 1) * blockDim.x + threadIdx.x; i < total;
+       i += int64_t(gridDim.x - 1) * blockDim.x) {
+    const int64_t per = w.rows * w.row_vecs;
+    const bool v = i >= per;
+    const int64_t j = v ? i - per : i;
+    const int64_t r = j / w.row_vecs, c = j - r * w.row_vecs;
+    const int64_t slot = w.slot_i64 ? static_cast<const int64_t *>(w.slots)[r]
+                                    : int64_t(static_cast<const int32_t *>(w.slots)[r]);
+    if (slot < 0 || slot >= w.num_slots) continue;
+    const uint8_t *src = v ? w.v_rows : w.k_rows;
+    uint8_t *dst = v ? w.v_cache : w.k_cache;
+    store_u32x4(dst + (slot * w.row_vecs + c) * 16, load_u32x4(src + (r * w.row_vecs + c) * 16));
+  }
+}
+
+// Workgroup 0 plans; workgroups 1.. perform the row writes (if any).
 template <int Unused = 0>
-__global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
+__global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, RowWrite wr) {
+  if (blockIdx.x > 0) {
+    prologue_write(wr);
+    return;
+  }
   constexpr int kBuckets = 257;  // 32-token buckets of PT <= 8192, plus empty rows
-  __shared__ int scan[1024];
   __shared__ int bucket[kBuckets];
   __shared__ int carry;
   const int tid = threadIdx.x;
@@ -65,6 +97,8 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
   if (tid == 0) carry = 0;
   __syncthreads();
   // Pass 1: full partitions in sequence order; histogram of partial ones.
+  __shared__ int wave_tot[16];
+  const int lane = tid & 63, wv = tid >> 6;
   for (int base = 0; base < p.num_seqs; base += 1024) {
     const int seq = base + tid;
     int nfull = 0, bk = -1;
@@ -75,18 +109,21 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
       bk = len <= 0 ? nb : (rem > 0 ? (PT - rem) / 32 : -1);
       if (bk >= 0) atomicAdd(&bucket[bk], 1);
     }
-    scan[tid] = nfull;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int v = tid >= off ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] += v;
-      __syncthreads();
+    // inclusive scan of nfull: within the wave by shuffles, then across waves
+    int x = nfull;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      x += lane >= off ? y : 0;
     }
-    const int start = carry + scan[tid] - nfull;
+    if (lane == 63) wave_tot[wv] = x;
+    __syncthreads();
+    int before = carry;
+    for (int w2 = 0; w2 < wv; ++w2) before += wave_tot[w2];
+    const int start = before + x - nfull;
     for (int k = 0; k < nfull; ++k) p.items[start + k] = (uint32_t(seq) << 12) | uint32_t(k);
     __syncthreads();
-    if (tid == 1023) carry += scan[1023];
+    if (tid == 1023) carry = start + nfull;
     __syncthreads();
   }
   // Exclusive scan of the bucket counts, offset by the full-item count.
@@ -114,41 +151,98 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(DecodeParams p) {
   }
 }
 
-// Merge split-K partials: one wave per (sequence, q head); lane l owns dims
-// [l*D/64, (l+1)*D/64).
+// Merge the split-K partials of one (sequence, head) with one wave; lane l
+// owns dims [l*D/64, (l+1)*D/64). Partitions are taken 64 at a time: lane k
+// holds partition k's (m, l), the weights reach the other lanes by shuffle, and
+// the partial-O loads of a batch are independent of each other.
 template <int D>
-__global__ __launch_bounds__(64) void paged_decode_reduce_kernel(DecodeParams p) {
-  const int seq = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
-  if (!decode_seq(p, seq)) return;
-  const int nparts = parts_of(clamp_len(p, seq), p.part_tokens);
-  if (nparts <= 1) return;
+__device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h, int nparts,
+                                           int lane) {
   constexpr int V = D / 64;
   const int64_t row0 = int64_t(seq) * p.max_parts * p.q_heads + h;
   const int64_t pstride = p.q_heads;
+  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + lane * V;
+  constexpr int kFast = 16;
+  if (nparts <= kFast) {
+    // One round trip: (m, l) of partition `lane` and every partial O slice are
+    // loaded together, then reduced in registers.
+    float2 ml = make_float2(-INFINITY, 0.0f);
+    if (lane < nparts) ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + lane * pstride) * 2);
+    float o[kFast][V];
+#pragma unroll
+    for (int u = 0; u < kFast; ++u)
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        o[u][i] = u < nparts ? p.part_o[(row0 + int64_t(u) * pstride) * D + lane * V + i] : 0.0f;
+    float mmax = ml.x;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+    const float w = lane < nparts ? fast_exp2(ml.x - mmax) : 0.0f;
+    float lsum = w * ml.y;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kFast; ++u) {
+      const float wu = __shfl(w, u, 64);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += wu * o[u][i];
+    }
+    const float inv = 1.0f / lsum;
+    if constexpr (V == 1) {
+      op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
+    } else {
+#pragma unroll
+      for (int i = 0; i < V; i += 2)
+        *reinterpret_cast<uint32_t *>(op + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
+    }
+    return;
+  }
   float mmax = -INFINITY;
   for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, p.part_ml[(row0 + k * pstride) * 2]);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
   float lsum = 0.0f;
-  for (int k = lane; k < nparts; k += 64) {
-    const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + k * pstride) * 2);
-    lsum += fast_exp2(ml.x - mmax) * ml.y;
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-#pragma unroll 4
-  for (int k = 0; k < nparts; ++k) {
-    const int64_t row = row0 + k * pstride;
-    const float w = fast_exp2(p.part_ml[row * 2] - mmax);
-    const float *src = p.part_o + row * D + lane * V;
+  for (int k0 = 0; k0 < nparts; k0 += 64) {
+    const int k = k0 + lane;
+    float w = 0.0f;
+    if (k < nparts) {
+      const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + k * pstride) * 2);
+      w = fast_exp2(ml.x - mmax);
+      lsum += w * ml.y;
+    }
+    const int n = nparts - k0 < 64 ? nparts - k0 : 64;
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      float o[8][V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] += w * src[i];
+      for (int u = 0; u < 8; ++u) {
+        const float *src = p.part_o + (row0 + int64_t(k0 + j + u) * pstride) * D + lane * V;
+#pragma unroll
+        for (int i = 0; i < V; ++i) o[u][i] = src[i];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wu = __shfl(w, j + u, 64);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] += wu * o[u][i];
+      }
+    }
+    for (; j < n; ++j) {
+      const float wu = __shfl(w, j, 64);
+      const float *src = p.part_o + (row0 + int64_t(k0 + j) * pstride) * D + lane * V;
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += wu * src[i];
+    }
   }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
   const float inv = 1.0f / lsum;
-  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + lane * V;
   if constexpr (V == 1) {
     op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
   } else {
@@ -156,6 +250,29 @@ __global__ __launch_bounds__(64) void paged_decode_reduce_kernel(DecodeParams p)
     for (int i = 0; i < V; i += 2)
       *reinterpret_cast<uint32_t *>(op + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
   }
+}
+
+// Merge launch: one wave per (sequence, head); only sequences split over more
+// than one partition have partials. (An in-kernel merge was measured slower:
+// partials written on other XCDs are only visible through an L2 writeback or
+// uncached accesses, both costlier than this launch.)
+template <int D>
+__global__ __launch_bounds__(1024) void split_k_merge_kernel(DecodeParams p) {
+  const int seq = blockIdx.x;
+  if (!decode_seq(p, seq)) return;
+  const int nparts = parts_of(clamp_len(p, seq), p.part_tokens);
+  if (nparts <= 1) return;
+  const int waves = blockDim.x >> 6;
+  for (int h = threadIdx.x >> 6; h < p.q_heads; h += waves)
+    merge_head<D>(p, seq, h, nparts, threadIdx.x & 63);
+}
+
+// One workgroup per sequence, one wave per head (up to 16 waves).
+template <int D>
+inline void launch_merge(const DecodeParams &p, hipStream_t s) {
+  if (p.max_parts <= 1) return;
+  const int waves = p.q_heads < 16 ? p.q_heads : 16;
+  split_k_merge_kernel<D><<<p.num_seqs, 64 * waves, 0, s>>>(p);
 }
 
 constexpr uint64_t kQueueBytes = 64;
@@ -214,9 +331,19 @@ inline void split_k_bind_workspace(DecodeParams &p, void *workspace, int heads, 
   uint8_t *w = static_cast<uint8_t *>(workspace);
   const uint64_t items = uint64_t(p.num_seqs) * p.max_parts;
   p.queue = reinterpret_cast<int32_t *>(w);
-  p.items = reinterpret_cast<uint32_t *>(w + kQueueBytes);
-  p.part_o = reinterpret_cast<float *>(w + kQueueBytes + align16(items * 4));
+  w += kQueueBytes;
+  p.items = reinterpret_cast<uint32_t *>(w);
+  w += align16(items * 4);
+  p.part_o = reinterpret_cast<float *>(w);
   p.part_ml = p.part_o + items * heads * dims;
+}
+
+// Prologue launch: planning workgroup plus enough writer workgroups for `wr`.
+inline void launch_prologue(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
+  const int64_t vecs = wr.rows * wr.row_vecs * (wr.v_rows ? 2 : 1);
+  const int64_t writers = vecs > 0 ? (vecs + 1023) / 1024 : 0;
+  const int grid = 1 + int(writers < 1024 ? writers : 1024);
+  decode_prologue_kernel<><<<grid, 1024, 0, s>>>(p, wr);
 }
 
 // Launches plan + decode + merge for the single-row sequences of a packed

@@ -170,6 +170,35 @@ def paged_decode(q, k_cache, v_cache, block_tables, seq_lens, max_context, scale
     return out
 
 
+def paged_decode_step(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, seq_lens,
+                      max_context, scale=None, out=None, workspace=None, stream=None):
+    """Slot-mapped write of k_new/v_new [rows, kv_heads, head_dim] followed by
+    paged decode over the updated bf16 caches, in two launches."""
+    _dev(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, seq_lens, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3, "q: bf16 [num_seqs, q_heads, head_dim]")
+    ns, hq, hd = q.shape
+    _req(k_cache.dtype == torch.bfloat16 and k_cache.dim() == 4 and k_cache.shape == v_cache.shape
+         and k_cache.shape[3] == hd, "caches: bf16 [num_blocks, block_size, kv_heads, head_dim]")
+    nb, bs, hkv, _ = k_cache.shape
+    _req(k_new.shape == v_new.shape and k_new.dim() == 3 and tuple(k_new.shape[1:]) == (hkv, hd)
+         and k_new.dtype == torch.bfloat16, "new rows: bf16 [rows, kv_heads, head_dim]")
+    _req(slot_mapping.numel() == k_new.shape[0], "one slot per new row")
+    _check_tables(block_tables, seq_lens, ns, bs, max_context)
+    if scale is None:
+        scale = 1.0 / math.sqrt(hd)
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        workspace = decode_workspace(ns, hq, hd, max_context, q.device)
+    st = lib().ifattn_paged_decode_step_bf16(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping),
+        _slot_dtype(slot_mapping), k_new.shape[0], _ptr(block_tables), block_tables.shape[1],
+        _ptr(seq_lens), _ptr(out), ns, hq, hkv, hd, bs, nb, max_context, float(scale),
+        _ptr(workspace), workspace.numel(), _stream(stream))
+    check(st, "ifattn_paged_decode_step_bf16")
+    return out
+
+
 # ---------------------------------------------------------------- varlen prefill
 
 def prefill_workspace(num_seqs, total_q, q_heads, head_dim, max_kv_len, device="cuda"):

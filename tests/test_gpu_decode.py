@@ -132,3 +132,31 @@ def test_graph_replay_matches_eager():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs from eager"
+
+
+def test_decode_step_matches_write_then_decode():
+    """The fused step (write folded into the decode prologue) equals a separate
+    write followed by decode, bit for bit, including partitioned sequences."""
+    import torch
+    from ironpangu_amd import ops
+    case = W.decode_host_case(12, num_seqs=9, lo=1, hi=9000, dist="loguniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=128, pool_blocks=9 * 71)
+    h = case.host
+    nb, bs, hkv, hd = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim
+    kc1 = to_dev(h["k_pool"]).view(nb, bs, hkv, hd)
+    vc1 = to_dev(h["v_pool"]).view(nb, bs, hkv, hd)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    args = (to_dev(h["q"]), to_dev(h["k_new"]), to_dev(h["v_new"]))
+    slots = to_dev(case.slot_mapping.astype(np.int32))
+    tables, lens = to_dev(case.block_tables), to_dev(case.seq_lens)
+    out1 = ops.paged_decode_step(args[0], args[1], args[2], kc1, vc1, slots, tables, lens,
+                                 case.max_context, case.scale)
+    ops.kv_cache_write(args[1], args[2], kc2, vc2, slots)
+    out2 = ops.paged_decode(args[0], kc2, vc2, tables, lens, case.max_context, case.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(out1, out2)
+    exp = oracle.paged_decode(h["q"], bits_host(kc2).reshape(-1, hkv, hd),
+                              bits_host(vc2).reshape(-1, hkv, hd), case.block_tables,
+                              case.seq_lens, 16, 2, 128, 128, case.scale)
+    assert_close(bf16_host(out1), exp)
