@@ -28,6 +28,19 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_decode_kernels.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the config-2 decode kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy calibration)."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch paged_decode_kernel config2:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def parse():
@@ -38,6 +51,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-seqs", type=int, default=64)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (counter calibration)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip configs 3-5 (reported under 'secondary')")
     return ap.parse_args()
@@ -338,6 +353,18 @@ def main():
     from ironpangu_amd import ops
     from ironpangu_amd import workloads as W
 
+    if args.calibrate_copy:
+        # Known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE: each copy
+        # reads and writes exactly 1 GiB.
+        src = torch.ones(1 << 29, dtype=torch.int16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30,
+                          "launches": 5}))
+        return
+
     case, t = gpu_workload(args.seed)
     ws = ops.decode_workspace(case.num_seqs, case.q_heads, case.head_dim, case.max_context)
     out = torch.empty_like(t["q"])
@@ -407,7 +434,9 @@ def main():
         "algorithmic_bytes_per_step": nbytes["total"],
         "roofline": {"bound": "hbm", "kernel": "paged_decode_step operator (prologue: plan + row writes; decode with fused split-K merge)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                     "traffic_note": "HBM bytes per decode-kernel launch, rocprofv3 FETCH_SIZE x2.0 + "
+                                     "WRITE_SIZE x1.0 (profiles/hbm_traffic_decode_kernels.md)",
                      "avg_ms": round(attn_avg, 5),
                      "algorithmic_bytes": nbytes["total"]},
     }
