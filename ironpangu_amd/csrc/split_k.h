@@ -151,55 +151,19 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
   }
 }
 
-// Merge the split-K partials of one (sequence, head) with one wave; lane l
-// owns dims [l*D/64, (l+1)*D/64). Partitions are taken 64 at a time: lane k
-// holds partition k's (m, l), the weights reach the other lanes by shuffle, and
-// the partial-O loads of a batch are independent of each other.
-template <int D>
+// Merge the split-K partials of one (sequence, head) over the dims
+// [dim0, dim0 + DW) with one wave; lane l owns DW/64 consecutive dims. Up to
+// kFast partitions go in one round trip: lane k holds partition k's (m, l) and
+// every partial-O slice is loaded before any is used; the weights reach the
+// other lanes by shuffle. Longer lists are taken kFast at a time.
+template <int D, int DW>
 __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h, int nparts,
-                                           int lane) {
-  constexpr int V = D / 64;
+                                           int dim0, int lane) {
+  constexpr int V = DW / 64;
+  constexpr int kFast = 32;
   const int64_t row0 = int64_t(seq) * p.max_parts * p.q_heads + h;
   const int64_t pstride = p.q_heads;
-  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + lane * V;
-  constexpr int kFast = 16;
-  if (nparts <= kFast) {
-    // One round trip: (m, l) of partition `lane` and every partial O slice are
-    // loaded together, then reduced in registers.
-    float2 ml = make_float2(-INFINITY, 0.0f);
-    if (lane < nparts) ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + lane * pstride) * 2);
-    float o[kFast][V];
-#pragma unroll
-    for (int u = 0; u < kFast; ++u)
-#pragma unroll
-      for (int i = 0; i < V; ++i)
-        o[u][i] = u < nparts ? p.part_o[(row0 + int64_t(u) * pstride) * D + lane * V + i] : 0.0f;
-    float mmax = ml.x;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
-    const float w = lane < nparts ? fast_exp2(ml.x - mmax) : 0.0f;
-    float lsum = w * ml.y;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-#pragma unroll
-    for (int u = 0; u < kFast; ++u) {
-      const float wu = __shfl(w, u, 64);
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += wu * o[u][i];
-    }
-    const float inv = 1.0f / lsum;
-    if constexpr (V == 1) {
-      op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
-    } else {
-#pragma unroll
-      for (int i = 0; i < V; i += 2)
-        *reinterpret_cast<uint32_t *>(op + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
-    }
-    return;
-  }
+  const int d = dim0 + lane * V;
   float mmax = -INFINITY;
   for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, p.part_ml[(row0 + k * pstride) * 2]);
 #pragma unroll
@@ -208,41 +172,29 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-  for (int k0 = 0; k0 < nparts; k0 += 64) {
-    const int k = k0 + lane;
-    float w = 0.0f;
-    if (k < nparts) {
-      const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + k * pstride) * 2);
-      w = fast_exp2(ml.x - mmax);
-      lsum += w * ml.y;
-    }
-    const int n = nparts - k0 < 64 ? nparts - k0 : 64;
-    int j = 0;
-    for (; j + 8 <= n; j += 8) {
-      float o[8][V];
+  for (int k0 = 0; k0 < nparts; k0 += kFast) {
+    const int n = nparts - k0 < kFast ? nparts - k0 : kFast;
+    float2 ml = make_float2(-INFINITY, 0.0f);
+    if (lane < n) ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + (k0 + lane) * pstride) * 2);
+    float o[kFast][V];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float *src = p.part_o + (row0 + int64_t(k0 + j + u) * pstride) * D + lane * V;
+    for (int u = 0; u < kFast; ++u)
 #pragma unroll
-        for (int i = 0; i < V; ++i) o[u][i] = src[i];
-      }
+      for (int i = 0; i < V; ++i)
+        o[u][i] = u < n ? p.part_o[(row0 + int64_t(k0 + u) * pstride) * D + d + i] : 0.0f;
+    const float w = lane < n ? fast_exp2(ml.x - mmax) : 0.0f;
+    lsum += w * ml.y;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float wu = __shfl(w, j + u, 64);
+    for (int u = 0; u < kFast; ++u) {
+      const float wu = __shfl(w, u, 64);
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] += wu * o[u][i];
-      }
-    }
-    for (; j < n; ++j) {
-      const float wu = __shfl(w, j, 64);
-      const float *src = p.part_o + (row0 + int64_t(k0 + j) * pstride) * D + lane * V;
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += wu * src[i];
+      for (int i = 0; i < V; ++i) acc[i] += wu * o[u][i];
     }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
   const float inv = 1.0f / lsum;
+  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + d;
   if constexpr (V == 1) {
     op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
   } else {
@@ -257,22 +209,21 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
 // partials written on other XCDs are only visible through an L2 writeback or
 // uncached accesses, both costlier than this launch.)
 template <int D>
-__global__ __launch_bounds__(1024) void split_k_merge_kernel(DecodeParams p) {
-  const int seq = blockIdx.x;
+__global__ __launch_bounds__(256) void split_k_merge_kernel(DecodeParams p) {
+  constexpr int DW = D < 128 ? D : 128;  // dims per wave
+  const int seq = blockIdx.x, h = blockIdx.y;
   if (!decode_seq(p, seq)) return;
   const int nparts = parts_of(clamp_len(p, seq), p.part_tokens);
   if (nparts <= 1) return;
-  const int waves = blockDim.x >> 6;
-  for (int h = threadIdx.x >> 6; h < p.q_heads; h += waves)
-    merge_head<D>(p, seq, h, nparts, threadIdx.x & 63);
+  merge_head<D, DW>(p, seq, h, nparts, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
 }
 
-// One workgroup per sequence, one wave per head (up to 16 waves).
+// One workgroup per (sequence, head); one wave per 128 output dims.
 template <int D>
 inline void launch_merge(const DecodeParams &p, hipStream_t s) {
   if (p.max_parts <= 1) return;
-  const int waves = p.q_heads < 16 ? p.q_heads : 16;
-  split_k_merge_kernel<D><<<p.num_seqs, 64 * waves, 0, s>>>(p);
+  constexpr int waves = D > 128 ? D / 128 : 1;
+  split_k_merge_kernel<D><<<dim3(p.num_seqs, p.q_heads), 64 * waves, 0, s>>>(p);
 }
 
 constexpr uint64_t kQueueBytes = 64;

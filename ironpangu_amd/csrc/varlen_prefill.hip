@@ -63,18 +63,19 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
   const int nbk = (p.max_kv + 255) / 256 + 1;  // <= kBuckets (host-checked)
   for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
   __syncthreads();
-  auto cost_bucket = [&](int seq, int qt, int count) {
-    int kv = p.kv_lens[seq];
-    kv = kv > p.max_kv ? p.max_kv : kv;
+  // Bucket of query tile qt: the key tokens it visits, most work first.
+  auto cost_bucket = [&](int kv, int qt, int count) {
     const int rows_end = (qt + 1) * QT < count ? (qt + 1) * QT : count;
     int reach = kv - count + rows_end;
     reach = reach < 0 ? 0 : (reach > p.max_kv ? p.max_kv : reach);
-    return nbk - 1 - reach / 256;  // most work first
+    return nbk - 1 - reach / 256;
   };
   for (int seq = tid; seq < p.num_seqs; seq += 1024) {
     const int count = p.cu[seq + 1] - p.cu[seq];
     if (count <= 1) continue;
-    for (int qt = 0; qt * QT < count; ++qt) atomicAdd(&bucket[cost_bucket(seq, qt, count)], 1);
+    int kv = p.kv_lens[seq];
+    kv = kv > p.max_kv ? p.max_kv : kv;
+    for (int qt = 0; qt * QT < count; ++qt) atomicAdd(&bucket[cost_bucket(kv, qt, count)], 1);
   }
   __syncthreads();
   if (tid == 0) {
@@ -90,9 +91,12 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
   for (int seq = tid; seq < p.num_seqs; seq += 1024) {
     const int count = p.cu[seq + 1] - p.cu[seq];
     if (count <= 1) continue;
-    for (int qt = 0; qt * QT < count; ++qt)
-      p.items[atomicAdd(&bucket[cost_bucket(seq, qt, count)], 1)] =
-          (uint32_t(seq) << 12) | uint32_t(qt);
+    int kv = p.kv_lens[seq];
+    kv = kv > p.max_kv ? p.max_kv : kv;
+    for (int qt = 0; qt * QT < count; ++qt) {
+      const int slot = atomicAdd(&bucket[cost_bucket(kv, qt, count)], 1);
+      p.items[slot] = (uint32_t(seq) << 12) | uint32_t(qt);
+    }
   }
 }
 
