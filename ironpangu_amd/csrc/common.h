@@ -55,6 +55,37 @@ __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
+// Buffer descriptor as four SGPR words, for the direct-to-LDS load below.
+__device__ __forceinline__ u32x4 raw_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(a))),
+               uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(a >> 32) & 0xffffu)),
+               uint32_t(__builtin_amdgcn_readfirstlane(bytes)), 0x00020000u};
+}
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return uint32_t(reinterpret_cast<uintptr_t>(
+      (const __attribute__((address_space(3))) char *)(p)));
+}
+// Direct-to-LDS load (buffer_load_dwordx4 ... lds): lane i's 16 bytes at
+// offset voff of the buffer land at LDS byte lds_base + 16*i (lds_base is
+// wave-uniform); offsets past the buffer end write zeros. The compiler does not
+// see these LDS writes: the caller waits for them with lds_dma_wait<N>() (N =
+// direct loads it may leave in flight) and a workgroup barrier before any wave
+// reads the bytes, and must not let such a load target bytes a wave may still
+// be reading.
+__device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds_base)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void lds_dma_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
 // v_perm_b32 byte select: result byte i = byte sel[i] of {hi:lo} (lo = bytes 0-3).
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);

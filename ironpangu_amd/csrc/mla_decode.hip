@@ -28,66 +28,33 @@ namespace ifattn {
 
 constexpr int kMlaWaves = 4;
 constexpr int kMlaTile = 32;
-constexpr int kMlaStages = 3;
 
 template <bool C8>
 struct MlaRow {
   static constexpr uint32_t BYTES = C8 ? 656 : 1152;
-  static constexpr uint32_t latent(uint32_t d) { return C8 ? d : 2 * d; }       // byte of dim d < 512
-  static constexpr uint32_t rope(uint32_t d) { return C8 ? 512 + 2 * d : 1024 + 2 * d; }  // d < 64
-  static constexpr uint32_t scale(uint32_t t) { return 640 + 4 * t; }
+  // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16) / 1312 (C8) 16-byte chunks.
+  static constexpr int NI = C8 ? 6 : 9;
+  static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
+  static constexpr int STAGES = C8 ? 6 : 4;
+  // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B, a multiple of
+  // 128) XOR the chunk index with the row's low 3 bits so the 16 rows that one
+  // K read touches spread over the banks; C8 rows (656 B) are not swizzled.
+  static __device__ __forceinline__ uint32_t chunk(uint32_t r, uint32_t j) {
+    return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ (r & 7));
+  }
 };
+static_assert(MlaRow<false>::SLOT * MlaRow<false>::STAGES + 4 * 64 * 32 <= 160 * 1024, "LDS");
+static_assert(MlaRow<true>::SLOT * MlaRow<true>::STAGES + 4 * 64 * 32 <= 160 * 1024, "LDS");
+static_assert(MlaRow<false>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
+static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 
-template <bool C8>
-struct MlaTileRegs {
-  u32x4 k[2][5];  // [mt][step]: 4 latent steps (C8: 8 codes in .xy), step 4 = rope (bf16)
-  u32x4 v[8];     // dims 128w + 8c .. +8 of token tile_token(g, j) (C8: 8 codes in .xy)
-  float sk[C8 ? 8 : 1];
-};
-
-struct MlaLane {
-  uint32_t k[2], kr[2], v[8], sc[8];
-};
+constexpr int kMlaLds =
+    MlaRow<false>::SLOT * MlaRow<false>::STAGES > MlaRow<true>::SLOT * MlaRow<true>::STAGES
+        ? MlaRow<false>::SLOT * MlaRow<false>::STAGES
+        : MlaRow<true>::SLOT * MlaRow<true>::STAGES;
 
 __device__ __forceinline__ int mla_tile_token(int g, int j) {
   return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-}
-
-template <bool C8>
-__device__ __forceinline__ void mla_load_tile(MlaTileRegs<C8> &t, const DecodeParams &p,
-                                              const uint8_t *cache, int lane_blocks, int t_begin,
-                                              int t0, int t_end, int w, const MlaLane &o) {
-  using R = MlaRow<C8>;
-  const int bs = p.block_size;
-  const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 - (t_begin & ~(bs - 1))) / bs);
-  const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
-  const int n_live = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
-  const auto rc = make_rsrc(cache + tok0 * R::BYTES, uint32_t(n_live) * R::BYTES);
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if constexpr (C8) {
-        const u32x2 x = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rc, o.k[mt] + 32 * s, 0, 0));
-        t.k[mt][s] = u32x4{x[0], x[1], 0u, 0u};
-      } else {
-        t.k[mt][s] = buf_load_x4(rc, o.k[mt] + 64 * s);
-      }
-    }
-    t.k[mt][4] = w < 2 ? buf_load_x4(rc, o.kr[mt]) : u32x4{0, 0, 0, 0};
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if constexpr (C8) {
-      const u32x2 x =
-          __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rc, o.v[j], 0, 0));
-      t.v[j] = u32x4{x[0], x[1], 0u, 0u};
-      t.sk[j] = buf_load_f32(rc, o.sc[j]);
-    } else {
-      t.v[j] = buf_load_x4(rc, o.v[j]);
-    }
-  }
 }
 
 __device__ __forceinline__ uint32_t mla_i8pair(int a, int b) {
@@ -99,11 +66,17 @@ __device__ __forceinline__ u32x4 mla_i8x8(uint32_t lo, uint32_t hi) {
                mla_i8pair(mla_i8(hi, 0), mla_i8(hi, 1)), mla_i8pair(mla_i8(hi, 2), mla_i8(hi, 3))};
 }
 
+// One (sequence, partition) item. The partition's 32-token tiles are copied
+// HBM -> LDS once by direct-to-LDS loads shared by the four waves (each tile is
+// 32 consecutive rows of one block) through a ring of R::STAGES slots; every
+// wave then reads its K operand (tokens in rows) and its V operand (dims in
+// rows) from the same LDS bytes.
 template <bool C8>
 __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *cache,
-                                         float (*xbuf)[kMlaWaves][64][8], int seq, int part, int w,
-                                         int lane) {
+                                         uint8_t *ring, float (*xbuf)[8], int seq, int part,
+                                         int w, int lane) {
   using R = MlaRow<C8>;
+  constexpr int S = R::STAGES;
   const int len = clamp_len(p, seq);
   const int PT = p.part_tokens;
   const int nparts = parts_of(len, PT);
@@ -130,22 +103,10 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
       qv[s] = head_live ? load_u32x4(qp + 128 * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
     qv[4] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
   }
-  MlaLane o;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const uint32_t row = uint32_t(16 * mt + c) * R::BYTES;
-    o.k[mt] = row + R::latent(128 * w + 8 * g);
-    o.kr[mt] = row + R::rope(32 * (w & 1) + 8 * g);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t row = uint32_t(mla_tile_token(g, j)) * R::BYTES;
-    o.v[j] = row + R::latent(128 * w + 8 * c);
-    o.sc[j] = row + R::scale(w);
-  }
 
   const int t_begin = part * PT;
   const int t_end = t_begin + PT < len ? t_begin + PT : len;
+  const int n_tiles = (t_end - t_begin + kMlaTile - 1) / kMlaTile;
   int lane_blocks;
   {
     const int first = t_begin / p.block_size;
@@ -153,23 +114,84 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
     int b = lane < nblk ? p.block_tables[int64_t(seq) * p.table_stride + first + lane] : 0;
     lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
   }
+  // Source offset (within a tile) of the 16-byte chunk each lane moves per load.
+  uint32_t src[R::NI];
+#pragma unroll
+  for (int k = 0; k < R::NI; ++k) {
+    const uint32_t l = uint32_t((k * 4 + w) * 64 + lane);
+    if constexpr (C8) {
+      src[k] = 16 * l;  // chunks past the 32 rows fall outside the tile's extent
+    } else {
+      const uint32_t r = l / 72, jj = l % 72;
+      src[k] = r * R::BYTES + 16 * (jj ^ (r & 7));
+    }
+  }
+  const uint32_t ring_base = lds_addr(ring);
+  auto issue = [&](int ti) {
+    const int t0 = t_begin + ti * kMlaTile;
+    const int bs = p.block_size;
+    const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 - (t_begin & ~(bs - 1))) / bs);
+    const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
+    const int n_live = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
+    const u32x4 rc = raw_rsrc(cache + tok0 * R::BYTES, uint32_t(n_live) * R::BYTES);
+    const uint32_t dst = ring_base + uint32_t(ti % S) * R::SLOT + uint32_t(w) * 1024;
+#pragma unroll
+    for (int k = 0; k < R::NI; ++k) lds_dma16(rc, src[k], dst + uint32_t(k) * 4096);
+  };
 
   f32x4 oacc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0, 0, 0, 0};
   float m_run = -INFINITY, l_run = 0.0f;
-  int parity = 0;
 
-  auto compute = [&](const MlaTileRegs<C8> &t, int t0) {
+  auto compute = [&](const uint8_t *tile, int t0) {
+    // K operand: token 16mt + c, latent dims 128w + 32s + 8g (+ rope dims 32(w&1) + 8g).
+    u32x4 k[2][5];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const uint32_t r = uint32_t(16 * mt + c);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if constexpr (C8) {
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + 128 * w + 32 * s + 8 * g);
+          k[mt][s] = u32x4{x[0], x[1], 0u, 0u};
+        } else {
+          k[mt][s] = load_u32x4(tile + R::chunk(r, uint32_t(16 * w + 4 * s + g)));
+        }
+      }
+      if (w < 2) {
+        if constexpr (C8)
+          k[mt][4] = load_u32x4(tile + r * R::BYTES + 512 + 64 * (w & 1) + 16 * g);
+        else
+          k[mt][4] = load_u32x4(tile + R::chunk(r, uint32_t(64 + 4 * (w & 1) + g)));
+      } else {
+        k[mt][4] = u32x4{0, 0, 0, 0};
+      }
+    }
+    // V operand rows: token tile_token(g, j), latent dims 128w + 8c .. +8.
+    u32x4 v[8];
+    float sk[C8 ? 8 : 1];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t r = uint32_t(mla_tile_token(g, j));
+      if constexpr (C8) {
+        const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + 128 * w + 8 * c);
+        v[j] = u32x4{x[0], x[1], 0u, 0u};
+        sk[j] = *reinterpret_cast<const float *>(tile + r * R::BYTES + 640 + 4 * w);
+      } else {
+        v[j] = load_u32x4(tile + R::chunk(r, uint32_t(16 * w + c)));
+      }
+    }
+
     f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if constexpr (C8) {
-        a0 = mfma16x16x32(mla_i8x8(t.k[0][s][0], t.k[0][s][1]), qv[s], a0);
-        a1 = mfma16x16x32(mla_i8x8(t.k[1][s][0], t.k[1][s][1]), qv[s], a1);
+        a0 = mfma16x16x32(mla_i8x8(k[0][s][0], k[0][s][1]), qv[s], a0);
+        a1 = mfma16x16x32(mla_i8x8(k[1][s][0], k[1][s][1]), qv[s], a1);
       } else {
-        a0 = mfma16x16x32(t.k[0][s], qv[s], a0);
-        a1 = mfma16x16x32(t.k[1][s], qv[s], a1);
+        a0 = mfma16x16x32(k[0][s], qv[s], a0);
+        a1 = mfma16x16x32(k[1][s], qv[s], a1);
       }
     }
     float part_s[8];
@@ -180,34 +202,33 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
     }
     if constexpr (C8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) part_s[j] *= t.sk[j];
+      for (int j = 0; j < 8; ++j) part_s[j] *= sk[j];
     }
     if (w < 2) {
-      f32x4 r0 = mfma16x16x32(t.k[0][4], qv[4], f32x4{0, 0, 0, 0});
-      f32x4 r1 = mfma16x16x32(t.k[1][4], qv[4], f32x4{0, 0, 0, 0});
+      f32x4 r0 = mfma16x16x32(k[0][4], qv[4], f32x4{0, 0, 0, 0});
+      f32x4 r1 = mfma16x16x32(k[1][4], qv[4], f32x4{0, 0, 0, 0});
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         part_s[r] += r0[r];
         part_s[4 + r] += r1[r];
       }
     }
-    // Sum the four waves' partial scores.
-    float(*slot)[64][8] = xbuf[parity];
-    *reinterpret_cast<f32x4 *>(&slot[w][lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
-    *reinterpret_cast<f32x4 *>(&slot[w][lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
+    // Sum the four waves' partial scores. The buffer is free again: every wave
+    // finished reading it before the barrier that starts this tile.
+    *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
+    *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
     __syncthreads();
     float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int v = 0; v < kMlaWaves; ++v) {
-      const f32x4 lo = *reinterpret_cast<const f32x4 *>(&slot[v][lane][0]);
-      const f32x4 hi = *reinterpret_cast<const f32x4 *>(&slot[v][lane][4]);
+    for (int u = 0; u < kMlaWaves; ++u) {
+      const f32x4 lo = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][0]);
+      const f32x4 hi = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][4]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         x[r] += lo[r];
         x[4 + r] += hi[r];
       }
     }
-    parity ^= 1;
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= p.scale_log2;
     if (t_end - t0 < kMlaTile) {
@@ -233,7 +254,7 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
     l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     if constexpr (C8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] *= t.sk[j];
+      for (int j = 0; j < 8; ++j) pr[j] *= sk[j];
     }
     const u32x4 pb = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
                       pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
@@ -242,41 +263,38 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
       u32x4 a;
       if constexpr (C8) {
         const int wd = b >> 2, y = b & 3;
-        a = u32x4{mla_i8pair(mla_i8(t.v[0][wd], y), mla_i8(t.v[1][wd], y)),
-                  mla_i8pair(mla_i8(t.v[2][wd], y), mla_i8(t.v[3][wd], y)),
-                  mla_i8pair(mla_i8(t.v[4][wd], y), mla_i8(t.v[5][wd], y)),
-                  mla_i8pair(mla_i8(t.v[6][wd], y), mla_i8(t.v[7][wd], y))};
+        a = u32x4{mla_i8pair(mla_i8(v[0][wd], y), mla_i8(v[1][wd], y)),
+                  mla_i8pair(mla_i8(v[2][wd], y), mla_i8(v[3][wd], y)),
+                  mla_i8pair(mla_i8(v[4][wd], y), mla_i8(v[5][wd], y)),
+                  mla_i8pair(mla_i8(v[6][wd], y), mla_i8(v[7][wd], y))};
       } else {
         const int wd = b >> 1;
         if (b & 1)
-          a = u32x4{pack_hi16(t.v[0][wd], t.v[1][wd]), pack_hi16(t.v[2][wd], t.v[3][wd]),
-                    pack_hi16(t.v[4][wd], t.v[5][wd]), pack_hi16(t.v[6][wd], t.v[7][wd])};
+          a = u32x4{pack_hi16(v[0][wd], v[1][wd]), pack_hi16(v[2][wd], v[3][wd]),
+                    pack_hi16(v[4][wd], v[5][wd]), pack_hi16(v[6][wd], v[7][wd])};
         else
-          a = u32x4{pack_lo16(t.v[0][wd], t.v[1][wd]), pack_lo16(t.v[2][wd], t.v[3][wd]),
-                    pack_lo16(t.v[4][wd], t.v[5][wd]), pack_lo16(t.v[6][wd], t.v[7][wd])};
+          a = u32x4{pack_lo16(v[0][wd], v[1][wd]), pack_lo16(v[2][wd], v[3][wd]),
+                    pack_lo16(v[4][wd], v[5][wd]), pack_lo16(v[6][wd], v[7][wd])};
       }
       oacc[b] = mfma16x16x32(a, pb, oacc[b]);
     }
   };
 
-  MlaTileRegs<C8> tr[kMlaStages];
-  auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (kMlaTile - 1)); };
+  // Ring: tile ti lives in slot ti % S. Tiles 0..S-2 are issued up front; the
+  // top of iteration ti waits for tile ti (S-2 newer tiles may stay in flight,
+  // fewer near the end), then a barrier both publishes it and retires every
+  // wave's reads of tile ti-1, whose slot receives tile ti+S-1.
 #pragma unroll
-  for (int i = 0; i < kMlaStages - 1; ++i)
-    mla_load_tile<C8>(tr[i], p, cache, lane_blocks, t_begin, clamp_tile(t_begin + i * kMlaTile),
-                      t_end, w, o);
-  int t0 = t_begin;
-  while (true) {
-#pragma unroll
-    for (int i = 0; i < kMlaStages; ++i) {
-      mla_load_tile<C8>(tr[(i + kMlaStages - 1) % kMlaStages], p, cache, lane_blocks, t_begin,
-                        clamp_tile(t0 + (kMlaStages - 1) * kMlaTile), t_end, w, o);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(tr[i], t0);
-      t0 += kMlaTile;
-      if (t0 >= t_end) break;
-    }
-    if (t0 >= t_end) break;
+  for (int i = 0; i < S - 1; ++i)
+    if (i < n_tiles) issue(i);
+  for (int ti = 0; ti < n_tiles; ++ti) {
+    if (ti + S - 2 < n_tiles)
+      lds_dma_wait<(S - 2) * R::NI>();
+    else
+      lds_dma_wait<0>();
+    __syncthreads();
+    if (ti + S - 1 < n_tiles) issue(ti + S - 1);
+    compute(ring + (ti % S) * R::SLOT, t_begin + ti * kMlaTile);
   }
 
   float l_tot = wave_sum_xor(l_run, 16);
@@ -313,7 +331,8 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
 template <bool C8>
 __global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_decode_kernel(DecodeParams p) {
   __shared__ int item_slot;
-  __shared__ __align__(16) float xbuf[2][kMlaWaves][64][8];
+  __shared__ __align__(16) uint8_t ring[kMlaLds];
+  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
   const uint8_t *cache = p.k_cache;
@@ -325,7 +344,7 @@ __global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_decode_kernel(DecodePar
     if (it >= p.queue[1]) break;
     const uint32_t e = uniform(p.items[it]);
     const int seq = int(e >> 12);
-    mla_item<C8>(p, cache, xbuf, seq, int(e & 0xfffu), w, lane);
+    mla_item<C8>(p, cache, ring, xbuf, seq, int(e & 0xfffu), w, lane);
   }
 }
 
@@ -375,9 +394,9 @@ int32_t mla_common(bool c8, const void *q, const void *cache, const int32_t *blo
   hipStream_t s = static_cast<hipStream_t>(stream);
   launch_prologue(p, RowWrite{}, s);
   if (c8)
-    mla_decode_kernel<true><<<device_cus() * 2, 64 * kMlaWaves, 0, s>>>(p);
+    mla_decode_kernel<true><<<device_cus(), 64 * kMlaWaves, 0, s>>>(p);
   else
-    mla_decode_kernel<false><<<device_cus() * 2, 64 * kMlaWaves, 0, s>>>(p);
+    mla_decode_kernel<false><<<device_cus(), 64 * kMlaWaves, 0, s>>>(p);
   launch_merge<512>(p, s);
   return launch_status("mla decode");
 }

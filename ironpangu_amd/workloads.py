@@ -214,9 +214,12 @@ class MlaCase:
 
 
 def mla_meta(seed=0, num_seqs=128, lo=1024, hi=65536, dist="loguniform", heads=16, block_size=64,
-             pool_blocks=None, c8=False) -> MlaCase:
+             pool_blocks=None, c8=False, fixed=None) -> MlaCase:
+    """``fixed`` maps sequence index -> length, overriding the drawn ones."""
     rng = np.random.default_rng(seed)
     lens = lengths(rng, num_seqs, lo, hi, dist)
+    for i, n in (fixed or {}).items():
+        lens[i] = n
     stride = (hi + block_size - 1) // block_size
     need = int(((lens.astype(np.int64) + block_size - 1) // block_size).sum())
     pool = int(pool_blocks or need + 64)

@@ -11,14 +11,13 @@ from ironpangu_amd import workloads as W
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("heads,c8", [(16, False), (16, True), (6, False), (6, True)])
-def test_mla_decode(heads, c8):
+@pytest.mark.parametrize("heads,c8,bs", [(16, False, 64), (16, True, 64), (6, False, 32),
+                                         (6, True, 128), (16, False, 256), (16, True, 32)])
+def test_mla_decode(heads, c8, bs):
     import torch
     from ironpangu_amd import ops
-    case = W.mla_host_case(3, num_seqs=5, lo=1, hi=5000, dist="loguniform", heads=heads,
-                           block_size=64)
-    case.seq_lens[0] = 1
-    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(5), 64)
+    case = W.mla_host_case(3, num_seqs=6, lo=1, hi=5000, dist="loguniform", heads=heads,
+                           block_size=bs, fixed={0: 1, 1: 4096, 2: 31, 3: 2049})
     h = case.host
     nb, bs = case.pool_blocks, case.block_size
     pool = h["pool"].copy()
