@@ -75,10 +75,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // reads the bytes, and must not let such a load target bytes a wave may still
 // be reading.
 __device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(rsrc), "s"(lds_base)
-               : "memory", "m0");
+               : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
+               : "memory");
 }
 template <int N>
 __device__ __forceinline__ void lds_dma_wait() {

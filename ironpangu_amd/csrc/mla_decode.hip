@@ -35,7 +35,16 @@ struct MlaRow {
   // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16) / 1312 (C8) 16-byte chunks.
   static constexpr int NI = C8 ? 6 : 9;
   static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
-  static constexpr int STAGES = C8 ? 6 : 4;
+#ifndef IFATTN_MLA_C8_STAGES
+#define IFATTN_MLA_C8_STAGES 6
+#endif
+#ifndef IFATTN_MLA_WGS
+#define IFATTN_MLA_WGS 1
+#endif
+#ifndef IFATTN_MLA_BF16_STAGES
+#define IFATTN_MLA_BF16_STAGES 4
+#endif
+  static constexpr int STAGES = C8 ? IFATTN_MLA_C8_STAGES : IFATTN_MLA_BF16_STAGES;
   // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B, a multiple of
   // 128) XOR the chunk index with the row's low 3 bits so the 16 rows that one
   // K read touches spread over the banks; C8 rows (656 B) are not swizzled.
@@ -292,9 +301,13 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
       lds_dma_wait<(S - 2) * R::NI>();
     else
       lds_dma_wait<0>();
+#ifndef IFATTN_EXP_NOBARRIER
     __syncthreads();
+#endif
     if (ti + S - 1 < n_tiles) issue(ti + S - 1);
+#ifndef IFATTN_EXP_NOCOMPUTE
     compute(ring + (ti % S) * R::SLOT, t_begin + ti * kMlaTile);
+#endif
   }
 
   float l_tot = wave_sum_xor(l_run, 16);
@@ -329,17 +342,19 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
 }
 
 template <bool C8>
-__global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_decode_kernel(DecodeParams p) {
-  __shared__ int item_slot;
+__global__ __launch_bounds__(64 * kMlaWaves, IFATTN_MLA_WGS) void mla_decode_kernel(DecodeParams p) {
   __shared__ __align__(16) uint8_t ring[kMlaLds];
   __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
+  // The item index travels through the score buffer, idle between items.
+  int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
   const uint8_t *cache = p.k_cache;
   while (true) {
-    if (threadIdx.x == 0) item_slot = atomicAdd(p.queue, 1);
     __syncthreads();
-    const int it = uniform(item_slot);
+    if (threadIdx.x == 0) *item_slot = atomicAdd(p.queue, 1);
+    __syncthreads();
+    const int it = uniform(*item_slot);
     __syncthreads();
     if (it >= p.queue[1]) break;
     const uint32_t e = uniform(p.items[it]);
@@ -394,9 +409,9 @@ int32_t mla_common(bool c8, const void *q, const void *cache, const int32_t *blo
   hipStream_t s = static_cast<hipStream_t>(stream);
   launch_prologue(p, RowWrite{}, s);
   if (c8)
-    mla_decode_kernel<true><<<device_cus(), 64 * kMlaWaves, 0, s>>>(p);
+    mla_decode_kernel<true><<<device_cus() * IFATTN_MLA_WGS, 64 * kMlaWaves, 0, s>>>(p);
   else
-    mla_decode_kernel<false><<<device_cus(), 64 * kMlaWaves, 0, s>>>(p);
+    mla_decode_kernel<false><<<device_cus() * IFATTN_MLA_WGS, 64 * kMlaWaves, 0, s>>>(p);
   launch_merge<512>(p, s);
   return launch_status("mla decode");
 }

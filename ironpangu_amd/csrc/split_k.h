@@ -160,12 +160,21 @@ template <int D, int DW>
 __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h, int nparts,
                                            int dim0, int lane) {
   constexpr int V = DW / 64;
-  constexpr int kFast = 32;
-  const int64_t row0 = int64_t(seq) * p.max_parts * p.q_heads + h;
-  const int64_t pstride = p.q_heads;
-  const int d = dim0 + lane * V;
+  constexpr int kFast = 16;
+  // This sequence's partials: partition k, head h is row k * q_heads + h.
+  // Buffer offsets stay 32-bit and rows past nparts read as zero.
+  const int64_t seq_row = int64_t(seq) * p.max_parts * p.q_heads;
+  const uint32_t rows = uint32_t(nparts) * uint32_t(p.q_heads);
+  const auto ro = make_rsrc(p.part_o + seq_row * D, rows * D * 4u);
+  const auto rm = make_rsrc(p.part_ml + seq_row * 2, rows * 8u);
+  const uint32_t ostride = uint32_t(p.q_heads) * D * 4u;
+  const uint32_t obase = (uint32_t(h) * D + uint32_t(dim0 + lane * V)) * 4u;
+  auto load_ml = [&](int k) {
+    const uint32_t off = (uint32_t(k) * p.q_heads + h) * 8u;
+    return make_float2(buf_load_f32(rm, off), buf_load_f32(rm, off + 4));
+  };
   float mmax = -INFINITY;
-  for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, p.part_ml[(row0 + k * pstride) * 2]);
+  for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, load_ml(k).x);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
   float lsum = 0.0f;
@@ -174,14 +183,19 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   for (int k0 = 0; k0 < nparts; k0 += kFast) {
     const int n = nparts - k0 < kFast ? nparts - k0 : kFast;
-    float2 ml = make_float2(-INFINITY, 0.0f);
-    if (lane < n) ml = *reinterpret_cast<const float2 *>(p.part_ml + (row0 + (k0 + lane) * pstride) * 2);
+    const float2 ml = lane < n ? load_ml(k0 + lane) : make_float2(-INFINITY, 0.0f);
     float o[kFast][V];
 #pragma unroll
-    for (int u = 0; u < kFast; ++u)
-#pragma unroll
-      for (int i = 0; i < V; ++i)
-        o[u][i] = u < n ? p.part_o[(row0 + int64_t(k0 + u) * pstride) * D + d + i] : 0.0f;
+    for (int u = 0; u < kFast; ++u) {
+      const uint32_t off = obase + uint32_t(k0 + u) * ostride;
+      if constexpr (V == 2) {
+        const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ro, off, 0, 0));
+        o[u][0] = __uint_as_float(x[0]);
+        o[u][1] = __uint_as_float(x[1]);
+      } else {
+        o[u][0] = buf_load_f32(ro, off);
+      }
+    }
     const float w = lane < n ? fast_exp2(ml.x - mmax) : 0.0f;
     lsum += w * ml.y;
 #pragma unroll
@@ -194,13 +208,11 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) lsum = wave_sum_xor(lsum, m);
   const float inv = 1.0f / lsum;
-  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + d;
+  uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + h) * D + dim0 + lane * V;
   if constexpr (V == 1) {
     op[0] = uint16_t(f32_to_bf16_bits(acc[0] * inv));
   } else {
-#pragma unroll
-    for (int i = 0; i < V; i += 2)
-      *reinterpret_cast<uint32_t *>(op + i) = pack_bf16x2(acc[i] * inv, acc[i + 1] * inv);
+    *reinterpret_cast<uint32_t *>(op) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
   }
 }
 
