@@ -78,6 +78,24 @@ int32_t ifattn_mla_cache_write_c8(const void *rows, void *cache, const void *slo
                                   int32_t slot_dtype, int64_t rows_count, int64_t num_slots,
                                   void *stream);
 
+/* Fused MLA cache writer: for each of `rows` (1..4096) rows x [rows, 576] bf16
+ * (512 latent + 64 rope): y = x[0:512] * rsqrt(mean(x[0:512]^2) + eps) * gamma,
+ * rope[d] = bf16(x[512+d]*cos[r,d] + (d < 32 ? -x[544+d] : x[480+d])*sin[r,d]),
+ * stored at cache row slot_mapping[r] as either a bf16 576-wide row
+ * {bf16(y), rope} (packed = 0) or the packed C8 656-byte row
+ * {int8 y/scale[t], rope, f32 scale[4]} (packed = 1; scale = tile max/127, 0
+ * for a zero tile, nearest-even codes). gamma [512] bf16, cos/sin [rows, 64]
+ * bf16. Slots < 0 or >= num_slots are skipped. fp32 arithmetic in a fixed
+ * order (bit-identical to the CPU oracle).
+ * Replaces aclnnAiInfraKvRmsNormRopeCache (mode "PA", rotary "half", quant
+ * "pertile128"/"none") behind resident::normalized_cache_append
+ * (native/src/resident_cache_writer.h:5-20); acceptance rules
+ * native/probes/prefill_cache_writer_probe.cpp:38-61. */
+int32_t ifattn_mla_norm_rope_cache_write(const void *x, const void *gamma, const void *cos,
+                                         const void *sin, const void *slot_mapping,
+                                         int32_t slot_dtype, int64_t rows, float eps, void *cache,
+                                         int32_t packed, int64_t num_slots, void *stream);
+
 /* ---- paged decode (one query row per sequence) --------------------------------- */
 
 /* Workspace bytes for the split-K partials of the decode kernels. */

@@ -85,6 +85,11 @@ typedef const IFKernelV1 *(*IFKernelEntryV1)(uint32_t requested_version);
  *       q, cache I8 [blocks, block_size, 656], block_tables, seq_lens ; out
  *   libifk_mla_cache_write_c8    "inferfabric.mla_cache_write.c8.v2"
  *       rows bf16 [rows, 576], slot_mapping ; cache I8 [blocks, block_size, 656] (access 3)
+ *   libifk_mla_norm_rope_cache_bf16 "inferfabric.mla_norm_rope_cache.bf16.v2"
+ *       x bf16 [rows <= 4096, 576], gamma bf16 [512], cos, sin bf16 [rows, 64], slot_mapping ;
+ *       cache bf16 [blocks, block_size, 576] (access 3); eps 1e-5
+ *   libifk_mla_norm_rope_cache_c8   "inferfabric.mla_norm_rope_cache.c8.v2"
+ *       same inputs ; cache I8 [blocks, block_size, 656] (access 3)
  * max_context is entries * block_size of the block-table descriptor.
  */
 

@@ -35,6 +35,7 @@ SIGNATURES = {
     "ifattn_kv_cache_write": (i32, [vp, vp, vp, vp, vp, i32, i64, i64, i64, vp]),
     "ifattn_kv_cache_write_c8": (i32, [vp, vp, vp, vp, vp, vp, vp, i32, i64, i32, i32, i64, vp]),
     "ifattn_mla_cache_write_c8": (i32, [vp, vp, vp, i32, i64, i64, vp]),
+    "ifattn_mla_norm_rope_cache_write": (i32, [vp, vp, vp, vp, vp, i32, i64, f32, vp, i32, i64, vp]),
     "ifattn_paged_decode_workspace_size": (u64, [i32, i32, i32, i32]),
     "ifattn_paged_decode_bf16": (i32, [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i64,
                                        i32, f32, vp, u64, vp]),

@@ -40,6 +40,8 @@ PLUGINS = {
     "mla_decode_bf16": 5,
     "mla_decode_c8": 6,
     "mla_cache_write_c8": 7,
+    "mla_norm_rope_cache_bf16": 8,
+    "mla_norm_rope_cache_c8": 9,
 }
 
 

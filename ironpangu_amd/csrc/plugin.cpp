@@ -23,6 +23,8 @@ enum Op : int {
   kMlaBf16,
   kMlaC8,
   kMlaWriteC8,
+  kMlaNormRopeBf16,
+  kMlaNormRopeC8,
   kOpCount
 };
 
@@ -31,6 +33,7 @@ const char *const kContract[kOpCount] = {
     "inferfabric.paged_decode.gqa.bf16.v2", "inferfabric.paged_decode.gqa.c8.v2",
     "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
     "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
+    "inferfabric.mla_norm_rope_cache.bf16.v2", "inferfabric.mla_norm_rope_cache.c8.v2",
 };
 constexpr const char *kTarget = "gfx950";
 
@@ -243,6 +246,26 @@ void prepare_op(State &s, const IFKernelTensorV1 *in, uint32_t nin, const IFKern
       s.num_slots = out[0].shape[0] * out[0].shape[1];
       return;
     }
+    case kMlaNormRopeBf16:
+    case kMlaNormRopeC8: {
+      const bool c8 = s.op == kMlaNormRopeC8;
+      require(nin == 5 && nout == 1, "mla norm/rope write: 5 inputs, 1 output");
+      check_tensor(in[0], BF, R, 2);
+      require(in[0].shape[1] == 576, "x must be [rows, 576]");
+      s.rows = in[0].shape[0];
+      require(s.rows >= 1 && s.rows <= 4096, "rows must be 1..4096");
+      check_tensor(in[1], BF, R, 1);
+      require(in[1].shape[0] == 512, "gamma must be [512]");
+      check_tensor(in[2], BF, R, 2);
+      check_tensor(in[3], BF, R, 2);
+      require(in[2].shape[0] == s.rows && in[2].shape[1] == 64 && same_shape(in[2], in[3]),
+              "cos/sin must be [rows, 64]");
+      check_slots(in[4], s.rows, s);
+      check_tensor(out[0], c8 ? I8 : BF, RW, 3);
+      require(out[0].shape[2] == (c8 ? 656 : 576), "cache rows: 576 bf16 or 656 bytes");
+      s.num_slots = out[0].shape[0] * out[0].shape[1];
+      return;
+    }
     default:
       require(false, "unknown operator");
   }
@@ -318,6 +341,13 @@ int32_t enqueue(void *state, void *workspace, uint64_t bytes, void *stream) {
     case kMlaWriteC8:
       return ifattn_mla_cache_write_c8(in[0].data, out[0].data, in[1].data, s->slot_dtype, s->rows,
                                        s->num_slots, stream);
+    case kMlaNormRopeBf16:
+    case kMlaNormRopeC8:
+      // eps 1e-5: the epsilon the reference passes (resident_cache_writer.h:16).
+      return ifattn_mla_norm_rope_cache_write(in[0].data, in[1].data, in[2].data, in[3].data,
+                                              in[4].data, s->slot_dtype, s->rows, 1e-5f,
+                                              out[0].data, s->op == kMlaNormRopeC8 ? 1 : 0,
+                                              s->num_slots, stream);
     default:
       return ifattn::fail(IFATTN_EINVAL, "enqueue: unknown operator");
   }
@@ -330,8 +360,8 @@ IFKernelV1 table() {
   return IFKernelV1{sizeof(IFKernelV1), 2, kContract[OP], kTarget, &prepare<OP>, &enqueue, &release};
 }
 
-const IFKernelV1 kTables[kOpCount] = {table<0>(), table<1>(), table<2>(), table<3>(),
-                                      table<4>(), table<5>(), table<6>(), table<7>()};
+const IFKernelV1 kTables[kOpCount] = {table<0>(), table<1>(), table<2>(), table<3>(), table<4>(),
+                                      table<5>(), table<6>(), table<7>(), table<8>(), table<9>()};
 
 }  // namespace
 

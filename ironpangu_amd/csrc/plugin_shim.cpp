@@ -13,6 +13,7 @@ const char *const kContracts[] = {
     "inferfabric.paged_decode.gqa.bf16.v2", "inferfabric.paged_decode.gqa.c8.v2",
     "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
     "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
+    "inferfabric.mla_norm_rope_cache.bf16.v2", "inferfabric.mla_norm_rope_cache.c8.v2",
 };
 }
 

@@ -111,6 +111,33 @@ def mla_cache_write_c8(rows, cache, slot_mapping, stream=None):
           "ifattn_mla_cache_write_c8")
 
 
+def mla_norm_rope_cache_write(x, gamma, cos, sin, cache, slot_mapping, eps=1e-5, stream=None):
+    """Fused RMSNorm(512) * gamma + half rotary(64) + cache store of bf16 x [rows, 576].
+
+    cache: bf16 [blocks, block_size, 576] (bf16 rows) or uint8 [blocks, block_size, 656]
+    (packed C8 rows); gamma [512] bf16; cos/sin [rows, 64] bf16; rows 1..4096.
+    """
+    _dev(x, gamma, cos, sin, cache, slot_mapping)
+    _req(x.dtype == torch.bfloat16 and x.dim() == 2 and x.shape[1] == 576, "x: bf16 [rows, 576]")
+    rows = x.shape[0]
+    _req(gamma.dtype == torch.bfloat16 and gamma.numel() == 512, "gamma: bf16 [512]")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _req(t.dtype == torch.bfloat16 and tuple(t.shape) == (rows, 64), f"{n}: bf16 [rows, 64]")
+    _req(cache.dim() == 3, "cache: [blocks, block_size, row]")
+    if cache.dtype == torch.uint8:
+        _req(cache.shape[2] == 656, "packed cache rows are 656 bytes")
+        packed = 1
+    else:
+        _req(cache.dtype == torch.bfloat16 and cache.shape[2] == 576, "bf16 cache rows are 576 wide")
+        packed = 0
+    _req(slot_mapping.numel() == rows, "one slot per row")
+    check(lib().ifattn_mla_norm_rope_cache_write(_ptr(x), _ptr(gamma), _ptr(cos), _ptr(sin),
+                                                 _ptr(slot_mapping), _slot_dtype(slot_mapping),
+                                                 rows, float(eps), _ptr(cache), packed,
+                                                 cache.shape[0] * cache.shape[1], _stream(stream)),
+          "ifattn_mla_norm_rope_cache_write")
+
+
 # ---------------------------------------------------------------- decode
 
 def decode_workspace(num_seqs, q_heads, head_dim, max_context, device="cuda"):

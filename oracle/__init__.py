@@ -38,6 +38,7 @@ def lib():
         l.oracle_quant_legacy.argtypes = [vp, i32, i32, vp, vp]
         l.oracle_dequant_legacy.argtypes = [vp, vp, vp, i64, i32, i32, i32]
         l.oracle_mla_pack_c8.argtypes = [vp, i64, vp]
+        l.oracle_mla_norm_rope_write.argtypes = [vp, vp, vp, vp, vp, i64, f32, vp, i32, i64]
         l.oracle_paged_decode.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, i32,
                                           i32, i32, f32, i32, i32]
         l.oracle_varlen_prefill.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32,
@@ -45,7 +46,8 @@ def lib():
         l.oracle_mla_decode.argtypes = [vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, f32, i32]
         l.oracle_hardware_threads.restype = i32
         for f in ("oracle_kv_write", "oracle_quant_rows", "oracle_quant_legacy",
-                  "oracle_dequant_legacy", "oracle_mla_pack_c8", "oracle_paged_decode",
+                  "oracle_dequant_legacy", "oracle_mla_pack_c8", "oracle_mla_norm_rope_write",
+                  "oracle_paged_decode",
                   "oracle_varlen_prefill", "oracle_mla_decode"):
             getattr(l, f).restype = None
         _lib = l
@@ -118,6 +120,21 @@ def mla_pack_c8(rows_bits):
     out = np.zeros((rows.shape[0], 656), np.uint8)
     lib().oracle_mla_pack_c8(_p(rows), rows.shape[0], _p(out))
     return out
+
+
+def mla_norm_rope_write(x, gamma, cos, sin, slots, cache, packed, eps=1e-5):
+    """In place on ``cache`` (uint8 [slots, 656] if packed else uint16 [slots, 576]):
+    RMSNorm * gamma + half rotary + cache row for every row of x [rows, 576]."""
+    x = _c(x, np.uint16).reshape(-1, 576)
+    gamma = _c(gamma, np.uint16)
+    cos = _c(cos, np.uint16).reshape(-1, 64)
+    sin = _c(sin, np.uint16).reshape(-1, 64)
+    slots = _c(slots, np.int64)
+    assert cache.flags.c_contiguous
+    num_slots = cache.shape[0]
+    lib().oracle_mla_norm_rope_write(_p(x), _p(gamma), _p(cos), _p(sin), _p(slots), x.shape[0],
+                                     float(eps), _p(cache), int(bool(packed)), num_slots)
+    return cache
 
 
 def paged_decode(q, k_cache, v_cache, block_tables, seq_lens, q_heads, kv_heads, head_dim,

@@ -20,6 +20,9 @@
 //                          Pinned: probe vectors, tie cases, nibble layout.
 //   oracle_mla_pack_c8     656-byte row, docs/packed-mla-cache.md:27-43; oracle checks of
 //                          packed_cache_probe.cpp:24-45. Pinned: tile scale/quant/rope bits.
+//   oracle_mla_norm_rope_write  fused RMSNorm + half-rope + cache row, resident_cache_writer.h:5-20.
+//                          Pinned: prefill_cache_writer_probe.cpp:38-61 fixtures and
+//                          tolerances, double-precision restatement, exact rope bits.
 //   oracle_paged_decode    attention.rs:221-253 (GQA kh = h/group at :226) without the bf16
 //                          rounding of intermediates (fp32 contract), plus an optional
 //                          mode that keeps the Rust oracle's roundings. Pinned: closed
@@ -164,6 +167,77 @@ void oracle_mla_pack_c8(const uint16_t *rows, int64_t n, uint8_t *out) {
       std::memcpy(o + 640 + 4 * t, &s, 4);
     }
     std::memcpy(o + 512, x + 512, 128);
+  }
+}
+
+// Fused MLA cache writer: RMSNorm(512) * gamma, half rotary on the 64 rope
+// values, then the cache row (bf16 576-wide, or the packed C8 656-byte row with
+// per-128 tile scales). Follows resident_cache_writer.h:5-20 and the checks of
+// prefill_cache_writer_probe.cpp:38-61 (norm 1/sqrt(mean(x^2)+eps), scale =
+// tile max/127 with 0 for a zero tile, nearest-even codes, rope
+// bf16(a*cos + (d<32 ? -b : b)*sin) with b = x[512 + (d+32)%64]).
+// The fp32 operation order is fixed so that the device writer is bit-exact:
+// each of 64 lanes sums the squares of its 8 consecutive values in order, the
+// 64 lane sums are combined by a xor butterfly (masks 32..1), rstd =
+// 1/sqrt(sum/512 + eps), y = (x*rstd)*gamma, C8 codes quantize y (fp32, no
+// bf16 step). slots < 0 or >= num_slots are skipped.
+void oracle_mla_norm_rope_write(const uint16_t *x, const uint16_t *gamma, const uint16_t *cosv,
+                                const uint16_t *sinv, const int64_t *slots, int64_t rows,
+                                float eps, uint8_t *cache, int32_t packed, int64_t num_slots) {
+  const int64_t stride = packed ? 656 : 1152;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (slots[r] < 0 || slots[r] >= num_slots) continue;
+    const uint16_t *in = x + r * 576;
+    uint8_t *o = cache + slots[r] * stride;
+    float lane[64];
+    for (int l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        const float v = bf(in[8 * l + i]);
+        const float sq = v * v;
+        acc = acc + sq;
+      }
+      lane[l] = acc;
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+      float nxt[64];
+      for (int l = 0; l < 64; ++l) nxt[l] = lane[l] + lane[l ^ m];
+      std::memcpy(lane, nxt, sizeof(lane));
+    }
+    const float mean = lane[0] * (1.0f / 512.0f);
+    const float rstd = 1.0f / std::sqrt(mean + eps);
+    float y[512];
+    for (int d = 0; d < 512; ++d) {
+      const float t = bf(in[d]) * rstd;
+      y[d] = t * bf(gamma[d]);
+    }
+    if (packed) {
+      for (int t = 0; t < 4; ++t) {
+        float m = 0.0f;
+        for (int d = 128 * t; d < 128 * t + 128; ++d) m = std::max(m, std::fabs(y[d]));
+        const float scale = m == 0.0f ? 0.0f : m / 127.0f;
+        for (int d = 128 * t; d < 128 * t + 128; ++d) {
+          int q = 0;
+          if (scale != 0.0f) q = int(std::nearbyint(y[d] / scale));
+          o[d] = uint8_t(int8_t(std::max(-127, std::min(127, q))));
+        }
+        std::memcpy(o + 640 + 4 * t, &scale, 4);
+      }
+    } else {
+      for (int d = 0; d < 512; ++d) {
+        const uint16_t b = to_bf(y[d]);
+        std::memcpy(o + 2 * d, &b, 2);
+      }
+    }
+    uint8_t *rope = o + (packed ? 512 : 1024);
+    for (int d = 0; d < 64; ++d) {
+      const float a = bf(in[512 + d]), b = bf(in[512 + (d + 32) % 64]);
+      const float c = bf(cosv[r * 64 + d]), sn = bf(sinv[r * 64 + d]);
+      const float p0 = a * c;
+      const float p1 = (d < 32 ? -b : b) * sn;
+      const uint16_t v = to_bf(p0 + p1);
+      std::memcpy(rope + 2 * d, &v, 2);
+    }
   }
 }
 

@@ -177,3 +177,27 @@ def test_write_and_mla_prepare():
     k.release(p.state)
     ins[1] = tensor([32, 64, 576], 1, 1)
     assert _prepare(k, ins, outs)[0] != 0
+
+
+def test_norm_rope_write_prepare():
+    so, entry = load_plugin("mla_norm_rope_cache_c8")
+    k = entry(2).contents
+    assert k.contract == b"inferfabric.mla_norm_rope_cache.c8.v2"
+
+    def ports(rows=17, width=656, cache_dtype=1, cos_rows=None):
+        ins = [tensor([rows, 576], 2, 1), tensor([512], 2, 1),
+               tensor([cos_rows or rows, 64], 2, 1), tensor([cos_rows or rows, 64], 2, 1),
+               tensor([rows], 5, 1)]
+        return ins, [tensor([256, 32, width], cache_dtype, 3)]
+
+    st, p = _prepare(k, *ports())
+    assert st == 0 and p.state and p.workspace_bytes == 0
+    k.release(p.state)
+    assert _prepare(k, *ports(width=576))[0] != 0        # c8 rows are 656 bytes
+    assert _prepare(k, *ports(cos_rows=3))[0] != 0       # cos/sin per row
+    assert _prepare(k, *ports(rows=4097))[0] != 0        # the reference's 4096-row bound
+    so, entry = load_plugin("mla_norm_rope_cache_bf16")
+    k = entry(2).contents
+    st, p = _prepare(k, *ports(width=576, cache_dtype=2))
+    assert st == 0
+    k.release(p.state)
