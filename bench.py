@@ -241,7 +241,7 @@ def bench_mla(seed, steps, warmup):
     tables = torch.from_numpy(case.block_tables).to(dev)
     lens = torch.from_numpy(case.seq_lens).to(dev)
     slots = torch.from_numpy(case.slot_mapping.astype(np.int64)).to(dev)
-    ws = ops.mla_workspace(case.num_seqs, case.heads, case.max_context)
+    ws = ops.mla_workspace(case.num_seqs, case.heads, case.max_context, case.block_size)
     out = torch.empty((case.num_seqs, case.heads, 512), dtype=torch.bfloat16, device=dev)
 
     def attn():

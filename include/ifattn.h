@@ -167,11 +167,13 @@ int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache, const voi
 
 /* ---- packed MLA latent decode -------------------------------------------------- */
 
-uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads, int32_t max_context);
+uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads, int32_t max_context,
+                                          int32_t block_size);
 
 /* q [num_seqs, heads, 576] bf16 (512 absorbed latent + 64 rope); cache rows of
  * 576 bf16; s_j = scale * q.row_j, o = softmax(s) . row_j[0:512];
- * out [num_seqs, heads, 512] bf16. heads <= 16 per call.
+ * out [num_seqs, heads, 512] bf16. heads <= 16 per call; block_size a power of
+ * two >= 16 (bf16 rows) or >= 32 (C8 rows).
  * Replaces the BF16 latent attention (token_executor.h:863-906); CPU oracle
  * native/probes/sliding_window_probe.cpp:144-163 without sinks/window. */
 int32_t ifattn_mla_decode_bf16(const void *q, const void *cache, const int32_t *block_tables,
@@ -189,6 +191,53 @@ int32_t ifattn_mla_decode_c8(const void *q, const void *cache, const int32_t *bl
                              int32_t num_seqs, int32_t heads, int32_t block_size,
                              int64_t num_blocks, int32_t max_context, float scale,
                              void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* ---- packed-MLA attention over query rows (windows, sparse lists, sinks) ----- */
+
+/* Rows: sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) (NULL:
+ * one row per sequence, num_rows = num_seqs) and kv_lens[s] cached keys
+ * (writes precede queries); row t of a sequence with `count` rows sees
+ * causal = kv_len - count + t + 1 keys (openpangu_attention_metadata.h:20-22).
+ * Learned sink rows (keys [n_sinks, 576], values [n_sinks, 512] bf16,
+ * n_sinks <= 128) join every row's softmax. q [num_rows, heads, 576] bf16,
+ * out [num_rows, heads, 512] bf16, heads <= 16, scale multiplies q.k. */
+uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_t heads, int32_t max_context,
+                                             int32_t window, int32_t topk, int32_t n_sinks,
+                                             int32_t block_size);
+
+/* BF16 latent rows (576 wide) over the window of each row: positions
+ * [max(0, causal - window), causal) (window 0 = all) read through the block
+ * table, which may be a ring of physical pages (sliding_window_layout.h:9-33:
+ * only the window must be resident). Replaces aclnnAiInfraFusedInferAttentionSink
+ * (TND, pre_tokens = window - 1, next_tokens = 0, learned sinks) of
+ * token_executor.h:863-906 / resident_window_attention.h:17-31; CPU oracle
+ * native/probes/sliding_window_probe.cpp:144-163. */
+int32_t ifattn_mla_window_attention_bf16(const void *q, const void *cache,
+                                         const int32_t *block_tables, int32_t table_stride,
+                                         const int32_t *cu_seqlens_q, const int32_t *kv_lens,
+                                         int32_t num_seqs, int32_t num_rows, int32_t window,
+                                         const void *sink_keys, const void *sink_values,
+                                         int32_t n_sinks, void *out, int32_t heads,
+                                         int32_t block_size, int64_t num_blocks,
+                                         int32_t max_context, float scale, void *workspace,
+                                         uint64_t workspace_bytes, void *stream);
+
+/* Packed C8 rows (656 bytes) over each row's candidate list indices[row][0..topk):
+ * logical positions of its sequence, the first min(causal, topk) distinct and
+ * < causal, then -1 (openpangu_attention_metadata.h:10-37); -1 or out-of-table
+ * entries are skipped. The cache must be below 4 GiB (32-bit row offsets).
+ * Replaces aclnnAiInfraKvQuantSparseFlashAttention (quant modes 2, tile 128, rope
+ * 64, learned sinks; token_executor.h:841-852, docs/packed-mla-cache.md:50-60);
+ * CPU oracle native/probes/packed_cache_probe.cpp:47-66. */
+int32_t ifattn_mla_sparse_attention_c8(const void *q, const void *cache, const int32_t *indices,
+                                       int32_t topk, const int32_t *block_tables,
+                                       int32_t table_stride, const int32_t *cu_seqlens_q,
+                                       const int32_t *kv_lens, int32_t num_seqs, int32_t num_rows,
+                                       const void *sink_keys, const void *sink_values,
+                                       int32_t n_sinks, void *out, int32_t heads,
+                                       int32_t block_size, int64_t num_blocks,
+                                       int32_t max_context, float scale, void *workspace,
+                                       uint64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

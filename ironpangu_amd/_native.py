@@ -46,11 +46,16 @@ SIGNATURES = {
     "ifattn_varlen_prefill_workspace_size": (u64, [i32, i32, i32, i32, i32]),
     "ifattn_varlen_prefill_bf16": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32,
                                          i32, i32, i32, i64, f32, vp, u64, vp]),
-    "ifattn_mla_decode_workspace_size": (u64, [i32, i32, i32]),
+    "ifattn_mla_decode_workspace_size": (u64, [i32, i32, i32, i32]),
     "ifattn_mla_decode_bf16": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, i64, i32, f32, vp,
                                      u64, vp]),
     "ifattn_mla_decode_c8": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, i64, i32, f32, vp, u64,
                                    vp]),
+    "ifattn_mla_attention_workspace_size": (u64, [i32, i32, i32, i32, i32, i32, i32]),
+    "ifattn_mla_window_attention_bf16": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, vp, i32,
+                                               vp, i32, i32, i64, i32, f32, vp, u64, vp]),
+    "ifattn_mla_sparse_attention_c8": (i32, [vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, vp, vp,
+                                             i32, vp, i32, i32, i64, i32, f32, vp, u64, vp]),
     "if_cache_quantize": (None, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "if_cache_dequantize": (None, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "if_packed_attention_metadata": (None, [vp, vp, vp, u32, vp]),

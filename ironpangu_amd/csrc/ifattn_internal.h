@@ -8,6 +8,8 @@
 
 namespace ifattn {
 int32_t fail(int32_t code, const char *message);
+// Message "<what>: <message>".
+int32_t fail(int32_t code, const char *what, const char *message);
 int32_t launch_status(const char *what);
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }

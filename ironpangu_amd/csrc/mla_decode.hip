@@ -1,25 +1,37 @@
-// Packed-MLA latent-cache decode for gfx950 (bf16 rows and packed C8 rows).
+// Packed-MLA latent-cache attention for gfx950 (bf16 rows and packed C8 rows).
 //
-// Per sequence b and head h (all heads share one cache row per token):
-//   s_j = scale * q[b,h,0:576] . row_j[0:576]
-//   out[b,h] = sum_j softmax(s)_j * row_j[0:512]
-// fp32 accumulation. This is the latent attention of the reference's MLA
-// decoder (native/src/token_executor.h:841-906) whose CPU oracles are
-// native/probes/packed_cache_probe.cpp:47-66 (C8) and
-// native/probes/sliding_window_probe.cpp:144-163 (bf16), here without learned
-// sinks or a window. C8 rows are {int8 latent[512], bf16 rope[64], f32 scale[4]}
-// (docs/packed-mla-cache.md:27-43); latent d dequantizes as int8 * scale[d/128]
-// (packed_cache_probe.cpp:57).
+// For each query row r and head h (all heads share one cache row per key):
+//   s_j = scale * q[r,h,0:576] . key_j[0:576]
+//   out[r,h] = sum_j softmax(s)_j * key_j[0:512]
+// over the row's keys plus optional learned sink rows, fp32 accumulation. This
+// is the latent attention of the reference's MLA decoder
+// (native/src/token_executor.h:841-906): the BF16 window attention with sinks
+// whose CPU oracle is native/probes/sliding_window_probe.cpp:144-163, and the
+// packed C8 sparse attention with sinks whose CPU oracle is
+// native/probes/packed_cache_probe.cpp:47-66. C8 rows are {int8 latent[512],
+// bf16 rope[64], f32 scale[4]} (docs/packed-mla-cache.md:27-43); latent d
+// dequantizes as int8 * scale[d/128] (packed_cache_probe.cpp:57).
 //
-// Decomposition: a workgroup of four waves owns a (sequence, partition) item
-// from the shared split-K queue. Wave w owns latent dims [128w, 128w+128) for
-// both QK^T and PV (K and V are the same bytes), waves 0 and 1 also take one
-// 32-dim step of the rope part. Partial 32-token score tiles are summed across
-// the waves through LDS (double-buffered, one barrier per tile); every wave then
-// runs the same online softmax. With C8 the wave's 128 dims are exactly one
-// scale tile, so the per-token tile scale multiplies the wave's partial score
-// and is folded into its probabilities for PV — dequantization stays in
-// registers. MFMA 16x16x32 bf16 with all 16 heads in the N dimension.
+// Keys of a row: rows are packed per sequence (cu_seqlens_q; one row per
+// sequence in plain decode). Row t of a sequence with `count` rows and kv_len
+// cached keys sees causal = kv_len - count + t + 1 keys
+// (openpangu_attention_metadata.h:20-22). Dense rows read positions
+// [max(0, causal - window), causal) through the block table (window 0 = all);
+// sparse rows read the logical positions of their index list
+// (min(causal, topk) candidates, -1 padding; openpangu_attention_metadata.h:13-33).
+//
+// Decomposition: a persistent workgroup of four waves takes (row, partition)
+// items from a device-built queue. A partition's 32-token tiles are copied
+// HBM -> LDS once by direct-to-LDS loads (dense: 32 consecutive rows of one
+// block; sparse: a gather of 32 rows named by the index list) through a ring
+// of slots; wave w then owns latent dims [128w, 128w+128) for QK^T and PV (K
+// and V are the same bytes) and waves 0 and 1 one 32-dim step of the rope part.
+// Partial score tiles are summed across the waves through LDS, every wave runs
+// the same online softmax. With C8 the wave's 128 dims are exactly one scale
+// tile, so the per-token tile scale multiplies the wave's partial score and is
+// folded into its probabilities for PV. MFMA 16x16x32 bf16 with the heads in
+// the N dimension. Rows split over several partitions, and rows with sinks,
+// write (m, l, O) partials; a merge kernel adds the sink rows and combines.
 #include "common.h"
 #include "ifattn_internal.h"
 #include "split_k.h"
@@ -28,23 +40,163 @@ namespace ifattn {
 
 constexpr int kMlaWaves = 4;
 constexpr int kMlaTile = 32;
+constexpr int kSparsePart = 1024;  // index-list entries per sparse partition
+constexpr int kMaxSinks = 128;
+
+struct MlaParams {
+  const uint16_t *q;            // [rows, heads, 576]
+  const uint8_t *cache;         // key rows of 1152 (bf16) or 656 (C8) bytes
+  const int32_t *block_tables;  // [seqs, table_stride]
+  const int32_t *kv_lens;       // [seqs] cached keys after this step's writes
+  const int32_t *cu_q;          // [seqs + 1] query rows per sequence; null: one row each
+  const int32_t *indices;       // [rows, topk] logical key positions (-1 pads); null: dense
+  const uint16_t *sink_k;       // [n_sinks, 576] bf16 or null
+  const uint16_t *sink_v;       // [n_sinks, 512] bf16
+  uint16_t *out;                // [rows, heads, 512]
+  int32_t *queue;               // [0] next item (atomic), [1] item count
+  uint32_t *items;              // (row << 12 | partition)
+  int32_t *row_seq;             // [rows] sequence of each row (plan output)
+  float *part_o;                // [rows, parts_per_row, heads, 512]
+  float *part_ml;               // [rows, parts_per_row, heads, 2]
+  int64_t num_blocks;
+  uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
+  int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks,
+      part_tokens, parts_per_row;
+  float scale_log2;
+};
+
+// Keys of one row: [lo, hi) are positions (dense) or index-list slots
+// (sparse); partitions of part_tokens start at `base` (lo rounded down to a
+// tile), so every tile is 32-aligned and never straddles a block.
+struct MlaSpan {
+  int seq, lo, hi, base;
+};
+
+__device__ __forceinline__ int mla_seq_of(const MlaParams &p, int row) {
+  if (!p.cu_q) return row;
+  int a = 0, b = p.num_seqs - 1;  // last sequence whose first row is <= row
+  while (a < b) {
+    const int m = (a + b + 1) >> 1;
+    if (p.cu_q[m] <= row) a = m; else b = m - 1;
+  }
+  return a;
+}
+
+__device__ __forceinline__ MlaSpan mla_span(const MlaParams &p, int row, int seq) {
+  const int start = p.cu_q ? p.cu_q[seq] : row;
+  const int count = p.cu_q ? p.cu_q[seq + 1] - start : 1;
+  int kv = p.kv_lens[seq];
+  kv = kv > p.max_context ? p.max_context : kv;
+  int causal = kv - count + (row - start) + 1;
+  causal = causal < 0 ? 0 : (causal > p.max_context ? p.max_context : causal);
+  MlaSpan s;
+  s.seq = seq;
+  if (p.indices) {
+    s.lo = 0;
+    s.hi = causal < p.topk ? causal : p.topk;
+    s.base = 0;
+  } else {
+    s.hi = causal;
+    s.lo = (p.window > 0 && causal > p.window) ? causal - p.window : 0;
+    s.base = s.lo & ~(kMlaTile - 1);
+  }
+  return s;
+}
+__device__ __forceinline__ int mla_parts(const MlaSpan &s, int pt) {
+  return s.hi > s.lo ? (s.hi - s.base + pt - 1) / pt : 0;
+}
+__device__ __forceinline__ int mla_part_size(const MlaSpan &s, int pt, int k) {
+  const int a = s.base + k * pt, b = a + pt;
+  return (s.hi < b ? s.hi : b) - (s.lo > a ? s.lo : a);
+}
+
+// Work list on the device (graph-safe: lengths are read at run time), in
+// longest-processing-time order: full partitions first (row order), then the
+// partial ones by decreasing size (32-token buckets), rows without keys last.
+// Also records each row's sequence. One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
+  constexpr int kBuckets = 257;
+  __shared__ int bucket[kBuckets];
+  __shared__ int carry;
+  __shared__ int wave_tot[16];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int PT = p.part_tokens;
+  const int nb = PT / 32;  // bucket b: sizes in (PT - 32(b+1), PT - 32b]; nb: no keys
+  for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  // The span of each thread's first row stays in registers for the later
+  // passes (calls with more than 1024 rows recompute the others).
+  MlaSpan first{0, 0, 0, 0};
+  for (int base = 0; base < p.num_rows; base += 1024) {
+    const int row = base + tid;
+    int nfull = 0;
+    if (row < p.num_rows) {
+      const int seq = mla_seq_of(p, row);
+      p.row_seq[row] = seq;
+      const MlaSpan s = mla_span(p, row, seq);
+      if (base == 0) first = s;
+      const int np = mla_parts(s, PT);
+      if (np == 0) atomicAdd(&bucket[nb], 1);
+      for (int k = 0; k < np; ++k) {
+        const int sz = mla_part_size(s, PT, k);
+        if (sz == PT) ++nfull;
+        else atomicAdd(&bucket[(PT - sz) / 32], 1);
+      }
+    }
+    int x = nfull;  // inclusive scan: shuffles within the wave, then across waves
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      x += lane >= off ? y : 0;
+    }
+    if (lane == 63) wave_tot[wv] = x;
+    __syncthreads();
+    int at = carry;
+    for (int w2 = 0; w2 < wv; ++w2) at += wave_tot[w2];
+    at += x - nfull;
+    if (nfull > 0) {
+      const MlaSpan s = base == 0 ? first : mla_span(p, row, mla_seq_of(p, row));
+      const int np = mla_parts(s, PT);
+      for (int k = 0; k < np; ++k)
+        if (mla_part_size(s, PT, k) == PT) p.items[at++] = (uint32_t(row) << 12) | uint32_t(k);
+    }
+    __syncthreads();
+    if (tid == 1023) carry = at;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int run = carry;
+    for (int b = 0; b <= nb; ++b) {
+      const int c = bucket[b];
+      bucket[b] = run;
+      run += c;
+    }
+    p.queue[0] = 0;
+    p.queue[1] = run;
+  }
+  __syncthreads();
+  for (int base = 0; base < p.num_rows; base += 1024) {
+    const int row = base + tid;
+    if (row >= p.num_rows) continue;
+    const MlaSpan s = base == 0 ? first : mla_span(p, row, mla_seq_of(p, row));
+    const int np = mla_parts(s, PT);
+    if (np == 0) p.items[atomicAdd(&bucket[nb], 1)] = uint32_t(row) << 12;
+    for (int k = 0; k < np; ++k) {
+      const int sz = mla_part_size(s, PT, k);
+      if (sz != PT) p.items[atomicAdd(&bucket[(PT - sz) / 32], 1)] = (uint32_t(row) << 12) | uint32_t(k);
+    }
+  }
+}
 
 template <bool C8>
 struct MlaRow {
   static constexpr uint32_t BYTES = C8 ? 656 : 1152;
+  static constexpr uint32_t CHUNKS = BYTES / 16;  // 72 or 41
   // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16) / 1312 (C8) 16-byte chunks.
   static constexpr int NI = C8 ? 6 : 9;
   static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
-#ifndef IFATTN_MLA_C8_STAGES
-#define IFATTN_MLA_C8_STAGES 6
-#endif
-#ifndef IFATTN_MLA_WGS
-#define IFATTN_MLA_WGS 1
-#endif
-#ifndef IFATTN_MLA_BF16_STAGES
-#define IFATTN_MLA_BF16_STAGES 4
-#endif
-  static constexpr int STAGES = C8 ? IFATTN_MLA_C8_STAGES : IFATTN_MLA_BF16_STAGES;
+  static constexpr int STAGES = C8 ? 6 : 4;
   // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B, a multiple of
   // 128) XOR the chunk index with the row's low 3 bits so the 16 rows that one
   // K read touches spread over the banks; C8 rows (656 B) are not swizzled.
@@ -52,15 +204,18 @@ struct MlaRow {
     return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ (r & 7));
   }
 };
-static_assert(MlaRow<false>::SLOT * MlaRow<false>::STAGES + 4 * 64 * 32 <= 160 * 1024, "LDS");
-static_assert(MlaRow<true>::SLOT * MlaRow<true>::STAGES + 4 * 64 * 32 <= 160 * 1024, "LDS");
+static_assert(MlaRow<false>::SLOT * MlaRow<false>::STAGES + 4 * 64 * 32 + 4 * kSparsePart <= 160 * 1024, "LDS");
+static_assert(MlaRow<true>::SLOT * MlaRow<true>::STAGES + 4 * 64 * 32 + 4 * kSparsePart <= 160 * 1024, "LDS");
 static_assert(MlaRow<false>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
+static_assert(18 * 64 == 16 * 72, "bf16 loads 0..17 move exactly tile rows 0..15");
 static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 
 constexpr int kMlaLds =
     MlaRow<false>::SLOT * MlaRow<false>::STAGES > MlaRow<true>::SLOT * MlaRow<true>::STAGES
         ? MlaRow<false>::SLOT * MlaRow<false>::STAGES
         : MlaRow<true>::SLOT * MlaRow<true>::STAGES;
+
+constexpr uint32_t kNoRow = 0xFFFFFFFFu;  // sparse slot list: no key
 
 __device__ __forceinline__ int mla_tile_token(int g, int j) {
   return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
@@ -75,29 +230,28 @@ __device__ __forceinline__ u32x4 mla_i8x8(uint32_t lo, uint32_t hi) {
                mla_i8pair(mla_i8(hi, 0), mla_i8(hi, 1)), mla_i8pair(mla_i8(hi, 2), mla_i8(hi, 3))};
 }
 
-// One (sequence, partition) item. The partition's 32-token tiles are copied
-// HBM -> LDS once by direct-to-LDS loads shared by the four waves (each tile is
-// 32 consecutive rows of one block) through a ring of R::STAGES slots; every
-// wave then reads its K operand (tokens in rows) and its V operand (dims in
-// rows) from the same LDS bytes.
-template <bool C8>
-__device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *cache,
-                                         uint8_t *ring, float (*xbuf)[8], int seq, int part,
-                                         int w, int lane) {
+// One (row, partition) item. Tiles of the partition go HBM -> LDS once by
+// direct-to-LDS loads shared by the four waves through a ring of R::STAGES
+// slots; every wave reads its K operand (keys in rows) and its V operand (dims
+// in rows) from the same LDS bytes.
+template <bool C8, bool SPARSE>
+__device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
+                                         uint32_t *slot_list, int row, int part, int w, int lane) {
   using R = MlaRow<C8>;
   constexpr int S = R::STAGES;
-  const int len = clamp_len(p, seq);
-  const int PT = p.part_tokens;
-  const int nparts = parts_of(len, PT);
-  const int c = lane & 15, g = lane >> 4;
-  const bool head_live = c < p.q_heads;
   constexpr int DV = 512;
+  const int PT = p.part_tokens;
+  const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
+  const int nparts = mla_parts(sp, PT);
+  const int c = lane & 15, g = lane >> 4;
+  const bool head_live = c < p.heads;
+  const bool partials = nparts > 1 || p.n_sinks > 0;
 
-  if (len <= 0) {
-    if (head_live) {
+  if (nparts == 0) {  // no keys: zeros, or nothing when the merge adds sinks
+    if (head_live && !partials) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        store_u32x4(p.out + (int64_t(seq) * p.q_heads + c) * DV + 128 * w + 32 * g + 8 * k,
+        store_u32x4(p.out + (int64_t(row) * p.heads + c) * DV + 128 * w + 32 * g + 8 * k,
                     u32x4{0, 0, 0, 0});
     }
     return;
@@ -106,46 +260,95 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
   // Q operand: latent dims 128w + 32s + 8g (s < 4), rope dims 32w + 8g (w < 2).
   u32x4 qv[5];
   {
-    const uint16_t *qp = p.q + (int64_t(seq) * p.q_heads + (head_live ? c : 0)) * 576;
+    const uint16_t *qp = p.q + (int64_t(row) * p.heads + (head_live ? c : 0)) * 576;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       qv[s] = head_live ? load_u32x4(qp + 128 * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
     qv[4] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
   }
 
-  const int t_begin = part * PT;
-  const int t_end = t_begin + PT < len ? t_begin + PT : len;
-  const int n_tiles = (t_end - t_begin + kMlaTile - 1) / kMlaTile;
-  int lane_blocks;
-  {
-    const int first = t_begin / p.block_size;
-    const int nblk = (t_end - 1) / p.block_size - first + 1;
-    int b = lane < nblk ? p.block_tables[int64_t(seq) * p.table_stride + first + lane] : 0;
-    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
-  }
-  // Source offset (within a tile) of the 16-byte chunk each lane moves per load.
-  uint32_t src[R::NI];
+  const int tile0 = sp.base + part * PT;
+  const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
+  const int t_end = sp.hi < tile0 + PT ? sp.hi : tile0 + PT;
+  const int n_tiles = (t_end - tile0 + kMlaTile - 1) / kMlaTile;
+  const int bs = p.block_size;
+  const int64_t seq_table = int64_t(sp.seq) * p.table_stride;
+
+  // Per-lane chunk of each direct-to-LDS load: tile row and byte within the row.
+  uint32_t lrow[R::NI], lcol[R::NI];
 #pragma unroll
   for (int k = 0; k < R::NI; ++k) {
     const uint32_t l = uint32_t((k * 4 + w) * 64 + lane);
-    if constexpr (C8) {
-      src[k] = 16 * l;  // chunks past the 32 rows fall outside the tile's extent
-    } else {
-      const uint32_t r = l / 72, jj = l % 72;
-      src[k] = r * R::BYTES + 16 * (jj ^ (r & 7));
-    }
+    lrow[k] = l / R::CHUNKS;
+    const uint32_t jj = l % R::CHUNKS;
+    lcol[k] = 16 * (C8 ? jj : (jj ^ (lrow[k] & 7)));
   }
+
+  int lane_blocks = 0;
+  if constexpr (SPARSE) {
+    // Physical rows of this partition's index entries (kNoRow for padding or
+    // out-of-table positions).
+    const int n = t_end - tile0;
+    for (int i = threadIdx.x; i < n; i += 64 * kMlaWaves) {
+      const int pos = p.indices[int64_t(row) * p.topk + tile0 + i];
+      uint32_t slot = kNoRow;
+      if (pos >= 0 && pos / bs < p.table_stride) {
+        int b = p.block_tables[seq_table + pos / bs];
+        b = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+        slot = uint32_t(b) * uint32_t(bs) + uint32_t(pos & (bs - 1));
+      }
+      slot_list[i] = slot;
+    }
+    __syncthreads();
+  } else {
+    const int first = tile0 / bs;
+    const int nblk = (t_end - 1) / bs - first + 1;  // <= 64 (host-checked partition size)
+    int b = lane < nblk ? p.block_tables[seq_table + first + lane] : 0;
+    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+  }
+
   const uint32_t ring_base = lds_addr(ring);
   auto issue = [&](int ti) {
-    const int t0 = t_begin + ti * kMlaTile;
-    const int bs = p.block_size;
-    const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 - (t_begin & ~(bs - 1))) / bs);
-    const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
-    const int n_live = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
-    const u32x4 rc = raw_rsrc(cache + tok0 * R::BYTES, uint32_t(n_live) * R::BYTES);
+    const int t0 = tile0 + ti * kMlaTile;
     const uint32_t dst = ring_base + uint32_t(ti % S) * R::SLOT + uint32_t(w) * 1024;
+    if constexpr (SPARSE) {
+      // Gather: rows named by the slot list; offsets from the cache base.
+      const u32x4 rc = raw_rsrc(p.cache, p.cache_bytes);
 #pragma unroll
-    for (int k = 0; k < R::NI; ++k) lds_dma16(rc, src[k], dst + uint32_t(k) * 4096);
+      for (int k = 0; k < R::NI; ++k) {
+        const uint32_t r = lrow[k];
+        const uint32_t slot = r < 32u && t0 + int(r) < t_end ? slot_list[ti * kMlaTile + r] : kNoRow;
+        const uint32_t off = slot == kNoRow ? 0xFFFFFFF0u : slot * R::BYTES + lcol[k];
+        lds_dma16(rc, off, dst + uint32_t(k) * 4096);
+      }
+    } else {
+      const int lower = t_begin > t0 ? t_begin - t0 : 0;  // rows before the window start
+      const int upper = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
+      // A tile is one block, or two 16-row blocks (bf16 rows only, where load
+      // n = 4k + w < 18 moves rows 0..15 and the rest rows 16..31). Each part's
+      // base sits at its first live row: earlier rows wrap to offsets past the
+      // extent and land as zeros, like rows past the end.
+      const int halves = bs < kMlaTile ? 2 : 1;
+      u32x4 rc[2];
+      uint32_t first_row[2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        if (hb < halves) {
+          const int r0 = hb * (kMlaTile / halves), r1 = r0 + kMlaTile / halves;
+          const int a = lower > r0 ? lower : r0, b = upper < r1 ? upper : r1;
+          const int blk = __builtin_amdgcn_readlane(lane_blocks, t0 / bs - tile0 / bs + hb);
+          const int64_t tok = int64_t(blk) * bs + (t0 & (bs - 1)) + (a - r0);
+          rc[hb] = raw_rsrc(p.cache + tok * R::BYTES, b > a ? uint32_t(b - a) * R::BYTES : 0u);
+          first_row[hb] = uint32_t(a);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < R::NI; ++k) {
+        const int hb = (halves == 2 && 4 * k + w >= 18) ? 1 : 0;
+        lds_dma16(hb ? rc[1] : rc[0], (lrow[k] - first_row[hb]) * R::BYTES + lcol[k],
+                  dst + uint32_t(k) * 4096);
+      }
+    }
   };
 
   f32x4 oacc[8];
@@ -154,6 +357,16 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
   float m_run = -INFINITY, l_run = 0.0f;
 
   auto compute = [&](const uint8_t *tile, int t0) {
+    // Live rows of this tile (wave-uniform mask).
+    uint32_t live;
+    if constexpr (SPARSE) {
+      const bool ok = lane < 32 && t0 + lane < t_end && slot_list[t0 - tile0 + lane] != kNoRow;
+      live = uint32_t(__ballot(ok));
+    } else {
+      const int lower = t_begin > t0 ? t_begin - t0 : 0;
+      const int upper = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
+      live = (upper >= 32 ? 0xFFFFFFFFu : ((1u << upper) - 1u)) & ~((1u << lower) - 1u);
+    }
     // K operand: token 16mt + c, latent dims 128w + 32s + 8g (+ rope dims 32(w&1) + 8g).
     u32x4 k[2][5];
 #pragma unroll
@@ -240,10 +453,9 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= p.scale_log2;
-    if (t_end - t0 < kMlaTile) {
-      const int n_live = t_end - t0;
+    if (live != 0xFFFFFFFFu) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = mla_tile_token(g, j) < n_live ? x[j] : -INFINITY;
+      for (int j = 0; j < 8; ++j) x[j] = (live >> mla_tile_token(g, j)) & 1u ? x[j] : -INFINITY;
     }
     float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
                        fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
@@ -301,13 +513,9 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
       lds_dma_wait<(S - 2) * R::NI>();
     else
       lds_dma_wait<0>();
-#ifndef IFATTN_EXP_NOBARRIER
     __syncthreads();
-#endif
     if (ti + S - 1 < n_tiles) issue(ti + S - 1);
-#ifndef IFATTN_EXP_NOCOMPUTE
-    compute(ring + (ti % S) * R::SLOT, t_begin + ti * kMlaTile);
-#endif
+    compute(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile);
   }
 
   float l_tot = wave_sum_xor(l_run, 16);
@@ -320,9 +528,9 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
 #pragma unroll
     for (int b = 0; b < 8; ++b) ov[8 * r + b] = oacc[b][r];
   const int d0 = 128 * w + 32 * g;
-  if (nparts == 1) {
+  if (!partials) {
     const float inv = 1.0f / l_tot;
-    uint16_t *op = p.out + (int64_t(seq) * p.q_heads + c) * DV + d0;
+    uint16_t *op = p.out + (int64_t(row) * p.heads + c) * DV + d0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const float *v = ov + 8 * k;
@@ -332,7 +540,7 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
                                     pack_bf16x2(v[6] * inv, v[7] * inv)});
     }
   } else {
-    const int64_t prow = (int64_t(seq) * p.max_parts + part) * p.q_heads + c;
+    const int64_t prow = (int64_t(row) * p.parts_per_row + part) * p.heads + c;
     float *po = p.part_o + prow * DV + d0;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
@@ -341,15 +549,15 @@ __device__ __forceinline__ void mla_item(const DecodeParams &p, const uint8_t *c
   }
 }
 
-template <bool C8>
-__global__ __launch_bounds__(64 * kMlaWaves, IFATTN_MLA_WGS) void mla_decode_kernel(DecodeParams p) {
+template <bool C8, bool SPARSE>
+__global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaParams p) {
   __shared__ __align__(16) uint8_t ring[kMlaLds];
   __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
+  __shared__ uint32_t slot_list[SPARSE ? kSparsePart : 1];
   // The item index travels through the score buffer, idle between items.
   int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
-  const uint8_t *cache = p.k_cache;
   while (true) {
     __syncthreads();
     if (threadIdx.x == 0) *item_slot = atomicAdd(p.queue, 1);
@@ -358,62 +566,231 @@ __global__ __launch_bounds__(64 * kMlaWaves, IFATTN_MLA_WGS) void mla_decode_ker
     __syncthreads();
     if (it >= p.queue[1]) break;
     const uint32_t e = uniform(p.items[it]);
-    const int seq = int(e >> 12);
-    mla_item<C8>(p, cache, ring, xbuf, seq, int(e & 0xfffu), w, lane);
+    mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
   }
+}
+
+// Combine one (row, head): the learned sink rows (scores and values computed
+// here, each thread 2 output dims) and the row's partition partials.
+__global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
+  const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
+  const int np = mla_parts(sp, p.part_tokens);
+  if (p.n_sinks == 0 && np <= 1) return;
+  __shared__ float qs[576];
+  __shared__ float sc[kMaxSinks];
+  float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  if (p.n_sinks > 0) {
+    const uint16_t *qp = p.q + (int64_t(row) * p.heads + h) * 576;
+    for (int i = tid; i < 576; i += 256) qs[i] = bf16_bits_to_f32(qp[i]);
+    __syncthreads();
+    const int i = tid >> 1, half = tid & 1;
+    float d = 0.0f;
+    if (i < p.n_sinks) {
+      const uint32_t *kp = reinterpret_cast<const uint32_t *>(p.sink_k + int64_t(i) * 576 + 288 * half);
+      const float *qh = qs + 288 * half;
+      for (int e = 0; e < 144; ++e) {
+        const uint32_t wv = kp[e];
+        d += qh[2 * e] * bf16_bits_to_f32(wv & 0xffffu) + qh[2 * e + 1] * bf16_bits_to_f32(wv >> 16);
+      }
+    }
+    d += __shfl_xor(d, 1, 64);
+    if (half == 0 && i < p.n_sinks) sc[i] = d * p.scale_log2;
+    __syncthreads();
+    for (int j = 0; j < p.n_sinks; ++j) M = fmaxf(M, sc[j]);
+    const uint32_t *vp = reinterpret_cast<const uint32_t *>(p.sink_v) + tid;
+    for (int j = 0; j < p.n_sinks; ++j) {
+      const float pj = fast_exp2(sc[j] - M);
+      L += pj;
+      const uint32_t wv = vp[int64_t(j) * 256];
+      o0 += pj * bf16_bits_to_f32(wv & 0xffffu);
+      o1 += pj * bf16_bits_to_f32(wv >> 16);
+    }
+  }
+  const int64_t prow0 = int64_t(row) * p.parts_per_row * p.heads + h;
+  // Largest partition max: threads stride over the partitions, then a
+  // workgroup reduction (4 waves).
+  __shared__ float wmax[4];
+  float mp = -INFINITY;
+  for (int k = tid; k < np; k += 256) mp = fmaxf(mp, p.part_ml[(prow0 + int64_t(k) * p.heads) * 2]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mp = wave_max_xor(mp, m);
+  if ((tid & 63) == 0) wmax[tid >> 6] = mp;
+  __syncthreads();
+  mp = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float Mt = fmaxf(M, mp);
+  if (Mt == -INFINITY) {  // no keys and no sinks
+    reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512)[tid] = 0u;
+    return;
+  }
+  const float a = fast_exp2(M - Mt);
+  L *= a;
+  o0 *= a;
+  o1 *= a;
+#pragma unroll 8
+  for (int k = 0; k < np; ++k) {
+    const int64_t pr = prow0 + int64_t(k) * p.heads;
+    const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+    const float2 o = *reinterpret_cast<const float2 *>(p.part_o + pr * 512 + 2 * tid);
+    const float wk = fast_exp2(ml.x - Mt);
+    L += wk * ml.y;
+    o0 += wk * o.x;
+    o1 += wk * o.y;
+  }
+  const float inv = 1.0f / L;
+  reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512)[tid] =
+      pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 namespace {
 
-int32_t mla_common(bool c8, const void *q, const void *cache, const int32_t *block_tables,
-                   int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs,
-                   int32_t heads, int32_t block_size, int64_t num_blocks, int32_t max_context,
-                   float scale, void *workspace, uint64_t workspace_bytes, void *stream) {
-  if (!q || !cache || !block_tables || !seq_lens || !out)
-    return fail(IFATTN_EINVAL, "mla decode: null pointer");
-  if (num_seqs <= 0 || heads <= 0 || heads > 16)
-    return fail(IFATTN_EINVAL, "mla decode: 1..16 heads per call");
-  if (block_size < 32 || (block_size & (block_size - 1)))
-    return fail(IFATTN_EINVAL, "mla decode: block_size must be a power of two >= 32");
-  if (max_context <= 0 || num_blocks <= 0 || table_stride <= 0 ||
-      int64_t(table_stride) * block_size < max_context)
-    return fail(IFATTN_EINVAL, "mla decode: table_stride * block_size must cover max_context");
-  if (!aligned16(q) || !aligned16(out) || !aligned16(cache))
-    return fail(IFATTN_EINVAL, "mla decode: q, out and cache must be 16-byte aligned");
-  if (uint64_t(block_size) * (c8 ? 656 : 1152) * 1 > (1ull << 31))
-    return fail(IFATTN_EINVAL, "mla decode: block too large");
-  DecodeParams p{};
-  p.q = (const uint16_t *)q;
-  p.k_cache = (const uint8_t *)cache;
-  p.block_tables = block_tables;
-  p.seq_lens = seq_lens;
-  p.out = (uint16_t *)out;
-  p.num_blocks = num_blocks;
-  p.num_seqs = num_seqs;
-  p.q_heads = heads;
-  p.kv_heads = 1;
-  p.group = heads;
-  p.table_stride = table_stride;
-  p.block_size = block_size;
-  p.max_context = max_context;
-  p.part_tokens = part_tokens();
-  p.max_parts = max_parts_for(max_context);
-  p.scale_log2 = scale * kLog2e;
-  if (p.max_parts > 4096) return fail(IFATTN_EINVAL, "mla decode: max_context above 1M tokens");
-  if (p.part_tokens > 64 * block_size)
-    return fail(IFATTN_EINVAL, "mla decode: partition spans more than 64 blocks");
-  const uint64_t need = ifattn_mla_decode_workspace_size(num_seqs, heads, max_context);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace))
-    return fail(IFATTN_EWORKSPACE, "mla decode: workspace missing, short or misaligned");
-  split_k_bind_workspace(p, workspace, heads, 512);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  launch_prologue(p, RowWrite{}, s);
-  if (c8)
-    mla_decode_kernel<true><<<device_cus() * IFATTN_MLA_WGS, 64 * kMlaWaves, 0, s>>>(p);
-  else
-    mla_decode_kernel<false><<<device_cus() * IFATTN_MLA_WGS, 64 * kMlaWaves, 0, s>>>(p);
-  launch_merge<512>(p, s);
-  return launch_status("mla decode");
+struct MlaCall {
+  int c8;
+  const void *q, *cache;
+  const int32_t *block_tables;
+  int32_t table_stride;
+  const int32_t *cu_q, *kv_lens;
+  int32_t num_seqs, num_rows;
+  const int32_t *indices;
+  int32_t topk, window;
+  const void *sink_k, *sink_v;
+  int32_t n_sinks;
+  void *out;
+  int32_t heads, block_size;
+  int64_t num_blocks;
+  int32_t max_context;
+  float scale;
+  void *workspace;
+  uint64_t workspace_bytes;
+  void *stream;
+};
+
+// Partition size and partitions per row of a call.
+inline int mla_part_tokens(bool sparse, int block_size) {
+  if (sparse) return kSparsePart;
+  // A partition starting on a 32-token tile spans 1 + ceil((PT - 32) / bs)
+  // blocks, at most the 64 one wave holds: PT <= 63 * bs + 32.
+  const int pt = part_tokens();
+  const int cap = (63 * block_size + 32) & ~31;
+  return pt < cap ? pt : cap;
+}
+inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size) {
+  const int pt = mla_part_tokens(sparse, block_size);
+  if (sparse) return (topk + pt - 1) / pt;
+  const int full = (max_context + pt - 1) / pt;
+  if (window <= 0) return full;
+  const int win = (window + 31 + pt - 1) / pt;
+  return win < full ? win : full;
+}
+inline uint64_t mla_workspace(int rows, int heads, int ppr, bool partials) {
+  const uint64_t items = uint64_t(rows) * uint64_t(ppr);
+  uint64_t b = kQueueBytes + align16(items * 4) + align16(uint64_t(rows) * 4);
+  if (partials) b += items * heads * (512 + 2) * sizeof(float);
+  return b;
+}
+
+int32_t mla_run(const MlaCall &c, const char *what) {
+  const bool sparse = c.indices != nullptr;
+  if (!c.q || !c.cache || !c.block_tables || !c.kv_lens || !c.out)
+    return fail(IFATTN_EINVAL, what, "null pointer");
+  if (c.num_seqs <= 0 || c.num_rows <= 0 || c.num_rows >= (1 << 20) || c.heads <= 0 || c.heads > 16)
+    return fail(IFATTN_EINVAL, what, "1..16 heads, 1..2^20-1 rows and at least one sequence");
+  if (!c.cu_q && c.num_rows != c.num_seqs)
+    return fail(IFATTN_EINVAL, what, "without cu_seqlens_q every sequence has one row");
+  if (c.block_size < (c.c8 ? 32 : 16) || (c.block_size & (c.block_size - 1)))
+    return fail(IFATTN_EINVAL, what, "block_size must be a power of two >= 16 (bf16) or >= 32 (C8)");
+  if (c.max_context <= 0 || c.num_blocks <= 0 || c.table_stride <= 0 ||
+      int64_t(c.table_stride) * c.block_size < c.max_context)
+    return fail(IFATTN_EINVAL, what, "table_stride * block_size must cover max_context");
+  if (!aligned16(c.q) || !aligned16(c.out) || !aligned16(c.cache))
+    return fail(IFATTN_EINVAL, what, "q, out and cache must be 16-byte aligned");
+  const uint64_t row_bytes = c.c8 ? 656 : 1152;
+  if (uint64_t(c.block_size) * row_bytes > (1ull << 31))
+    return fail(IFATTN_EINVAL, what, "block too large");
+  const uint64_t cache_bytes = uint64_t(c.num_blocks) * c.block_size * row_bytes;
+  if (sparse && (c.topk <= 0 || cache_bytes > 0xFFFFFFF0ull))
+    return fail(IFATTN_EINVAL, what, "sparse attention needs topk > 0 and a cache below 4 GiB");
+  if (c.window < 0) return fail(IFATTN_EINVAL, what, "window must be >= 0");
+  if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
+      (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
+    return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
+  const int pt = mla_part_tokens(sparse, c.block_size);
+  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
+  if (ppr > 4096) return fail(IFATTN_EINVAL, what, "more than 4096 partitions per row");
+  const bool partials = ppr > 1 || c.n_sinks > 0;
+  const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, partials);
+  if (!c.workspace || c.workspace_bytes < need || !aligned16(c.workspace))
+    return fail(IFATTN_EWORKSPACE, what, "workspace missing, short or misaligned");
+  MlaParams p{};
+  p.q = static_cast<const uint16_t *>(c.q);
+  p.cache = static_cast<const uint8_t *>(c.cache);
+  p.block_tables = c.block_tables;
+  p.kv_lens = c.kv_lens;
+  p.cu_q = c.cu_q;
+  p.indices = c.indices;
+  p.sink_k = static_cast<const uint16_t *>(c.sink_k);
+  p.sink_v = static_cast<const uint16_t *>(c.sink_v);
+  p.out = static_cast<uint16_t *>(c.out);
+  p.num_blocks = c.num_blocks;
+  p.cache_bytes = sparse ? uint32_t(cache_bytes) : 0u;
+  p.num_seqs = c.num_seqs;
+  p.num_rows = c.num_rows;
+  p.heads = c.heads;
+  p.table_stride = c.table_stride;
+  p.block_size = c.block_size;
+  p.max_context = c.max_context;
+  p.topk = c.topk;
+  p.window = c.window;
+  p.n_sinks = c.n_sinks;
+  p.part_tokens = pt;
+  p.parts_per_row = ppr;
+  p.scale_log2 = c.scale * kLog2e;
+  uint8_t *ws = static_cast<uint8_t *>(c.workspace);
+  const uint64_t items = uint64_t(c.num_rows) * ppr;
+  p.queue = reinterpret_cast<int32_t *>(ws);
+  ws += kQueueBytes;
+  p.items = reinterpret_cast<uint32_t *>(ws);
+  ws += align16(items * 4);
+  p.row_seq = reinterpret_cast<int32_t *>(ws);
+  ws += align16(uint64_t(c.num_rows) * 4);
+  p.part_o = partials ? reinterpret_cast<float *>(ws) : nullptr;
+  p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
+  hipStream_t s = static_cast<hipStream_t>(c.stream);
+  mla_plan_kernel<<<1, 1024, 0, s>>>(p);
+  const int grid = device_cus();
+  if (c.c8) {
+    if (sparse) mla_attention_kernel<true, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+    else mla_attention_kernel<true, false><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+  } else {
+    if (sparse) mla_attention_kernel<false, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+    else mla_attention_kernel<false, false><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+  }
+  if (partials) mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
+  return launch_status(what);
+}
+
+MlaCall decode_call(bool c8, const void *q, const void *cache, const int32_t *block_tables,
+                    int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs,
+                    int32_t heads, int32_t block_size, int64_t num_blocks, int32_t max_context,
+                    float scale, void *workspace, uint64_t workspace_bytes, void *stream) {
+  MlaCall c{};
+  c.c8 = c8;
+  c.q = q;
+  c.cache = cache;
+  c.block_tables = block_tables;
+  c.table_stride = table_stride;
+  c.kv_lens = seq_lens;
+  c.num_seqs = c.num_rows = num_seqs;
+  c.out = out;
+  c.heads = heads;
+  c.block_size = block_size;
+  c.num_blocks = num_blocks;
+  c.max_context = max_context;
+  c.scale = scale;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.stream = stream;
+  return c;
 }
 
 }  // namespace
@@ -422,9 +799,10 @@ int32_t mla_common(bool c8, const void *q, const void *cache, const int32_t *blo
 using namespace ifattn;
 
 extern "C" uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads,
-                                                     int32_t max_context) {
-  if (num_seqs <= 0 || heads <= 0 || max_context <= 0) return 0;
-  return split_k_workspace_bytes(num_seqs, heads, 512, max_context);
+                                                     int32_t max_context, int32_t block_size) {
+  if (num_seqs <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
+  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size);
+  return mla_workspace(num_seqs, heads, ppr, ppr > 1);
 }
 
 extern "C" int32_t ifattn_mla_decode_bf16(const void *q, const void *cache,
@@ -433,8 +811,10 @@ extern "C" int32_t ifattn_mla_decode_bf16(const void *q, const void *cache,
                                           int32_t heads, int32_t block_size, int64_t num_blocks,
                                           int32_t max_context, float scale, void *workspace,
                                           uint64_t workspace_bytes, void *stream) {
-  return mla_common(false, q, cache, block_tables, table_stride, seq_lens, out, num_seqs, heads,
-                    block_size, num_blocks, max_context, scale, workspace, workspace_bytes, stream);
+  return mla_run(decode_call(false, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
+                             heads, block_size, num_blocks, max_context, scale, workspace,
+                             workspace_bytes, stream),
+                 "mla decode");
 }
 
 extern "C" int32_t ifattn_mla_decode_c8(const void *q, const void *cache,
@@ -443,6 +823,57 @@ extern "C" int32_t ifattn_mla_decode_c8(const void *q, const void *cache,
                                         int32_t heads, int32_t block_size, int64_t num_blocks,
                                         int32_t max_context, float scale, void *workspace,
                                         uint64_t workspace_bytes, void *stream) {
-  return mla_common(true, q, cache, block_tables, table_stride, seq_lens, out, num_seqs, heads,
-                    block_size, num_blocks, max_context, scale, workspace, workspace_bytes, stream);
+  return mla_run(decode_call(true, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
+                             heads, block_size, num_blocks, max_context, scale, workspace,
+                             workspace_bytes, stream),
+                 "mla decode c8");
+}
+
+extern "C" uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_t heads,
+                                                        int32_t max_context, int32_t window,
+                                                        int32_t topk, int32_t n_sinks,
+                                                        int32_t block_size) {
+  if (num_rows <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
+  const bool sparse = topk > 0;
+  const int ppr = mla_parts_per_row(sparse, topk, window, max_context, block_size);
+  return mla_workspace(num_rows, heads, ppr, ppr > 1 || n_sinks > 0);
+}
+
+extern "C" int32_t ifattn_mla_window_attention_bf16(
+    const void *q, const void *cache, const int32_t *block_tables, int32_t table_stride,
+    const int32_t *cu_seqlens_q, const int32_t *kv_lens, int32_t num_seqs, int32_t num_rows,
+    int32_t window, const void *sink_keys, const void *sink_values, int32_t n_sinks, void *out,
+    int32_t heads, int32_t block_size, int64_t num_blocks, int32_t max_context, float scale,
+    void *workspace, uint64_t workspace_bytes, void *stream) {
+  MlaCall c = decode_call(false, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
+                          heads, block_size, num_blocks, max_context, scale, workspace,
+                          workspace_bytes, stream);
+  c.cu_q = cu_seqlens_q;
+  c.num_rows = num_rows;
+  c.window = window;
+  c.sink_k = sink_keys;
+  c.sink_v = sink_values;
+  c.n_sinks = n_sinks;
+  return mla_run(c, "mla window attention");
+}
+
+extern "C" int32_t ifattn_mla_sparse_attention_c8(
+    const void *q, const void *cache, const int32_t *indices, int32_t topk,
+    const int32_t *block_tables, int32_t table_stride, const int32_t *cu_seqlens_q,
+    const int32_t *kv_lens, int32_t num_seqs, int32_t num_rows, const void *sink_keys,
+    const void *sink_values, int32_t n_sinks, void *out, int32_t heads, int32_t block_size,
+    int64_t num_blocks, int32_t max_context, float scale, void *workspace,
+    uint64_t workspace_bytes, void *stream) {
+  if (!indices) return fail(IFATTN_EINVAL, "mla sparse attention: null indices");
+  MlaCall c = decode_call(true, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
+                          heads, block_size, num_blocks, max_context, scale, workspace,
+                          workspace_bytes, stream);
+  c.cu_q = cu_seqlens_q;
+  c.num_rows = num_rows;
+  c.indices = indices;
+  c.topk = topk;
+  c.sink_k = sink_keys;
+  c.sink_v = sink_values;
+  c.n_sinks = n_sinks;
+  return mla_run(c, "mla sparse attention");
 }

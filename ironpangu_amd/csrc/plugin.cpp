@@ -232,7 +232,7 @@ void prepare_op(State &s, const IFKernelTensorV1 *in, uint32_t nin, const IFKern
       require(out[0].shape[0] == s.n && out[0].shape[1] == s.q_heads && out[0].shape[2] == 512,
               "out must be [n, heads, 512]");
       s.scale = 1.0f / std::sqrt(192.0f);
-      s.workspace = ifattn_mla_decode_workspace_size(s.n, s.q_heads, s.max_ctx);
+      s.workspace = ifattn_mla_decode_workspace_size(s.n, s.q_heads, s.max_ctx, s.block_size);
       return;
     }
     case kMlaWriteC8: {

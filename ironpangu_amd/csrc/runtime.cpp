@@ -13,6 +13,10 @@ int32_t fail(int32_t code, const char *message) {
   g_last_error = message ? message : "";
   return code;
 }
+int32_t fail(int32_t code, const char *what, const char *message) {
+  g_last_error = std::string(what ? what : "") + ": " + (message ? message : "");
+  return code;
+}
 int32_t launch_status(const char *what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

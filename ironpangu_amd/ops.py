@@ -261,8 +261,8 @@ def varlen_prefill(q, k_cache, v_cache, block_tables, cu_seqlens_q, kv_lens, max
 
 # ---------------------------------------------------------------- MLA decode
 
-def mla_workspace(num_seqs, heads, max_context, device="cuda"):
-    n = lib().ifattn_mla_decode_workspace_size(num_seqs, heads, max_context)
+def mla_workspace(num_seqs, heads, max_context, block_size, device="cuda"):
+    n = lib().ifattn_mla_decode_workspace_size(num_seqs, heads, max_context, block_size)
     return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
 
 
@@ -284,12 +284,71 @@ def mla_decode(q, cache, block_tables, seq_lens, max_context, scale=None, out=No
         out = torch.empty((ns, h, 512), dtype=torch.bfloat16, device=q.device)
     _req(tuple(out.shape) == (ns, h, 512) and out.dtype == torch.bfloat16, "out: bf16 [n, heads, 512]")
     if workspace is None:
-        workspace = mla_workspace(ns, h, max_context, q.device)
+        workspace = mla_workspace(ns, h, max_context, bs, q.device)
     fn = lib().ifattn_mla_decode_c8 if c8 else lib().ifattn_mla_decode_bf16
     st = fn(_ptr(q), _ptr(cache), _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens),
             _ptr(out), ns, h, bs, nb, max_context, float(scale), _ptr(workspace),
             workspace.numel(), _stream(stream))
     check(st, "ifattn_mla_decode")
+    return out
+
+
+def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None, indices=None,
+                  window=0, sink_keys=None, sink_values=None, scale=None, out=None,
+                  workspace=None, stream=None):
+    """Packed-MLA attention over query rows.
+
+    q [rows, heads, 576] bf16; rows per sequence from cu_seqlens int32 [seqs+1]
+    (None: one row per sequence); kv_lens int32 [seqs]. bf16 caches
+    [blocks, bs, 576] take the window path (``window`` 0 = all keys); packed C8
+    caches uint8 [blocks, bs, 656] take the sparse path with ``indices`` int32
+    [rows, topk]. sink_keys [n, 576] / sink_values [n, 512] bf16 (n <= 128) are
+    optional. Returns out [rows, heads, 512] bf16.
+    """
+    c8 = cache.dtype == torch.uint8
+    _dev(q, cache, block_tables, kv_lens, cu_seqlens, indices, sink_keys, sink_values, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == 576, "q: bf16 [rows, heads, 576]")
+    rows, h, _ = q.shape
+    _req(cache.dim() == 3 and cache.shape[2] == (656 if c8 else 576)
+         and cache.dtype in (torch.uint8, torch.bfloat16), "cache: bf16 [.., 576] or uint8 [.., 656]")
+    _req(c8 == (indices is not None), "C8 caches take index lists, bf16 caches take windows")
+    nb, bs, _ = cache.shape
+    seqs = rows if cu_seqlens is None else cu_seqlens.numel() - 1
+    _req(cu_seqlens is None or (cu_seqlens.dtype == torch.int32 and seqs >= 1),
+         "cu_seqlens: int32 [seqs + 1]")
+    _check_tables(block_tables, kv_lens, seqs, bs, max_context)
+    topk = 0
+    if indices is not None:
+        _req(indices.dtype == torch.int32 and indices.dim() == 2 and indices.shape[0] == rows,
+             "indices: int32 [rows, topk]")
+        topk = indices.shape[1]
+    ns = 0
+    if sink_keys is not None:
+        ns = sink_keys.shape[0]
+        _req(sink_keys.dtype == torch.bfloat16 and tuple(sink_keys.shape) == (ns, 576)
+             and sink_values is not None and sink_values.dtype == torch.bfloat16
+             and tuple(sink_values.shape) == (ns, 512), "sinks: bf16 keys [n, 576], values [n, 512]")
+    if scale is None:
+        scale = 1.0 / math.sqrt(192.0)
+    if out is None:
+        out = torch.empty((rows, h, 512), dtype=torch.bfloat16, device=q.device)
+    _req(tuple(out.shape) == (rows, h, 512) and out.dtype == torch.bfloat16, "out: bf16 [rows, heads, 512]")
+    if workspace is None:
+        n = lib().ifattn_mla_attention_workspace_size(rows, h, max_context, int(window), topk, ns, bs)
+        workspace = torch.empty(max(int(n), 16), dtype=torch.uint8, device=q.device)
+    if c8:
+        st = lib().ifattn_mla_sparse_attention_c8(
+            _ptr(q), _ptr(cache), _ptr(indices), topk, _ptr(block_tables), block_tables.shape[1],
+            _ptr(cu_seqlens), _ptr(kv_lens), seqs, rows, _ptr(sink_keys), _ptr(sink_values), ns,
+            _ptr(out), h, bs, nb, max_context, float(scale), _ptr(workspace), workspace.numel(),
+            _stream(stream))
+    else:
+        st = lib().ifattn_mla_window_attention_bf16(
+            _ptr(q), _ptr(cache), _ptr(block_tables), block_tables.shape[1], _ptr(cu_seqlens),
+            _ptr(kv_lens), seqs, rows, int(window), _ptr(sink_keys), _ptr(sink_values), ns,
+            _ptr(out), h, bs, nb, max_context, float(scale), _ptr(workspace), workspace.numel(),
+            _stream(stream))
+    check(st, "ifattn_mla_attention")
     return out
 
 

@@ -44,11 +44,13 @@ def lib():
         l.oracle_varlen_prefill.argtypes = [vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32,
                                             i32, f32, i32]
         l.oracle_mla_decode.argtypes = [vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, f32, i32]
+        l.oracle_mla_attention.argtypes = [vp, vp, i32, vp, i32, vp, vp, i32, i32, vp, i32, i32,
+                                           vp, vp, i32, vp, i32, i32, f32, i32]
         l.oracle_hardware_threads.restype = i32
         for f in ("oracle_kv_write", "oracle_quant_rows", "oracle_quant_legacy",
                   "oracle_dequant_legacy", "oracle_mla_pack_c8", "oracle_mla_norm_rope_write",
                   "oracle_paged_decode",
-                  "oracle_varlen_prefill", "oracle_mla_decode"):
+                  "oracle_varlen_prefill", "oracle_mla_decode", "oracle_mla_attention"):
             getattr(l, f).restype = None
         _lib = l
     return _lib
@@ -180,4 +182,26 @@ def mla_decode(q, cache, block_tables, seq_lens, heads, block_size, scale, c8=Fa
     out = np.zeros((n, heads, 512), np.float32)
     lib().oracle_mla_decode(_p(q), _p(cache), int(c8), _p(tables), tables.shape[1], _p(lens),
                             _p(out), n, heads, block_size, scale, threads)
+    return out
+
+
+def mla_attention(q, cache, block_tables, kv_lens, heads, block_size, scale, c8=False,
+                  cu_seqlens=None, indices=None, window=0, sink_k=None, sink_v=None, threads=0):
+    """fp32 [rows, heads, 512]. q [rows, heads, 576] bf16 bits; rows per sequence from
+    cu_seqlens (None: one row per sequence); indices [rows, topk] for sparse rows."""
+    q = _c(q, np.uint16).reshape(-1, heads, 576)
+    rows = q.shape[0]
+    cache = _c(cache, np.uint8 if c8 else np.uint16)
+    tables = _c(block_tables, np.int32)
+    kv = _c(kv_lens, np.int32)
+    cu = None if cu_seqlens is None else _c(cu_seqlens, np.int32)
+    idx = None if indices is None else _c(indices, np.int32).reshape(rows, -1)
+    topk = 0 if idx is None else idx.shape[1]
+    sk = None if sink_k is None else _c(sink_k, np.uint16).reshape(-1, 576)
+    sv = None if sink_v is None else _c(sink_v, np.uint16).reshape(-1, 512)
+    ns = 0 if sk is None else sk.shape[0]
+    out = np.zeros((rows, heads, 512), np.float32)
+    lib().oracle_mla_attention(_p(q), _p(cache), int(c8), _p(tables), tables.shape[1], _p(cu),
+                               _p(kv), kv.size, rows, _p(idx), topk, int(window), _p(sk), _p(sv),
+                               ns, _p(out), heads, block_size, float(scale), threads)
     return out

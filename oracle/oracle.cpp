@@ -32,6 +32,10 @@
 //                          Pinned: q = 0 causal prefix means, decode-row equivalence.
 //   oracle_mla_decode      packed_cache_probe.cpp:47-66 / sliding_window_probe.cpp:144-163
 //                          without sinks. Pinned: q = 0 latent mean, rope-only scores.
+//   oracle_mla_attention   the same with query rows, windows, sparse index lists and
+//                          learned sinks. Pinned: the two probes' fixtures against a
+//                          float64 restatement, agreement with oracle_mla_decode,
+//                          sparse list = dense range, order invariance.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -389,6 +393,88 @@ void oracle_mla_decode(const uint16_t *q, const void *cache, int32_t c8, const i
     for (int e = 0; e < 512; ++e) {
       float acc = 0.0f;
       for (int j = 0; j < len; ++j) acc += s[j] * val(slot[j], e);
+      o[e] = acc;
+    }
+  });
+}
+
+// General packed-MLA attention over query rows: the BF16 window attention with
+// learned sinks (sliding_window_probe.cpp:144-163) and the packed C8 sparse
+// attention with learned sinks (packed_cache_probe.cpp:47-66). Row t of
+// sequence s (rows cu_q[s]..cu_q[s+1]-1, or row = s when cu_q is null) sees
+// causal = kv_lens[s] - count + (t - start) + 1 keys (openpangu_attention_metadata.h:20-22).
+// Dense (indices null): positions [max(0, causal - window), causal), window 0 =
+// unbounded. Sparse: the logical positions indices[t][j], j < min(causal, topk),
+// that are >= 0 (openpangu_attention_metadata.h:13-33). Sink rows (keys [n,576],
+// values [n,512] bf16) join every row's softmax. out: fp32 [rows, heads, 512];
+// a row with neither keys nor sinks is zero.
+void oracle_mla_attention(const uint16_t *q, const void *cache, int32_t c8, const int32_t *tables,
+                          int32_t stride, const int32_t *cu_q, const int32_t *kv_lens,
+                          int32_t num_seqs, int32_t num_rows, const int32_t *indices, int32_t topk,
+                          int32_t window, const uint16_t *sink_k, const uint16_t *sink_v,
+                          int32_t n_sinks, float *out, int32_t heads, int32_t bs, float scale,
+                          int32_t threads) {
+  auto val = [&](int64_t slot, int e) -> float {
+    if (!c8) return bf(static_cast<const uint16_t *>(cache)[slot * 576 + e]);
+    const uint8_t *row = static_cast<const uint8_t *>(cache) + slot * 656;
+    if (e < 512) {
+      float sc;
+      std::memcpy(&sc, row + 640 + (e / 128) * 4, 4);
+      return float(int8_t(row[e])) * sc;
+    }
+    uint16_t v;
+    std::memcpy(&v, row + 512 + (e - 512) * 2, 2);
+    return bf(v);
+  };
+  std::vector<int> row_seq(num_rows), row_pos(num_rows);
+  for (int s = 0; s < num_seqs; ++s) {
+    const int start = cu_q ? cu_q[s] : s, end = cu_q ? cu_q[s + 1] : s + 1;
+    for (int t = start; t < end && t < num_rows; ++t) {
+      row_seq[t] = s;
+      row_pos[t] = kv_lens[s] - (end - start) + (t - start);  // position of row t
+    }
+  }
+  parallel_for(int64_t(num_rows) * heads, default_threads(threads), [&](int64_t unit) {
+    const int t = int(unit / heads);
+    const int seq = row_seq[t];
+    const int causal = std::max(0, row_pos[t] + 1);
+    std::vector<int64_t> slots;
+    if (indices) {
+      for (int j = 0; j < std::min(causal, topk); ++j) {
+        const int pos = indices[int64_t(t) * topk + j];
+        if (pos < 0) continue;
+        slots.push_back(int64_t(tables[int64_t(seq) * stride + pos / bs]) * bs + pos % bs);
+      }
+    } else {
+      const int lo = window > 0 ? std::max(0, causal - window) : 0;
+      for (int pos = lo; pos < causal; ++pos)
+        slots.push_back(int64_t(tables[int64_t(seq) * stride + pos / bs]) * bs + pos % bs);
+    }
+    const int nk = int(slots.size()), n = nk + n_sinks;
+    float *o = out + unit * 512;
+    if (n == 0) {
+      std::fill(o, o + 512, 0.0f);
+      return;
+    }
+    const uint16_t *qh = q + unit * 576;
+    std::vector<float> sc(n);
+    float mx = -INFINITY;
+    for (int j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      if (j < nk)
+        for (int e = 0; e < 576; ++e) acc += bf(qh[e]) * val(slots[j], e);
+      else
+        for (int e = 0; e < 576; ++e) acc += bf(qh[e]) * bf(sink_k[int64_t(j - nk) * 576 + e]);
+      sc[j] = acc * scale;
+      mx = std::max(mx, sc[j]);
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < n; ++j) sum += std::exp(sc[j] - mx);
+    for (int j = 0; j < n; ++j) sc[j] = std::exp(sc[j] - mx) / sum;
+    for (int e = 0; e < 512; ++e) {
+      float acc = 0.0f;
+      for (int j = 0; j < n; ++j)
+        acc += sc[j] * (j < nk ? val(slots[j], e) : bf(sink_v[int64_t(j - nk) * 512 + e]));
       o[e] = acc;
     }
   });

@@ -43,7 +43,7 @@ def test_host_errors_without_device():
     st = lib.ifattn_kv_cache_write(1, 2, 3, 4, 5, 7, 1, 1024, 10, None)  # bad slot dtype
     assert st == -1 and b"dtype" in lib.ifattn_last_error()
     assert lib.ifattn_paged_decode_workspace_size(256, 16, 128, 256) > 64
-    assert lib.ifattn_mla_decode_workspace_size(0, 16, 64) == 0
+    assert lib.ifattn_mla_decode_workspace_size(0, 16, 64, 64) == 0
 
 
 class Tensor(C.Structure):
@@ -173,7 +173,7 @@ def test_write_and_mla_prepare():
            tensor([4], 4, 1)]
     outs = [tensor([4, 16, 512], 2, 2)]
     st, p = _prepare(k, ins, outs)
-    assert st == 0 and p.workspace_bytes == _native.lib().ifattn_mla_decode_workspace_size(4, 16, 1024)
+    assert st == 0 and p.workspace_bytes == _native.lib().ifattn_mla_decode_workspace_size(4, 16, 1024, 64)
     k.release(p.state)
     ins[1] = tensor([32, 64, 576], 1, 1)
     assert _prepare(k, ins, outs)[0] != 0
