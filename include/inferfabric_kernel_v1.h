@@ -90,6 +90,16 @@ typedef const IFKernelV1 *(*IFKernelEntryV1)(uint32_t requested_version);
  *       cache bf16 [blocks, block_size, 576] (access 3); eps 1e-5
  *   libifk_mla_norm_rope_cache_c8   "inferfabric.mla_norm_rope_cache.c8.v2"
  *       same inputs ; cache I8 [blocks, block_size, 656] (access 3)
+ *   libifk_mla_window_attention_w512_bf16  "inferfabric.mla_window_attention.w512.bf16.v2"
+ *   libifk_mla_window_attention_w2048_bf16 "inferfabric.mla_window_attention.w2048.bf16.v2"
+ *       q bf16 [rows, heads, 576], cache bf16 [blocks, block_size, 576], block_tables I32
+ *       [seqs, entries], cu_seqlens_q I32 [seqs+1], kv_lens I32 [seqs], sink_keys bf16
+ *       [n <= 128, 576], sink_values bf16 [n, 512] ; out bf16 [rows, heads, 512]
+ *       (window 512 or 2048 keys, the two windows of examples/openpangu/92b-tp8-ep8.inferfabric:97)
+ *   libifk_mla_sparse_attention_c8 "inferfabric.mla_sparse_attention.c8.v2"
+ *       q, cache I8 [blocks, block_size, 656], indices I32 [rows, topk], block_tables,
+ *       cu_seqlens_q, kv_lens, sink_keys, sink_values ; out bf16 [rows, heads, 512]
+ * Attention contracts use scale 1/sqrt(192) for MLA and 1/sqrt(head_dim) for GQA.
  * max_context is entries * block_size of the block-table descriptor.
  */
 

@@ -42,6 +42,9 @@ PLUGINS = {
     "mla_cache_write_c8": 7,
     "mla_norm_rope_cache_bf16": 8,
     "mla_norm_rope_cache_c8": 9,
+    "mla_window_attention_w512_bf16": 10,
+    "mla_window_attention_w2048_bf16": 11,
+    "mla_sparse_attention_c8": 12,
 }
 
 

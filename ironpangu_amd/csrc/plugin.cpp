@@ -25,6 +25,9 @@ enum Op : int {
   kMlaWriteC8,
   kMlaNormRopeBf16,
   kMlaNormRopeC8,
+  kMlaWindow512,
+  kMlaWindow2048,
+  kMlaSparseC8,
   kOpCount
 };
 
@@ -34,6 +37,9 @@ const char *const kContract[kOpCount] = {
     "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
     "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
     "inferfabric.mla_norm_rope_cache.bf16.v2", "inferfabric.mla_norm_rope_cache.c8.v2",
+    "inferfabric.mla_window_attention.w512.bf16.v2",
+    "inferfabric.mla_window_attention.w2048.bf16.v2",
+    "inferfabric.mla_sparse_attention.c8.v2",
 };
 constexpr const char *kTarget = "gfx950";
 
@@ -44,6 +50,7 @@ struct State {
   int32_t slot_dtype;
   int64_t rows, row_bytes, num_slots, num_blocks;
   int32_t n, q_heads, kv_heads, head_dim, block_size, stride, max_ctx, total_q;
+  int32_t window, topk, n_sinks;
   float scale;
 };
 
@@ -266,6 +273,51 @@ void prepare_op(State &s, const IFKernelTensorV1 *in, uint32_t nin, const IFKern
       s.num_slots = out[0].shape[0] * out[0].shape[1];
       return;
     }
+    case kMlaWindow512:
+    case kMlaWindow2048:
+    case kMlaSparseC8: {
+      const bool sparse = s.op == kMlaSparseC8;
+      const uint32_t t = sparse ? 3 : 2;  // first metadata port after q, cache (, indices)
+      require(nin == t + 5 && nout == 1,
+              sparse ? "mla sparse attention: 8 inputs, 1 output" : "mla window attention: 7 inputs, 1 output");
+      check_tensor(in[0], BF, R, 3);
+      require(in[0].shape[2] == 576, "q must be [rows, heads, 576]");
+      check_tensor(in[1], sparse ? I8 : BF, R, 3);
+      require(in[1].shape[2] == (sparse ? 656 : 576), "cache rows: 576 bf16 or 656 bytes");
+      s.total_q = int32_t(in[0].shape[0]);
+      s.q_heads = int32_t(in[0].shape[1]);
+      require(s.q_heads <= 16 && s.total_q < (1 << 20), "at most 16 heads and 2^20-1 rows");
+      s.num_blocks = in[1].shape[0];
+      s.block_size = int32_t(in[1].shape[1]);
+      if (sparse) {
+        check_tensor(in[2], I32, R, 2);
+        require(in[2].shape[0] == s.total_q, "indices must be [rows, topk]");
+        s.topk = int32_t(in[2].shape[1]);
+      }
+      check_tensor(in[t], I32, R, 2);
+      check_tensor(in[t + 1], I32, R, 1);
+      check_tensor(in[t + 2], I32, R, 1);
+      s.n = int32_t(in[t + 1].shape[0] - 1);
+      require(s.n >= 1 && in[t].shape[0] >= s.n && in[t + 2].shape[0] >= s.n,
+              "tables [seqs, entries], cu_seqlens_q [seqs+1], kv_lens [seqs]");
+      s.stride = int32_t(in[t].shape[1]);
+      require(int64_t(s.stride) * s.block_size <= (int64_t(1) << 20), "max_context above 1M");
+      s.max_ctx = s.stride * s.block_size;
+      check_tensor(in[t + 3], BF, R, 2);
+      check_tensor(in[t + 4], BF, R, 2);
+      s.n_sinks = int32_t(in[t + 3].shape[0]);
+      require(in[t + 3].shape[1] == 576 && in[t + 4].shape[0] == s.n_sinks &&
+                  in[t + 4].shape[1] == 512 && s.n_sinks <= 128,
+              "sinks: keys [n <= 128, 576], values [n, 512]");
+      check_tensor(out[0], BF, W, 3);
+      require(out[0].shape[0] == s.total_q && out[0].shape[1] == s.q_heads && out[0].shape[2] == 512,
+              "out must be [rows, heads, 512]");
+      s.window = s.op == kMlaWindow512 ? 512 : (s.op == kMlaWindow2048 ? 2048 : 0);
+      s.scale = 1.0f / std::sqrt(192.0f);
+      s.workspace = ifattn_mla_attention_workspace_size(s.total_q, s.q_heads, s.max_ctx, s.window,
+                                                        s.topk, s.n_sinks, s.block_size);
+      return;
+    }
     default:
       require(false, "unknown operator");
   }
@@ -348,6 +400,20 @@ int32_t enqueue(void *state, void *workspace, uint64_t bytes, void *stream) {
                                               in[4].data, s->slot_dtype, s->rows, 1e-5f,
                                               out[0].data, s->op == kMlaNormRopeC8 ? 1 : 0,
                                               s->num_slots, stream);
+    case kMlaWindow512:
+    case kMlaWindow2048:
+      return ifattn_mla_window_attention_bf16(
+          in[0].data, in[1].data, static_cast<const int32_t *>(in[2].data), s->stride,
+          static_cast<const int32_t *>(in[3].data), static_cast<const int32_t *>(in[4].data), s->n,
+          s->total_q, s->window, in[5].data, in[6].data, s->n_sinks, out[0].data, s->q_heads,
+          s->block_size, s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
+    case kMlaSparseC8:
+      return ifattn_mla_sparse_attention_c8(
+          in[0].data, in[1].data, static_cast<const int32_t *>(in[2].data), s->topk,
+          static_cast<const int32_t *>(in[3].data), s->stride,
+          static_cast<const int32_t *>(in[4].data), static_cast<const int32_t *>(in[5].data), s->n,
+          s->total_q, in[6].data, in[7].data, s->n_sinks, out[0].data, s->q_heads, s->block_size,
+          s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
     default:
       return ifattn::fail(IFATTN_EINVAL, "enqueue: unknown operator");
   }
@@ -360,8 +426,10 @@ IFKernelV1 table() {
   return IFKernelV1{sizeof(IFKernelV1), 2, kContract[OP], kTarget, &prepare<OP>, &enqueue, &release};
 }
 
-const IFKernelV1 kTables[kOpCount] = {table<0>(), table<1>(), table<2>(), table<3>(), table<4>(),
-                                      table<5>(), table<6>(), table<7>(), table<8>(), table<9>()};
+const IFKernelV1 kTables[kOpCount] = {table<0>(),  table<1>(),  table<2>(), table<3>(),
+                                      table<4>(),  table<5>(),  table<6>(), table<7>(),
+                                      table<8>(),  table<9>(),  table<10>(), table<11>(),
+                                      table<12>()};
 
 }  // namespace
 

@@ -14,6 +14,9 @@ const char *const kContracts[] = {
     "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
     "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
     "inferfabric.mla_norm_rope_cache.bf16.v2", "inferfabric.mla_norm_rope_cache.c8.v2",
+    "inferfabric.mla_window_attention.w512.bf16.v2",
+    "inferfabric.mla_window_attention.w2048.bf16.v2",
+    "inferfabric.mla_sparse_attention.c8.v2",
 };
 }
 

@@ -201,3 +201,30 @@ def test_norm_rope_write_prepare():
     st, p = _prepare(k, *ports(width=576, cache_dtype=2))
     assert st == 0
     k.release(p.state)
+
+
+def test_mla_attention_prepare():
+    so, entry = load_plugin("mla_sparse_attention_c8")
+    k = entry(2).contents
+
+    def ports(rows=5, heads=6, topk=512, sinks=128, width=656):
+        ins = [tensor([rows, heads, 576], 2, 1), tensor([64, 32, width], 1, 1),
+               tensor([rows, topk], 4, 1), tensor([2, 32], 4, 1), tensor([3], 4, 1),
+               tensor([2], 4, 1), tensor([sinks, 576], 2, 1), tensor([sinks, 512], 2, 1)]
+        return ins, [tensor([rows, heads, 512], 2, 2)]
+
+    st, p = _prepare(k, *ports())
+    lib = _native.lib()
+    assert st == 0 and p.workspace_bytes == lib.ifattn_mla_attention_workspace_size(5, 6, 1024, 0, 512, 128, 32)
+    k.release(p.state)
+    assert _prepare(k, *ports(sinks=129))[0] != 0     # at most 128 sink rows
+    assert _prepare(k, *ports(width=576))[0] != 0     # C8 rows are 656 bytes
+    assert _prepare(k, *ports(heads=17))[0] != 0
+    so, entry = load_plugin("mla_window_attention_w2048_bf16")
+    k = entry(2).contents
+    ins = [tensor([4, 16, 576], 2, 1), tensor([64, 16, 576], 2, 1), tensor([1, 4096], 4, 1),
+           tensor([2], 4, 1), tensor([1], 4, 1), tensor([128, 576], 2, 1), tensor([128, 512], 2, 1)]
+    st, p = _prepare(k, ins, [tensor([4, 16, 512], 2, 2)])
+    assert st == 0
+    assert p.workspace_bytes == lib.ifattn_mla_attention_workspace_size(4, 16, 65536, 2048, 0, 128, 16)
+    k.release(p.state)

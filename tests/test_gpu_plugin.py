@@ -86,3 +86,55 @@ def test_plugin_mla_c8_write_and_decode():
     out2 = ops.mla_decode(q, cache2, tables, lens, tables.shape[1] * 64, 1.0 / np.sqrt(192.0))
     torch.cuda.synchronize()
     assert torch.equal(out1, out2)
+
+
+def test_plugin_norm_rope_write_and_attention_contracts():
+    """Fused writer (C8), sparse C8 attention with sinks and the w512 window
+    contract, each against the direct call."""
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(21)
+    rows, nslots = 64, 2048
+    x = to_dev(W.bf16_randn(rng, (rows, 576)))
+    g = to_dev(W.bf16_randn(rng, (512,)))
+    cs, sn = to_dev(W.bf16_randn(rng, (rows, 64))), to_dev(W.bf16_randn(rng, (rows, 64)))
+    slots = torch.from_numpy(rng.permutation(nslots)[:rows].astype(np.int64)).cuda()
+    c1 = torch.zeros((nslots // 32, 32, 656), dtype=torch.int8, device="cuda")
+    c2 = torch.zeros((nslots // 32, 32, 656), dtype=torch.uint8, device="cuda")
+    run("mla_norm_rope_cache_c8", [(x, 1), (g, 1), (cs, 1), (sn, 1), (slots, 1)], [(c1, 3)])
+    ops.mla_norm_rope_cache_write(x, g, cs, sn, c2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(c1.view(torch.uint8), c2)
+
+    # sparse C8 attention over the written cache: 2 sequences, 3 + 2 rows
+    pool = W.bf16_randn(rng, (nslots, 576), std=0.5)
+    ops.mla_cache_write_c8(to_dev(pool), c2, torch.arange(nslots, dtype=torch.int64, device="cuda"))
+    table = torch.from_numpy(rng.permutation(64).astype(np.int32).reshape(2, 32)).cuda()
+    cu = torch.tensor([0, 3, 5], dtype=torch.int32, device="cuda")
+    kv = torch.tensor([900, 400], dtype=torch.int32, device="cuda")
+    topk = 512
+    idx = np.full((5, topk), -1, np.int32)
+    for t, causal in enumerate([898, 899, 900, 399, 400]):
+        n = min(causal, topk)
+        idx[t, :n] = rng.choice(causal, n, replace=False)
+    idx = torch.from_numpy(idx).cuda()
+    q = to_dev(W.bf16_randn(rng, (5, 6, 576), std=0.5))
+    sk, sv = to_dev(W.bf16_randn(rng, (128, 576))), to_dev(W.bf16_randn(rng, (128, 512)))
+    o1 = torch.empty((5, 6, 512), dtype=torch.bfloat16, device="cuda")
+    run("mla_sparse_attention_c8", [(q, 1), (c2.view(torch.int8), 1), (idx, 1), (table, 1), (cu, 1),
+                                    (kv, 1), (sk, 1), (sv, 1)], [(o1, 2)])
+    o2 = ops.mla_attention(q, c2, table, kv, 1024, cu_seqlens=cu, indices=idx, sink_keys=sk,
+                           sink_values=sv)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+    # w512 window over a bf16 cache with 16-token pages
+    cb = to_dev(pool).view(nslots // 16, 16, 576)
+    table16 = torch.from_numpy(rng.permutation(128).astype(np.int32).reshape(2, 64)).cuda()
+    o3 = torch.empty_like(o1)
+    run("mla_window_attention_w512_bf16", [(q, 1), (cb, 1), (table16, 1), (cu, 1), (kv, 1), (sk, 1),
+                                           (sv, 1)], [(o3, 2)])
+    o4 = ops.mla_attention(q, cb, table16, kv, 1024, cu_seqlens=cu, window=512, sink_keys=sk,
+                           sink_values=sv)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, o4)
