@@ -72,6 +72,25 @@ int32_t ifattn_sequence_batch_make(const ifattn_sequence_slice *slices, uint64_t
                                    uint32_t *sample_rows, uint32_t *sample_residents,
                                    uint64_t *rows, uint64_t *samples);
 
+/* Sliding-window page ring (SlidingWindowLayout, native/include/sliding_window_layout.h:9-33):
+ * a window of `window` tokens whose chunk of `chunk` rows is written before it
+ * is queried keeps physical_pages pages of page_tokens tokens; the block table
+ * has table_entries absolute logical pages, logical page l -> ring page
+ * l % physical_pages. Rejects a zero argument, chunk > context and overflow. */
+int32_t ifattn_window_layout(uint32_t context, uint32_t window, uint32_t chunk,
+                             uint32_t page_tokens, uint32_t *physical_pages,
+                             uint32_t *table_entries);
+/* Block-table row [table_entries]: ring page ids, or owned[ring page] when the
+ * resident owns `owned` (physical_pages distinct ids). */
+int32_t ifattn_window_table(uint32_t context, uint32_t window, uint32_t chunk,
+                            uint32_t page_tokens, const int32_t *owned, uint64_t owned_count,
+                            int32_t *table);
+/* Physical token row of each absolute position (the append of
+ * sliding_window_layout.h:28-31 through the same page ids as the table). */
+int32_t ifattn_window_slots(uint32_t context, uint32_t window, uint32_t chunk,
+                            uint32_t page_tokens, const int32_t *owned, uint64_t owned_count,
+                            const uint32_t *positions, uint64_t count, int64_t *slots);
+
 #ifdef __cplusplus
 }
 #endif

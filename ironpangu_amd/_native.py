@@ -71,6 +71,9 @@ SIGNATURES = {
     "ifattn_pages_batch_table": (i32, [vp, pi32, u64, u32, i32, pi32]),
     "ifattn_pages_copy_plan": (i32, [vp, u32, u32, u32, i32, u64, pu64, u64, pu64]),
     "ifattn_page_spans": (i32, [pi32, u64, u64, u64, pu64, u64, pu64]),
+    "ifattn_window_layout": (i32, [u32, u32, u32, u32, pu32, pu32]),
+    "ifattn_window_table": (i32, [u32, u32, u32, u32, pi32, u64, pi32]),
+    "ifattn_window_slots": (i32, [u32, u32, u32, u32, pi32, u64, pu32, u64, pi64]),
     "ifattn_sequence_batch_make": (i32, [C.POINTER(SequenceSlice), u64, u32, u32, u32, u64, pi32,
                                          pi32, pi32, pi32, pi32, pi32, pi32, pi64, pu32, pu32,
                                          pu64, pu64]),

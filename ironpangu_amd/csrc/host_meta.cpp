@@ -181,3 +181,49 @@ extern "C" int32_t ifattn_sequence_batch_make(
     if (samples) *samples = b.sample_rows.size();
   });
 }
+
+extern "C" int32_t ifattn_window_layout(uint32_t context, uint32_t window, uint32_t chunk,
+                                        uint32_t page_tokens, uint32_t *physical_pages,
+                                        uint32_t *table_entries) {
+  return guarded([&] {
+    const ifattn::host::WindowRing ring(context, window, chunk, page_tokens);
+    if (physical_pages) *physical_pages = ring.pages;
+    if (table_entries) *table_entries = ring.entries();
+  });
+}
+
+extern "C" int32_t ifattn_window_table(uint32_t context, uint32_t window, uint32_t chunk,
+                                       uint32_t page_tokens, const int32_t *owned,
+                                       uint64_t owned_count, int32_t *table) {
+  return guarded([&] {
+    const ifattn::host::WindowRing ring(context, window, chunk, page_tokens);
+    require(table != nullptr, "null table output");
+    require(owned == nullptr || owned_count == ring.pages, "owned pages must number the ring pages");
+    if (owned) {
+      require(!ifattn::host::has_duplicates(std::vector<int32_t>(owned, owned + owned_count)),
+              "owned pages alias");
+      for (uint64_t i = 0; i < owned_count; ++i) require(owned[i] >= 0, "negative page id");
+    }
+    for (uint32_t l = 0; l < ring.entries(); ++l) {
+      const uint32_t ph = ring.physical_page(l);
+      table[l] = owned ? owned[ph] : int32_t(ph);
+    }
+  });
+}
+
+extern "C" int32_t ifattn_window_slots(uint32_t context, uint32_t window, uint32_t chunk,
+                                       uint32_t page_tokens, const int32_t *owned,
+                                       uint64_t owned_count, const uint32_t *positions,
+                                       uint64_t count, int64_t *slots) {
+  return guarded([&] {
+    const ifattn::host::WindowRing ring(context, window, chunk, page_tokens);
+    require(slots != nullptr && (positions != nullptr || count == 0), "null slot argument");
+    require(owned == nullptr || owned_count == ring.pages, "owned pages must number the ring pages");
+    for (uint64_t i = 0; i < count; ++i) require(positions[i] < context, "sliding append bounds");
+    for (uint64_t i = 0; i < count; ++i) {
+      const uint32_t s = ring.slot(positions[i]);
+      const uint32_t ph = s / page_tokens;
+      slots[i] = int64_t(owned ? owned[ph] : int32_t(ph)) * page_tokens + s % page_tokens;
+    }
+  });
+}

@@ -7,6 +7,7 @@
 //  * ResidentPageTable ~ ResidentPages (native/src/page_binding.h:65-188)
 //  * PackedBatch  ~ SequenceBatch::make (native/include/sequence_batch.h:23-59)
 //  * coalesce_page_spans ~ page_spans (native/src/page_binding.h:19-35)
+//  * WindowRing   ~ SlidingWindowLayout (native/include/sliding_window_layout.h:9-33)
 // Every mutating call validates its whole input before changing state, so a
 // rejected update leaves the previous mapping intact (page_binding_test.cpp:17-22).
 #pragma once
@@ -45,6 +46,37 @@ inline std::vector<Span> coalesce_page_spans(std::vector<int32_t> pages, uint64_
   }
   return out;
 }
+
+// Page ring of a sliding-window cache whose chunk writes precede the chunk's
+// queries: the window plus the later rows of a chunk span window + chunk - 1
+// tokens, which can touch one page more than they fill, so that many physical
+// pages (never more than the context needs) hold every live row. Block-table
+// entries stay absolute logical pages; logical page l lives in physical page
+// l % pages, so the attention kernels read the window through an ordinary table.
+class WindowRing {
+ public:
+  uint32_t context, window, chunk, page_tokens, pages;
+  WindowRing(uint32_t c, uint32_t w, uint32_t q, uint32_t p)
+      : context(c), window(w), chunk(q), page_tokens(p), pages(0) {
+    if (c == 0 || w == 0 || q == 0 || p == 0 || q > c)
+      throw std::runtime_error("invalid sliding window layout");
+    const uint64_t span = uint64_t(w) + q - 1;       // tokens live at once
+    uint64_t need = (span + p - 2) / p + 1;           // pages such a span can touch
+    const uint64_t all = (uint64_t(c) + p - 1) / p;   // pages of the whole context
+    need = need < all ? need : all;
+    if (need * p > UINT32_MAX) throw std::runtime_error("sliding window capacity overflow");
+    pages = uint32_t(need);
+  }
+  uint32_t entries() const { return uint32_t((uint64_t(context) + page_tokens - 1) / page_tokens); }
+  uint32_t physical_page(uint32_t logical) const {
+    if (logical >= entries()) throw std::runtime_error("sliding page bounds");
+    return logical % pages;
+  }
+  uint32_t slot(uint32_t position) const {
+    if (position >= context) throw std::runtime_error("sliding append bounds");
+    return physical_page(position / page_tokens) * page_tokens + position % page_tokens;
+  }
+};
 
 // True when `ids` names some value twice (sort-based, no allocation sized by
 // the id range).

@@ -119,6 +119,57 @@ def page_spans(pages, page_bytes: int, field_bytes: int) -> list:
     return [(int(buf[2 * i]), int(buf[2 * i + 1])) for i in range(n.value)]
 
 
+class WindowLayout:
+    """Page ring of a sliding-window cache
+    (native/include/sliding_window_layout.h:9-33): ``physical_pages`` pages
+    hold the window plus a chunk of rows written before they are queried; the
+    block table keeps absolute logical pages, logical page l -> ring page
+    l % physical_pages. ``owned`` optionally names the resident's page ids
+    (one per ring page), as a ResidentPages ring table does."""
+
+    def __init__(self, context: int, window: int, chunk: int, page_tokens: int):
+        pages, entries = C.c_uint32(), C.c_uint32()
+        _check(lib().ifattn_window_layout(context, window, chunk, page_tokens, C.byref(pages),
+                                          C.byref(entries)))
+        self.context, self.window, self.chunk, self.page_tokens = context, window, chunk, page_tokens
+        self.physical_pages, self.table_entries = pages.value, entries.value
+
+    def _owned(self, owned):
+        if owned is None:
+            return None, None, 0
+        a, p = _i32(owned)
+        return a, p, a.size
+
+    def table(self, owned=None) -> np.ndarray:
+        keep, p, n = self._owned(owned)
+        out = np.zeros(self.table_entries, np.int32)
+        _check(lib().ifattn_window_table(self.context, self.window, self.chunk, self.page_tokens,
+                                         p, n, out.ctypes.data_as(C.POINTER(C.c_int32))))
+        return out
+
+    def slots(self, positions, owned=None) -> np.ndarray:
+        keep, p, n = self._owned(owned)
+        pos = np.ascontiguousarray(positions, dtype=np.uint32)
+        out = np.zeros(pos.size, np.int64)
+        _check(lib().ifattn_window_slots(self.context, self.window, self.chunk, self.page_tokens,
+                                         p, n, pos.ctypes.data_as(C.POINTER(C.c_uint32)), pos.size,
+                                         out.ctypes.data_as(C.POINTER(C.c_int64))))
+        return out
+
+    def physical_page(self, logical: int) -> int:
+        if logical < 0 or logical >= self.table_entries:
+            raise MetadataError("sliding page bounds")
+        return logical % self.physical_pages
+
+    def append(self, position: int) -> int:
+        return int(self.slots([position])[0]) if 0 <= position < self.context else \
+            _raise("sliding append bounds")
+
+
+def _raise(msg):
+    raise MetadataError(msg)
+
+
 @dataclass
 class SequenceBatch:
     """Packed varlen layout (native/include/sequence_batch.h:15-59); ``starts``

@@ -103,4 +103,20 @@ int ref_sequence_batch(const RefSlice *sl, uint64_t n, uint32_t cap, uint32_t bu
     *samples = b.sample_rows.size();
   });
 }
+
+int ref_window_layout(uint32_t context, uint32_t window, uint32_t chunk, uint32_t page,
+                      uint32_t *pages, uint32_t *entries) {
+  return guarded([&] {
+    inferfabric::state::SlidingWindowLayout l(context, window, chunk, page);
+    *pages = l.physical_pages;
+    *entries = l.table_entries();
+  });
+}
+int ref_window_append(uint32_t context, uint32_t window, uint32_t chunk, uint32_t page,
+                      uint32_t position, uint32_t *slot) {
+  return guarded([&] {
+    inferfabric::state::SlidingWindowLayout l(context, window, chunk, page);
+    *slot = l.append(position);
+  });
+}
 }

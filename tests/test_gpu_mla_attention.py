@@ -48,10 +48,12 @@ def sinks(n, seed):
 
 @pytest.mark.parametrize("rows", [1, 4, 16])
 def test_window_ring_probe(rows):
+    from ironpangu_amd.host import WindowLayout
     window, page = 512, 16
     chunk = max(rows, 4)
-    pages = (window + chunk - 1 + page - 2) // page + 1
-    table = (np.arange(65536 // page) % pages).astype(np.int32)[None, :]
+    lay = WindowLayout(65536, window, chunk, page)  # sliding_window_probe.cpp:85
+    pages = lay.physical_pages
+    table = lay.table()[None, :]
     hq = bf(((np.arange(rows * 6 * 512) * 7) % 97 - 48).astype(f32) / f32(128)).reshape(rows, 6, 512)
     hqr = bf(((np.arange(rows * 6 * 64) * 11) % 89 - 44).astype(f32) / f32(128)).reshape(rows, 6, 64)
     hs = bf(((np.arange(128 * 512) * 19) % 103 - 51).astype(f32) / f32(128)).reshape(128, 512)
@@ -62,7 +64,7 @@ def test_window_ring_probe(rows):
         cache = np.full((pages * page, 576), bf([4.0])[0], np.uint16)  # poison outside the window
         pos = np.arange(max(0, start - window + 1), start + chunk)
         d = np.arange(576)
-        cache[table[0, pos // page] * page + pos % page] = bf(
+        cache[lay.slots(pos)] = bf(
             ((pos[:, None] * 17 + d[None, :] * 13) % 101 - 50).astype(f32) / f32(128))
         got, exp = run(q, cache.reshape(pages, page, 576), table, [start + rows], 65536,
                        cu=[0, rows], window=window, sk=sk, sv=hs)
