@@ -342,6 +342,138 @@ def bench_mixed(seed, steps, warmup):
     return res
 
 
+def bench_mla_rows(seed, steps, warmup, sparse):
+    """MLA attention over query rows with 128 learned sinks: 128 decode rows,
+    contexts U[4096, 65536], 16 heads. BF16 rows over a 2048-token window
+    (16-token pages), or packed C8 rows over top-2048 causal candidate lists
+    (32-token pages) gathered at random."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    rng = np.random.default_rng(seed + 11)
+    n, heads, topk, window = 128, 16, 2048, 2048
+    bs = 32 if sparse else 16
+    lens = rng.integers(4096, 65537, n).astype(np.int32)
+    ctx = 65536
+    if sparse:
+        need = (lens.astype(np.int64) + bs - 1) // bs
+        pool = int(need.sum())
+        table = W.block_tables_for(rng, lens, bs, pool, ctx // bs)
+    else:
+        # ring of the last window + 1 pages per sequence (sliding_window_layout.h)
+        from ironpangu_amd.host import WindowLayout
+        lay = WindowLayout(ctx, window, 1, bs)
+        pool = n * lay.physical_pages
+        table = np.stack([lay.table(np.arange(lay.physical_pages) + s * lay.physical_pages)
+                          for s in range(n)]).astype(np.int32)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 12)
+    row = 656 if sparse else 576
+    if sparse:
+        cache = torch.empty((pool, bs, 656), dtype=torch.uint8, device=dev)
+        src = torch.empty((1 << 16, 576), dtype=torch.bfloat16, device=dev)
+        for r0 in range(0, pool * bs, 1 << 16):
+            fill_randn(src, g, std=0.5)
+            m = min(1 << 16, pool * bs - r0)
+            ops.mla_cache_write_c8(src[:m], cache, torch.arange(r0, r0 + m, dtype=torch.int64, device=dev))
+        idx = torch.empty((n, topk), dtype=torch.int32, device=dev)
+        for i in range(n):  # distinct random causal candidates
+            idx[i] = torch.randperm(int(lens[i]), generator=g, device=dev)[:topk].to(torch.int32)
+    else:
+        cache = torch.empty((pool, bs, 576), dtype=torch.bfloat16, device=dev)
+        fill_randn(cache, g, std=0.5)
+        idx = None
+    q = (torch.randn((n, heads, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    sk = (torch.randn((128, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    sv = (torch.randn((128, 512), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    tables = torch.from_numpy(table).to(dev)
+    kv = torch.from_numpy(lens).to(dev)
+    out = torch.empty((n, heads, 512), dtype=torch.bfloat16, device=dev)
+    nws = ops.lib().ifattn_mla_attention_workspace_size(n, heads, ctx, 0 if sparse else window,
+                                                        topk if sparse else 0, 128, bs)
+    ws = torch.empty(int(nws), dtype=torch.uint8, device=dev)
+
+    def attn():
+        ops.mla_attention(q, cache, tables, kv, ctx, indices=idx, window=0 if sparse else window,
+                          sink_keys=sk, sink_values=sv, out=out, workspace=ws)
+
+    ms = timed(attn, steps, warmup)
+    keys = n * (topk if sparse else window)
+    nbytes = keys * row + n * heads * (576 + 512) * 2 + 128 * (576 + 512) * 2 + \
+        (keys * 4 if sparse else n * ((window + bs - 1) // bs + 1) * 4)
+    name = ("C8 sparse top-2048 MLA attention + 128 sinks" if sparse
+            else "BF16 window-2048 MLA attention (ring pages) + 128 sinks")
+    res = {"workload": f"{name}, 128 decode rows, 16 heads", "value": round(nbytes / ms / 1e6, 2),
+           "unit": "GB/s", "ms_per_call": round(ms, 5), "keys_per_call": keys,
+           "roofline": {"bound": "hbm", "kernel": "mla_attention operator (plan, attention, merge)",
+                        "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes}}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_slot_reuse(seed, steps, warmup):
+    """Slot reuse on a 2 GiB page field (20992-byte pages, the packed C8 MLA
+    page): state copy of 1 GiB of pages from one resident to another (read +
+    write) and the page reset (zeroing) of 1 GiB of owned spans."""
+    import torch
+    from ironpangu_amd import ops
+    page = 32 * 656
+    n_pages = (2 << 30) // page
+    field = torch.zeros(n_pages * page, dtype=torch.uint8, device="cuda")
+    half = n_pages // 2
+    rng = np.random.default_rng(seed)
+    src = rng.permutation(half)
+    plan = np.stack([src * page, (half + np.arange(half)) * page, np.full(half, page)], 1)
+    ranges = torch.from_numpy(plan.astype(np.int64)).cuda()
+    from ironpangu_amd.host import page_spans
+    spans = torch.from_numpy(np.array(page_spans(rng.permutation(n_pages)[:half].astype(np.int32),
+                                                 page, n_pages * page), np.int64)).cuda()
+    ms_copy = timed(lambda: ops.state_copy(field, ranges), steps, warmup)
+    ms_reset = timed(lambda: ops.page_reset(field, spans), steps, warmup)
+    copy_b = 2 * half * page
+    reset_b = half * page
+    res = {"workload": "state copy (1 GiB of 20992-byte pages) and page reset (1 GiB of spans)",
+           "value": round(copy_b / ms_copy / 1e6, 2), "unit": "GB/s (copy, read + write)",
+           "ms_copy": round(ms_copy, 5), "ms_reset": round(ms_reset, 5),
+           "reset_gbps": round(reset_b / ms_reset / 1e6, 2),
+           "roofline": {"bound": "hbm", "kernel": "state_span_kernel<copy>",
+                        "achieved": round(copy_b / ms_copy / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(copy_b / ms_copy / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms_copy, 5), "algorithmic_bytes": copy_b}}
+    del field
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_norm_rope_write(seed, steps, warmup):
+    """Fused MLA cache writer at the reference's batch bound: 4096 rows of 576
+    bf16 -> packed C8 rows at random slots of a 65536-row cache."""
+    import torch
+    from ironpangu_amd import ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 13)
+    rows = 4096
+    x = torch.randn((rows, 576), generator=g, device="cuda").to(torch.bfloat16)
+    gamma = torch.randn(512, generator=g, device="cuda").to(torch.bfloat16)
+    cs = torch.randn((rows, 64), generator=g, device="cuda").to(torch.bfloat16)
+    sn = torch.randn((rows, 64), generator=g, device="cuda").to(torch.bfloat16)
+    cache = torch.zeros((2048, 32, 656), dtype=torch.uint8, device="cuda")
+    slots = torch.randperm(65536, generator=g, device="cuda")[:rows]
+    ms = timed(lambda: ops.mla_norm_rope_cache_write(x, gamma, cs, sn, cache, slots), steps, warmup)
+    nbytes = rows * (1152 + 2 * 128 + 8 + 656) + 1024
+    return {"workload": "fused RMSNorm + rope + C8 MLA cache write, 4096 rows",
+            "value": round(rows / ms * 1e3, 1), "unit": "rows/s", "ms_per_call": round(ms, 5),
+            "roofline": {"bound": "hbm", "kernel": "mla_norm_rope_write_kernel",
+                         "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                         "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes,
+                         "note": "launch-bound at this size (8.5 MB per call)"}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -432,7 +564,7 @@ def main():
         "tokens_per_s": round(case.num_seqs / (ms_step * 1e-3), 1),
         "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_step": nbytes["total"],
-        "roofline": {"bound": "hbm", "kernel": "paged_decode_step operator (prologue: plan + row writes; decode with fused split-K merge)",
+        "roofline": {"bound": "hbm", "kernel": "paged_decode_step operator (prologue: plan + row writes; decode; split-K merge)",
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "traffic_note": "HBM bytes per decode-kernel launch, rocprofv3 FETCH_SIZE x2.0 + "
@@ -447,7 +579,11 @@ def main():
         torch.cuda.empty_cache()
         res["secondary"] = {"c8_decode": bench_c8(args.seed, args.steps, args.warmup),
                             "mla_decode": bench_mla(args.seed, args.steps, args.warmup),
-                            "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup)}
+                            "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup),
+                            "mla_window_attention": bench_mla_rows(args.seed, args.steps, args.warmup, False),
+                            "mla_sparse_attention": bench_mla_rows(args.seed, args.steps, args.warmup, True),
+                            "slot_reuse": bench_slot_reuse(args.seed, args.steps, args.warmup),
+                            "norm_rope_write": bench_norm_rope_write(args.seed, args.steps, args.warmup)}
     print(json.dumps(res), flush=True)
 
 

@@ -192,6 +192,22 @@ int32_t ifattn_mla_decode_c8(const void *q, const void *cache, const int32_t *bl
                              int64_t num_blocks, int32_t max_context, float scale,
                              void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* ---- resident slot reuse: page reset and state copy --------------------------- */
+
+/* Zero the {offset, bytes} spans (uint64 pairs in DEVICE memory, as produced by
+ * ifattn_page_spans) of a device state field of field_bytes bytes: the reset of
+ * a resident's owned pages before reuse (native/src/page_binding.h:19-35).
+ * Spans outside the field are skipped. */
+int32_t ifattn_page_reset(void *field, uint64_t field_bytes, const uint64_t *spans,
+                          uint64_t count, void *stream);
+/* Copy the {source, destination, bytes} ranges (uint64 triples in DEVICE
+ * memory, as produced by ifattn_pages_copy_plan) inside one device state field:
+ * a resident's completed pages to another slot (page_binding.h:161-187).
+ * Ranges must not overlap one another or themselves (the plan guarantees it);
+ * ranges outside the field are skipped. */
+int32_t ifattn_state_copy(void *field, uint64_t field_bytes, const uint64_t *ranges,
+                          uint64_t count, void *stream);
+
 /* ---- packed-MLA attention over query rows (windows, sparse lists, sinks) ----- */
 
 /* Rows: sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) (NULL:

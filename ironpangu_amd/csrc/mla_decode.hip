@@ -42,6 +42,7 @@ constexpr int kMlaWaves = 4;
 constexpr int kMlaTile = 32;
 constexpr int kSparsePart = 1024;  // index-list entries per sparse partition
 constexpr int kMaxSinks = 128;
+inline int wgs_mla() { return 1; }  // persistent workgroups per CU (LDS-bound)
 
 struct MlaParams {
   const uint16_t *q;            // [rows, heads, 576]
@@ -230,6 +231,119 @@ __device__ __forceinline__ u32x4 mla_i8x8(uint32_t lo, uint32_t hi) {
                mla_i8pair(mla_i8(hi, 0), mla_i8(hi, 1)), mla_i8pair(mla_i8(hi, 2), mla_i8(hi, 3))};
 }
 
+// Scores, online softmax and PV of one 32-key tile, from the operands already
+// in registers: k = keys 16mt + c of the wave's dims (+ rope), v = keys
+// tile_token(g, j) of the wave's 128 latent dims, sk = C8 tile scales of those
+// keys. The four waves' partial scores are summed through xbuf (one barrier;
+// every wave finished reading xbuf before the barrier that began this tile).
+// Keys whose bit is clear in `live` get probability 0.
+struct MlaAcc {
+  f32x4 o[8];
+  float m, l;
+};
+
+template <bool C8>
+__device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5], const u32x4 (&v)[8],
+                                              const float *sk, const u32x4 (&qv)[5],
+                                              float (*xbuf)[8], uint32_t live, float scale_log2,
+                                              int w, int lane) {
+  const int g = lane >> 4;
+  f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if constexpr (C8) {
+      a0 = mfma16x16x32(mla_i8x8(k[0][s][0], k[0][s][1]), qv[s], a0);
+      a1 = mfma16x16x32(mla_i8x8(k[1][s][0], k[1][s][1]), qv[s], a1);
+    } else {
+      a0 = mfma16x16x32(k[0][s], qv[s], a0);
+      a1 = mfma16x16x32(k[1][s], qv[s], a1);
+    }
+  }
+  float part_s[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    part_s[r] = a0[r];
+    part_s[4 + r] = a1[r];
+  }
+  if constexpr (C8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part_s[j] *= sk[j];
+  }
+  if (w < 2) {
+    f32x4 r0 = mfma16x16x32(k[0][4], qv[4], f32x4{0, 0, 0, 0});
+    f32x4 r1 = mfma16x16x32(k[1][4], qv[4], f32x4{0, 0, 0, 0});
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      part_s[r] += r0[r];
+      part_s[4 + r] += r1[r];
+    }
+  }
+  // Sum the four waves' partial scores. The buffer is free again: every wave
+  // finished reading it before the barrier that starts this tile.
+  *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
+  *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
+  __syncthreads();
+  float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < kMlaWaves; ++u) {
+    const f32x4 lo = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][0]);
+    const f32x4 hi = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][4]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] += lo[r];
+      x[4 + r] += hi[r];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] *= scale_log2;
+  if (live != 0xFFFFFFFFu) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (live >> mla_tile_token(g, j)) & 1u ? x[j] : -INFINITY;
+  }
+  float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+  tmax = wave_max_xor(tmax, 16);
+  tmax = wave_max_xor(tmax, 32);
+  if (__any(tmax > acc.m + 8.0f)) {
+    const float m_new = fmaxf(acc.m, tmax);
+    const float alpha = fast_exp2(acc.m - m_new);
+    acc.m = m_new;
+    acc.l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+  }
+  float pr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(x[j] - acc.m);
+  acc.l += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+  if constexpr (C8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pr[j] *= sk[j];
+  }
+  const u32x4 pb = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                    pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    u32x4 a;
+    if constexpr (C8) {
+      const int wd = b >> 2, y = b & 3;
+      a = u32x4{mla_i8pair(mla_i8(v[0][wd], y), mla_i8(v[1][wd], y)),
+                mla_i8pair(mla_i8(v[2][wd], y), mla_i8(v[3][wd], y)),
+                mla_i8pair(mla_i8(v[4][wd], y), mla_i8(v[5][wd], y)),
+                mla_i8pair(mla_i8(v[6][wd], y), mla_i8(v[7][wd], y))};
+    } else {
+      const int wd = b >> 1;
+      if (b & 1)
+        a = u32x4{pack_hi16(v[0][wd], v[1][wd]), pack_hi16(v[2][wd], v[3][wd]),
+                  pack_hi16(v[4][wd], v[5][wd]), pack_hi16(v[6][wd], v[7][wd])};
+      else
+        a = u32x4{pack_lo16(v[0][wd], v[1][wd]), pack_lo16(v[2][wd], v[3][wd]),
+                  pack_lo16(v[4][wd], v[5][wd]), pack_lo16(v[6][wd], v[7][wd])};
+    }
+    acc.o[b] = mfma16x16x32(a, pb, acc.o[b]);
+  }
+}
+
 // One (row, partition) item. Tiles of the partition go HBM -> LDS once by
 // direct-to-LDS loads shared by the four waves through a ring of R::STAGES
 // slots; every wave reads its K operand (keys in rows) and its V operand (dims
@@ -351,10 +465,11 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     }
   };
 
-  f32x4 oacc[8];
+  MlaAcc acc;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) oacc[i] = f32x4{0, 0, 0, 0};
-  float m_run = -INFINITY, l_run = 0.0f;
+  for (int i = 0; i < 8; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
+  acc.m = -INFINITY;
+  acc.l = 0.0f;
 
   auto compute = [&](const uint8_t *tile, int t0) {
     // Live rows of this tile (wave-uniform mask).
@@ -405,100 +520,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
     }
 
-    f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if constexpr (C8) {
-        a0 = mfma16x16x32(mla_i8x8(k[0][s][0], k[0][s][1]), qv[s], a0);
-        a1 = mfma16x16x32(mla_i8x8(k[1][s][0], k[1][s][1]), qv[s], a1);
-      } else {
-        a0 = mfma16x16x32(k[0][s], qv[s], a0);
-        a1 = mfma16x16x32(k[1][s], qv[s], a1);
-      }
-    }
-    float part_s[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      part_s[r] = a0[r];
-      part_s[4 + r] = a1[r];
-    }
-    if constexpr (C8) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) part_s[j] *= sk[j];
-    }
-    if (w < 2) {
-      f32x4 r0 = mfma16x16x32(k[0][4], qv[4], f32x4{0, 0, 0, 0});
-      f32x4 r1 = mfma16x16x32(k[1][4], qv[4], f32x4{0, 0, 0, 0});
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        part_s[r] += r0[r];
-        part_s[4 + r] += r1[r];
-      }
-    }
-    // Sum the four waves' partial scores. The buffer is free again: every wave
-    // finished reading it before the barrier that starts this tile.
-    *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
-    *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
-    __syncthreads();
-    float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int u = 0; u < kMlaWaves; ++u) {
-      const f32x4 lo = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][0]);
-      const f32x4 hi = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][4]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] += lo[r];
-        x[4 + r] += hi[r];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] *= p.scale_log2;
-    if (live != 0xFFFFFFFFu) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = (live >> mla_tile_token(g, j)) & 1u ? x[j] : -INFINITY;
-    }
-    float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
-    if (__any(tmax > m_run + 8.0f)) {
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) oacc[i] *= alpha;
-    }
-    float pr[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(x[j] - m_run);
-    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-    if constexpr (C8) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] *= sk[j];
-    }
-    const u32x4 pb = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                      pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      u32x4 a;
-      if constexpr (C8) {
-        const int wd = b >> 2, y = b & 3;
-        a = u32x4{mla_i8pair(mla_i8(v[0][wd], y), mla_i8(v[1][wd], y)),
-                  mla_i8pair(mla_i8(v[2][wd], y), mla_i8(v[3][wd], y)),
-                  mla_i8pair(mla_i8(v[4][wd], y), mla_i8(v[5][wd], y)),
-                  mla_i8pair(mla_i8(v[6][wd], y), mla_i8(v[7][wd], y))};
-      } else {
-        const int wd = b >> 1;
-        if (b & 1)
-          a = u32x4{pack_hi16(v[0][wd], v[1][wd]), pack_hi16(v[2][wd], v[3][wd]),
-                    pack_hi16(v[4][wd], v[5][wd]), pack_hi16(v[6][wd], v[7][wd])};
-        else
-          a = u32x4{pack_lo16(v[0][wd], v[1][wd]), pack_lo16(v[2][wd], v[3][wd]),
-                    pack_lo16(v[4][wd], v[5][wd]), pack_lo16(v[6][wd], v[7][wd])};
-      }
-      oacc[b] = mfma16x16x32(a, pb, oacc[b]);
-    }
+    mla_tile_math<C8>(acc, k, v, sk, qv, xbuf, live, p.scale_log2, w, lane);
   };
 
   // Ring: tile ti lives in slot ti % S. Tiles 0..S-2 are issued up front; the
@@ -518,7 +540,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     compute(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile);
   }
 
-  float l_tot = wave_sum_xor(l_run, 16);
+  float l_tot = wave_sum_xor(acc.l, 16);
   l_tot = wave_sum_xor(l_tot, 32);
   if (!head_live) return;
   // Lane holds rows m = 4g + r of MFMA b -> dim 128w + 8(4g + r) + b.
@@ -526,7 +548,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int b = 0; b < 8; ++b) ov[8 * r + b] = oacc[b][r];
+    for (int b = 0; b < 8; ++b) ov[8 * r + b] = acc.o[b][r];
   const int d0 = 128 * w + 32 * g;
   if (!partials) {
     const float inv = 1.0f / l_tot;
@@ -545,7 +567,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       *reinterpret_cast<f32x4 *>(po + 4 * k) = f32x4{ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]};
-    if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
+    if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
   }
 }
 
@@ -570,76 +592,103 @@ __global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaPar
   }
 }
 
-// Combine one (row, head): the learned sink rows (scores and values computed
-// here, each thread 2 output dims) and the row's partition partials.
+// Learned sink rows of one query row (keys [n, 576], values [n, 512] bf16,
+// shared by every row, so they are read from L2): the same tile math as the
+// cache keys, four waves per row, heads in the MFMA N dimension. The (m, l, O)
+// partial of the sinks alone goes to the row's last partial slot.
+__global__ __launch_bounds__(64 * kMlaWaves) void mla_sink_kernel(MlaParams p) {
+  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
+  const int row = blockIdx.x, lane = threadIdx.x & 63;
+  const int w = uniform(int(threadIdx.x >> 6));
+  const int c = lane & 15, g = lane >> 4, n = p.n_sinks;
+  const bool head_live = c < p.heads;
+  u32x4 qv[5];
+  {
+    const uint16_t *qp = p.q + (int64_t(row) * p.heads + (head_live ? c : 0)) * 576;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qv[s] = head_live ? load_u32x4(qp + 128 * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+    qv[4] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+  MlaAcc acc;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
+  acc.m = -INFINITY;
+  acc.l = 0.0f;
+  for (int t0 = 0; t0 < n; t0 += kMlaTile) {
+    const int live_n = n - t0 < kMlaTile ? n - t0 : kMlaTile;
+    // Rows past the last sink read as zero (buffer extent).
+    const auto rk = make_rsrc(p.sink_k + int64_t(t0) * 576, uint32_t(live_n) * 1152u);
+    const auto rv = make_rsrc(p.sink_v + int64_t(t0) * 512, uint32_t(live_n) * 1024u);
+    u32x4 k[2][5], v[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const uint32_t r = uint32_t(16 * mt + c) * 1152u;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) k[mt][s] = buf_load_x4(rk, r + 2 * (128 * w + 32 * s + 8 * g));
+      k[mt][4] = w < 2 ? buf_load_x4(rk, r + 1024 + 2 * (32 * (w & 1) + 8 * g)) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      v[j] = buf_load_x4(rv, uint32_t(mla_tile_token(g, j)) * 1024u + 2 * (128 * w + 8 * c));
+    const uint32_t live = live_n >= 32 ? 0xFFFFFFFFu : ((1u << live_n) - 1u);
+    mla_tile_math<false>(acc, k, v, nullptr, qv, xbuf, live, p.scale_log2, w, lane);
+    __syncthreads();  // xbuf is rewritten by the next tile
+  }
+  float l_tot = wave_sum_xor(acc.l, 16);
+  l_tot = wave_sum_xor(l_tot, 32);
+  if (!head_live) return;
+  const int64_t prow = (int64_t(row) * p.parts_per_row + p.parts_per_row - 1) * p.heads + c;
+  float *po = p.part_o + prow * 512 + 128 * w + 32 * g;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int r = (4 * k) / 8, b = (4 * k) % 8;  // ov index 4k -> row r, mfma b
+    *reinterpret_cast<f32x4 *>(po + 4 * k) =
+        f32x4{acc.o[b][r], acc.o[b + 1][r], acc.o[b + 2][r], acc.o[b + 3][r]};
+  }
+  if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
+}
+
+// Combine one (row, head): the row's partition partials and, with sinks, the
+// sink partial in the row's last slot. Each thread owns 2 output dims.
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
   const int np = mla_parts(sp, p.part_tokens);
   if (p.n_sinks == 0 && np <= 1) return;
-  __shared__ float qs[576];
-  __shared__ float sc[kMaxSinks];
-  float M = -INFINITY, L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  if (p.n_sinks > 0) {
-    const uint16_t *qp = p.q + (int64_t(row) * p.heads + h) * 576;
-    for (int i = tid; i < 576; i += 256) qs[i] = bf16_bits_to_f32(qp[i]);
-    __syncthreads();
-    const int i = tid >> 1, half = tid & 1;
-    float d = 0.0f;
-    if (i < p.n_sinks) {
-      const uint32_t *kp = reinterpret_cast<const uint32_t *>(p.sink_k + int64_t(i) * 576 + 288 * half);
-      const float *qh = qs + 288 * half;
-      for (int e = 0; e < 144; ++e) {
-        const uint32_t wv = kp[e];
-        d += qh[2 * e] * bf16_bits_to_f32(wv & 0xffffu) + qh[2 * e + 1] * bf16_bits_to_f32(wv >> 16);
-      }
-    }
-    d += __shfl_xor(d, 1, 64);
-    if (half == 0 && i < p.n_sinks) sc[i] = d * p.scale_log2;
-    __syncthreads();
-    for (int j = 0; j < p.n_sinks; ++j) M = fmaxf(M, sc[j]);
-    const uint32_t *vp = reinterpret_cast<const uint32_t *>(p.sink_v) + tid;
-    for (int j = 0; j < p.n_sinks; ++j) {
-      const float pj = fast_exp2(sc[j] - M);
-      L += pj;
-      const uint32_t wv = vp[int64_t(j) * 256];
-      o0 += pj * bf16_bits_to_f32(wv & 0xffffu);
-      o1 += pj * bf16_bits_to_f32(wv >> 16);
-    }
-  }
   const int64_t prow0 = int64_t(row) * p.parts_per_row * p.heads + h;
-  // Largest partition max: threads stride over the partitions, then a
+  auto part_at = [&](int k) {  // k == np: the sink slot
+    return prow0 + int64_t(k < np ? k : p.parts_per_row - 1) * p.heads;
+  };
+  const int total = np + (p.n_sinks > 0 ? 1 : 0);
+  // Largest partial max: threads stride over the partials, then a
   // workgroup reduction (4 waves).
   __shared__ float wmax[4];
   float mp = -INFINITY;
-  for (int k = tid; k < np; k += 256) mp = fmaxf(mp, p.part_ml[(prow0 + int64_t(k) * p.heads) * 2]);
+  for (int k = tid; k < total; k += 256) mp = fmaxf(mp, p.part_ml[part_at(k) * 2]);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mp = wave_max_xor(mp, m);
   if ((tid & 63) == 0) wmax[tid >> 6] = mp;
   __syncthreads();
-  mp = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  const float Mt = fmaxf(M, mp);
+  const float Mt = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  uint32_t *op = reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512) + tid;
   if (Mt == -INFINITY) {  // no keys and no sinks
-    reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512)[tid] = 0u;
+    *op = 0u;
     return;
   }
-  const float a = fast_exp2(M - Mt);
-  L *= a;
-  o0 *= a;
-  o1 *= a;
+  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll 8
-  for (int k = 0; k < np; ++k) {
-    const int64_t pr = prow0 + int64_t(k) * p.heads;
-    const float2 ml = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+  for (int k = 0; k < total; ++k) {
+    const int64_t pr = part_at(k);
+    const float2 m_l = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
     const float2 o = *reinterpret_cast<const float2 *>(p.part_o + pr * 512 + 2 * tid);
-    const float wk = fast_exp2(ml.x - Mt);
-    L += wk * ml.y;
+    const float wk = fast_exp2(m_l.x - Mt);
+    L += wk * m_l.y;
     o0 += wk * o.x;
     o1 += wk * o.y;
   }
   const float inv = 1.0f / L;
-  reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512)[tid] =
-      pack_bf16x2(o0 * inv, o1 * inv);
+  *op = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 namespace {
@@ -665,17 +714,27 @@ struct MlaCall {
   void *stream;
 };
 
-// Partition size and partitions per row of a call.
-inline int mla_part_tokens(bool sparse, int block_size) {
-  if (sparse) return kSparsePart;
-  // A partition starting on a 32-token tile spans 1 + ceil((PT - 32) / bs)
-  // blocks, at most the 64 one wave holds: PT <= 63 * bs + 32.
-  const int pt = part_tokens();
-  const int cap = (63 * block_size + 32) & ~31;
-  return pt < cap ? pt : cap;
+// Partition size of a call: the default (sparse lists: kSparsePart entries),
+// shrunk for small calls so that the largest possible key count still makes
+// about two items per workgroup (the rows' key counts are only known on the
+// device), and never below 256 keys. A dense partition starting on a 32-token
+// tile spans 1 + ceil((PT - 32) / bs) blocks, at most the 64 one wave holds:
+// PT <= 63 * bs + 32.
+inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int window,
+                           int max_context) {
+  int pt = sparse ? kSparsePart : part_tokens();
+  if (!sparse) {
+    const int cap = (63 * block_size + 32) & ~31;
+    pt = pt < cap ? pt : cap;
+  }
+  const int64_t keys = sparse ? topk : (window > 0 && window < max_context ? window : max_context);
+  const int64_t fit = keys * rows / (2 * int64_t(device_cus()) * wgs_mla());
+  const int64_t want = fit < 256 ? 256 : (fit & ~int64_t(31));
+  return want < pt ? int(want) : pt;
 }
-inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size) {
-  const int pt = mla_part_tokens(sparse, block_size);
+inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size,
+                             int rows) {
+  const int pt = mla_part_tokens(sparse, block_size, rows, topk, window, max_context);
   if (sparse) return (topk + pt - 1) / pt;
   const int full = (max_context + pt - 1) / pt;
   if (window <= 0) return full;
@@ -714,8 +773,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
     return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
-  const int pt = mla_part_tokens(sparse, c.block_size);
-  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
+  const int pt = mla_part_tokens(sparse, c.block_size, c.num_rows, c.topk, c.window, c.max_context);
+  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, c.num_rows) +
+                  (c.n_sinks > 0 ? 1 : 0);  // sinks: one more partial slot per row
   if (ppr > 4096) return fail(IFATTN_EINVAL, what, "more than 4096 partitions per row");
   const bool partials = ppr > 1 || c.n_sinks > 0;
   const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, partials);
@@ -757,6 +817,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
+  if (c.n_sinks > 0) mla_sink_kernel<<<c.num_rows, 64 * kMlaWaves, 0, s>>>(p);
   const int grid = device_cus();
   if (c.c8) {
     if (sparse) mla_attention_kernel<true, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
@@ -801,7 +862,7 @@ using namespace ifattn;
 extern "C" uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads,
                                                      int32_t max_context, int32_t block_size) {
   if (num_seqs <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
-  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size);
+  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size, num_seqs);
   return mla_workspace(num_seqs, heads, ppr, ppr > 1);
 }
 
@@ -835,7 +896,8 @@ extern "C" uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_
                                                         int32_t block_size) {
   if (num_rows <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
   const bool sparse = topk > 0;
-  const int ppr = mla_parts_per_row(sparse, topk, window, max_context, block_size);
+  const int ppr =
+      mla_parts_per_row(sparse, topk, window, max_context, block_size, num_rows) + (n_sinks > 0 ? 1 : 0);
   return mla_workspace(num_rows, heads, ppr, ppr > 1 || n_sinks > 0);
 }
 

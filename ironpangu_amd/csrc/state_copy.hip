@@ -1,0 +1,78 @@
+// Device execution of the host page plans: zeroing the owned page spans of a
+// state field when a resident slot is reset (page_spans,
+// native/src/page_binding.h:19-35) and copying a resident's pages to another
+// slot (copy_plan, page_binding.h:161-187). The plans are read on the device,
+// so the launches can be recorded into a HIP graph and replayed with new plans.
+//
+// Both kernels are HBM-streaming: one grid row of workgroups per span, each
+// taking a strided share of its 16-byte vectors (nontemporal stores: the bytes
+// are not read again soon). Spans whose offset, size or base are not 16-byte
+// aligned fall back to a byte loop; spans outside the field are skipped.
+#include "common.h"
+#include "ifattn_internal.h"
+#include "split_k.h"
+
+namespace ifattn {
+
+// spans: {offset, bytes} pairs (reset) or {source, destination, bytes} triples
+// (copy). Workgroup (i, j) takes span i and every gridDim.y-th 4 KiB piece of
+// it starting at piece j.
+template <bool COPY>
+__global__ __launch_bounds__(256) void state_span_kernel(uint8_t *__restrict__ field,
+                                                         uint64_t field_bytes,
+                                                         const uint64_t *__restrict__ spans) {
+  constexpr int W = COPY ? 3 : 2;
+  const uint64_t i = blockIdx.x;
+  const uint64_t src = spans[W * i];
+  const uint64_t dst = COPY ? spans[W * i + 1] : src;
+  const uint64_t bytes = spans[W * i + W - 1];
+  if (bytes == 0 || src > field_bytes || bytes > field_bytes - src || dst > field_bytes ||
+      bytes > field_bytes - dst)
+    return;
+  const uint64_t lanes = uint64_t(gridDim.y) * blockDim.x;
+  const uint64_t me = uint64_t(blockIdx.y) * blockDim.x + threadIdx.x;
+  if (((src | dst | bytes | reinterpret_cast<uintptr_t>(field)) & 15u) == 0) {
+    const uint64_t n = bytes / 16;
+    for (uint64_t v = me; v < n; v += lanes) {
+      const u32x4 x = COPY ? load_u32x4(field + src + 16 * v) : u32x4{0, 0, 0, 0};
+      __builtin_nontemporal_store(x, reinterpret_cast<u32x4 *>(field + dst + 16 * v));
+    }
+  } else {
+    for (uint64_t b = me; b < bytes; b += lanes) field[dst + b] = COPY ? field[src + b] : 0;
+  }
+}
+
+namespace {
+int32_t run_spans(bool copy, void *field, uint64_t field_bytes, const uint64_t *spans,
+                  uint64_t count, void *stream, const char *what) {
+  if (!field || (!spans && count) || field_bytes == 0)
+    return fail(IFATTN_EINVAL, what, "null field or plan");
+  if (!aligned8(spans)) return fail(IFATTN_EINVAL, what, "plan must be 8-byte aligned");
+  if (count == 0) return IFATTN_OK;
+  if (count >= (1ull << 31)) return fail(IFATTN_EINVAL, what, "more than 2^31-1 spans");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Span sizes live on the device: size the second grid dimension for the
+  // average span (one workgroup per 4 KiB of it, up to 1024).
+  const uint64_t avg = field_bytes / count;
+  const unsigned split = unsigned(avg / 4096 + 1 < 1024 ? avg / 4096 + 1 : 1024);
+  const dim3 grid(unsigned(count), split);
+  if (copy)
+    state_span_kernel<true><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans);
+  else
+    state_span_kernel<false><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans);
+  return launch_status(what);
+}
+}  // namespace
+}  // namespace ifattn
+
+using namespace ifattn;
+
+extern "C" int32_t ifattn_page_reset(void *field, uint64_t field_bytes, const uint64_t *spans,
+                                     uint64_t count, void *stream) {
+  return run_spans(false, field, field_bytes, spans, count, stream, "page reset");
+}
+
+extern "C" int32_t ifattn_state_copy(void *field, uint64_t field_bytes, const uint64_t *ranges,
+                                     uint64_t count, void *stream) {
+  return run_spans(true, field, field_bytes, ranges, count, stream, "state copy");
+}

@@ -352,6 +352,28 @@ def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None,
     return out
 
 
+# ---------------------------------------------------------------- slot reuse
+
+def page_reset(field, spans, stream=None):
+    """Zero the {offset, bytes} spans (uint64 [count, 2] on the device, e.g. from
+    host.page_spans) of a device state tensor, viewed as bytes."""
+    _dev(field, spans)
+    _req(spans.dtype in (torch.int64, torch.uint64) and spans.dim() == 2 and spans.shape[1] == 2,
+         "spans: uint64/int64 [count, 2]")
+    check(lib().ifattn_page_reset(_ptr(field), field.numel() * field.element_size(), _ptr(spans),
+                                  spans.shape[0], _stream(stream)), "ifattn_page_reset")
+
+
+def state_copy(field, ranges, stream=None):
+    """Copy the {source, destination, bytes} ranges (uint64 [count, 3] on the
+    device, e.g. from ResidentPages.copy_plan) inside one device state tensor."""
+    _dev(field, ranges)
+    _req(ranges.dtype in (torch.int64, torch.uint64) and ranges.dim() == 2 and ranges.shape[1] == 3,
+         "ranges: uint64/int64 [count, 3]")
+    check(lib().ifattn_state_copy(_ptr(field), field.numel() * field.element_size(), _ptr(ranges),
+                                  ranges.shape[0], _stream(stream)), "ifattn_state_copy")
+
+
 # ---------------------------------------------------------------- legacy launchers
 
 def cache_quantize(row, packed, scales, position, bits=8, stream=None):
