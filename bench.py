@@ -369,7 +369,7 @@ def bench_mla_rows(seed, steps, warmup, sparse):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 12)
-    row = 656 if sparse else 576
+    row = 656 if sparse else 1152  # bytes per key row
     if sparse:
         cache = torch.empty((pool, bs, 656), dtype=torch.uint8, device=dev)
         src = torch.empty((1 << 16, 576), dtype=torch.bfloat16, device=dev)
