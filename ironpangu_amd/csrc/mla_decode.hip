@@ -61,6 +61,7 @@ struct MlaParams {
   float *part_ml;               // [rows, parts_per_row, heads, 2]
   int64_t num_blocks;
   uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
+  int static_items;      // items 0..static_items-1 go to workgroups by index; the queue starts after
   int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks,
       part_tokens, parts_per_row;
   float scale_log2;
@@ -166,15 +167,12 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     if (tid == 1023) carry = at;
     __syncthreads();
   }
-  if (tid == 0) {
-    int run = carry;
-    for (int b = 0; b <= nb; ++b) {
-      const int c = bucket[b];
-      bucket[b] = run;
-      run += c;
+  {
+    const int run = bucket_prefix(bucket, nb, carry, tid);
+    if (tid == 0) {
+      p.queue[0] = p.static_items;
+      p.queue[1] = run;
     }
-    p.queue[0] = 0;
-    p.queue[1] = run;
   }
   __syncthreads();
   for (int base = 0; base < p.num_rows; base += 1024) {
@@ -580,15 +578,20 @@ __global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaPar
   int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
-  while (true) {
-    __syncthreads();
-    if (threadIdx.x == 0) *item_slot = atomicAdd(p.queue, 1);
-    __syncthreads();
-    const int it = uniform(*item_slot);
-    __syncthreads();
-    if (it >= p.queue[1]) break;
+  // Item blockIdx.x first (the plan starts the queue after the static items);
+  // each item pops its successor up front, so the queue round trip overlaps the
+  // item's own loads.
+  const int total = p.queue[1];
+  int it = blockIdx.x;
+  while (it < total) {
+    int next = 0;
+    if (threadIdx.x == 0) next = atomicAdd(p.queue, 1);
     const uint32_t e = uniform(p.items[it]);
     mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
+    __syncthreads();  // every wave is done with xbuf (and the ring)
+    if (threadIdx.x == 0) *item_slot = next;
+    __syncthreads();
+    it = uniform(*item_slot);
   }
 }
 
@@ -816,6 +819,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_o = partials ? reinterpret_cast<float *>(ws) : nullptr;
   p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
+  p.static_items = device_cus();  // the attention grid
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.n_sinks > 0) mla_sink_kernel<<<c.num_rows, 64 * kMlaWaves, 0, s>>>(p);
   const int grid = device_cus();

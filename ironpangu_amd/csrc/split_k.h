@@ -31,6 +31,7 @@ struct DecodeParams {
   int64_t num_blocks;
   int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_context, max_parts,
       part_tokens;
+  int static_items;  // items below this index are not queued (0: the queue hands out every item)
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -45,6 +46,37 @@ __device__ __forceinline__ int64_t q_row_of(const DecodeParams &p, int seq) {
 }
 __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
   return !p.cu_seqlens || p.cu_seqlens[seq + 1] - p.cu_seqlens[seq] == 1;
+}
+
+// Exclusive prefix of bucket[0..nb] (nb < 320) offset by `start`, by the first
+// wave (5 buckets per lane, a shuffle scan across lanes); returns the total to
+// lane 0 of that wave. Replaces a serial loop of LDS round trips.
+__device__ __forceinline__ int bucket_prefix(int *bucket, int nb, int start, int tid) {
+  int total = 0;
+  if (tid < 64) {
+    int c[5], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int b = 5 * tid + i;
+      c[i] = b <= nb ? bucket[b] : 0;
+      sum += c[i];
+    }
+    int x = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(x, off, 64);
+      x += tid >= off ? y : 0;
+    }
+    int run = start + x - sum;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int b = 5 * tid + i;
+      if (b <= nb) bucket[b] = run;
+      run += c[i];
+    }
+    total = start + __shfl(x, 63, 64);
+  }
+  return total;
 }
 
 // Builds the compact work list on the device (graph-safe: lengths are read at
@@ -127,15 +159,12 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
     __syncthreads();
   }
   // Exclusive scan of the bucket counts, offset by the full-item count.
-  if (tid == 0) {
-    int run = carry;
-    for (int b = 0; b <= nb; ++b) {
-      const int c = bucket[b];
-      bucket[b] = run;
-      run += c;
+  {
+    const int run = bucket_prefix(bucket, nb, carry, tid);
+    if (tid == 0) {
+      p.queue[0] = p.static_items;
+      p.queue[1] = run;
     }
-    p.queue[0] = 0;
-    p.queue[1] = run;
   }
   __syncthreads();
   // Pass 2: place each partial / empty item in its bucket.
@@ -173,10 +202,14 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
     const uint32_t off = (uint32_t(k) * p.q_heads + h) * 8u;
     return make_float2(buf_load_f32(rm, off), buf_load_f32(rm, off + 4));
   };
+  // Up to kFast partitions take one round trip: the max comes from the same
+  // batch of (m, l) loads as the weights. Longer lists scan the maxima first.
   float mmax = -INFINITY;
-  for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, load_ml(k).x);
+  if (nparts > kFast) {
+    for (int k = lane; k < nparts; k += 64) mmax = fmaxf(mmax, load_ml(k).x);
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+    for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+  }
   float lsum = 0.0f;
   float acc[V];
 #pragma unroll
@@ -195,6 +228,11 @@ __device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h
       } else {
         o[u][0] = buf_load_f32(ro, off);
       }
+    }
+    if (nparts <= kFast) {
+      mmax = ml.x;
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
     }
     const float w = lane < n ? fast_exp2(ml.x - mmax) : 0.0f;
     lsum += w * ml.y;
