@@ -111,6 +111,28 @@ __device__ __forceinline__ float wave_sum_xor(float v, int mask) {
   return v + __shfl_xor(v, mask, 64);
 }
 
+// Lane exchange across 16-lane rows (partner lane l ^ 16) and across halves
+// (l ^ 32) on the VALU: v_permlane16_swap / v_permlane32_swap return, in both
+// partner lanes, {value of the even-row lane, value of the odd-row lane}, so a
+// max or sum of the pair is one more VALU op (no LDS round trip, unlike
+// ds_bpermute). Both partners get bit-identical results.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <typename T>
 __device__ __forceinline__ T uniform(T v) {
   return __builtin_amdgcn_readfirstlane(v);

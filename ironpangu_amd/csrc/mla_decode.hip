@@ -300,8 +300,8 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5
   }
   float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
                      fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-  tmax = wave_max_xor(tmax, 16);
-  tmax = wave_max_xor(tmax, 32);
+  tmax = max_xor16(tmax);
+  tmax = max_xor32(tmax);
   if (__any(tmax > acc.m + 8.0f)) {
     const float m_new = fmaxf(acc.m, tmax);
     const float alpha = fast_exp2(acc.m - m_new);
@@ -538,8 +538,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     compute(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile);
   }
 
-  float l_tot = wave_sum_xor(acc.l, 16);
-  l_tot = wave_sum_xor(l_tot, 32);
+  float l_tot = sum_xor16(acc.l);
+  l_tot = sum_xor32(l_tot);
   if (!head_live) return;
   // Lane holds rows m = 4g + r of MFMA b -> dim 128w + 8(4g + r) + b.
   float ov[32];
@@ -638,8 +638,8 @@ __global__ __launch_bounds__(64 * kMlaWaves) void mla_sink_kernel(MlaParams p) {
     mla_tile_math<false>(acc, k, v, nullptr, qv, xbuf, live, p.scale_log2, w, lane);
     __syncthreads();  // xbuf is rewritten by the next tile
   }
-  float l_tot = wave_sum_xor(acc.l, 16);
-  l_tot = wave_sum_xor(l_tot, 32);
+  float l_tot = sum_xor16(acc.l);
+  l_tot = sum_xor32(l_tot);
   if (!head_live) return;
   const int64_t prow = (int64_t(row) * p.parts_per_row + p.parts_per_row - 1) * p.heads + c;
   float *po = p.part_o + prow * 512 + 128 * w + 32 * g;

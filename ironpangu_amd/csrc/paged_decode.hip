@@ -256,8 +256,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
     }
     float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
                        fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
     if (__any(tmax > m_run + kRescaleSlack)) {
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = fast_exp2(m_run - m_new);
@@ -325,8 +325,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
     if (t0 >= t_end) break;
   }
 
-  float l_tot = wave_sum_xor(l_run, 16);
-  l_tot = wave_sum_xor(l_tot, 32);
+  float l_tot = sum_xor16(l_run);
+  l_tot = sum_xor32(l_tot);
   if (!head_live) return;
 
   // Lane holds O^T rows m = 4g + r of MFMA b -> dim (4g + r)*VPL + b: the

@@ -48,9 +48,16 @@ struct PrefillParams {
   float scale_log2;
 };
 
-constexpr int kPrefillWaves = 4;
+#ifndef IFATTN_PREFILL_WAVES
+#define IFATTN_PREFILL_WAVES 8
+#endif
+// Eight waves (two per SIMD) with two column blocks each: one wave's softmax
+// VALU work overlaps the other's MFMAs.
+constexpr int kPrefillWaves = IFATTN_PREFILL_WAVES;
 constexpr int kPrefillTile = 32;
-constexpr int prefill_nb(int d) { return d > 128 ? 2 : 4; }        // column blocks per wave
+constexpr int prefill_nb(int d) {  // column blocks per wave
+  return kPrefillWaves == 8 ? (d > 128 ? 1 : 2) : (d > 128 ? 2 : 4);
+}
 constexpr int prefill_q_tile(int d, int g) { return kPrefillWaves * prefill_nb(d) * 16 / g; }
 
 // Work list for the multi-row sequences, sorted by the number of key tokens
@@ -104,21 +111,47 @@ __device__ __forceinline__ int pf_tile_token(int g, int j) {
   return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
 }
 
+// K/V tile staging: a ring of kPrefillStages slots, each holding a 32-token
+// K tile and V tile (rows of D bf16, no padding). The 16-byte chunks of a row
+// are XOR-swizzled by the row index so that the 16 rows one K read touches, and
+// the 16 chunks one V read touches, fall in different banks.
+#ifndef IFATTN_PF_STAGES
+#define IFATTN_PF_STAGES 4
+#endif
+// Ring depth: up to 128 KiB of staged tiles (16 KiB per stage at head_dim 128).
+constexpr int prefill_stages(int d) {
+  return IFATTN_PF_STAGES * 4 * 32 * d <= 131072 ? IFATTN_PF_STAGES : 131072 / (4 * 32 * d);
+}
 template <int D>
-struct PrefillLds {
-  static constexpr int ROW = D + 8;  // bf16 elements per padded row
-  uint16_t k[2][kPrefillTile][ROW];
-  uint16_t v[2][kPrefillTile][ROW];
+struct PrefillRing {
+  static constexpr int CH = D / 8;                  // 16-byte chunks per row
+  static constexpr int SW = CH < 16 ? CH - 1 : 15;  // swizzle mask
+  static constexpr int TILE = kPrefillTile * D * 2;  // bytes of one K (or V) tile
+  static constexpr int SLOT = 2 * TILE;
+  static constexpr int NIW = CH / kPrefillWaves;    // direct-to-LDS loads per wave per tile
+  static_assert(CH % kPrefillWaves == 0, "every wave moves the same number of chunks");
+#ifndef IFATTN_PF_ABL
+#define IFATTN_PF_ABL 0
+#endif
+#ifndef IFATTN_PF_SWZ
+#define IFATTN_PF_SWZ 0
+#endif
+  static __device__ __forceinline__ int swz(int row) {
+    return IFATTN_PF_SWZ == 1 ? 0 : (IFATTN_PF_SWZ == 2 ? ((row >> 1) & SW) : (row & SW));
+  }
+  static __device__ __forceinline__ uint32_t at(int row, int chunk) {
+    return uint32_t(row) * (D * 2) + 16u * uint32_t(chunk ^ swz(row));
+  }
 };
 
 template <int D, int G>
-__global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(PrefillParams p) {
   constexpr int NB = prefill_nb(D);
   constexpr int QT = prefill_q_tile(D, G);
   constexpr int VPL = D / 16;                        // V dims per lane
-  constexpr int CHUNKS = kPrefillTile * D / 8;       // 16-byte pieces per K (or V) tile
-  constexpr int CPT = CHUNKS / (64 * kPrefillWaves);  // pieces per thread
-  __shared__ __align__(16) PrefillLds<D> lds;
+  using RG = PrefillRing<D>;
+  constexpr int S = prefill_stages(D);
+  __shared__ __align__(16) uint8_t ring[S * RG::SLOT];
 
   if (int(blockIdx.x) >= *p.n_items) return;
   const uint32_t e = p.items[blockIdx.x];
@@ -158,31 +191,47 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
 
   const int32_t *table_row = p.block_tables + int64_t(seq) * p.table_stride;
   const uint32_t row_bytes = uint32_t(p.kv_heads) * D * 2;
-  // Global -> register prefetch of one K/V tile (CPT 16-byte pieces each).
-  u32x4 pk[CPT], pv[CPT];
-  auto fetch = [&](int t0) {
-    int blk = uniform(table_row[t0 / p.block_size]);
+  // Per-lane source offset (within a tile) of each direct-to-LDS load: load
+  // n = (waves)k + w moves chunks 64n .. 64n+63 of the K tile (n < CH/2) or of the
+  // V tile (n >= CH/2), in LDS order.
+  uint32_t src[RG::NIW];
+#pragma unroll
+  for (int k = 0; k < RG::NIW; ++k) {
+    const int n = kPrefillWaves * k + w;
+    const int l = (n % (RG::CH / 2)) * 64 + lane;
+    const int row = l / RG::CH, pos = l % RG::CH;
+    src[k] = uint32_t(row) * row_bytes + 16u * uint32_t(pos ^ RG::swz(row));
+  }
+  // Block ids of a 64-block window, one per lane, read with v_readlane: a
+  // dependent scalar table load in front of every tile's loads would stall the
+  // wave for a memory round trip per tile. The window moves (one vector load)
+  // when a tile leaves it.
+  const int n_blocks = range_end > 0 ? (range_end - 1) / p.block_size + 1 : 0;
+  int win0 = 0;
+  int lane_blk = lane < n_blocks ? table_row[lane] : 0;
+  const uint32_t ring_base = lds_addr(ring);
+  auto issue = [&](int ti) {
+    const int t0 = ti * kPrefillTile;
+    const int bi = t0 / p.block_size;
+    if (bi >= win0 + 64) {
+      win0 = bi;
+      lane_blk = win0 + lane < n_blocks ? table_row[win0 + lane] : 0;
+    }
+    int blk = __builtin_amdgcn_readlane(lane_blk, bi - win0);
     blk = blk < 0 ? 0 : (blk >= p.num_blocks ? int(p.num_blocks - 1) : blk);
     const int64_t tok0 = int64_t(blk) * p.block_size + (t0 & (p.block_size - 1));
     const int n_live = range_end - t0 < kPrefillTile ? range_end - t0 : kPrefillTile;
-    const uint32_t extent = uint32_t(n_live - 1) * row_bytes + D * 2;
+    const uint32_t extent = uint32_t(n_live - 1) * row_bytes + D * 2;  // later rows read as zero
     const int64_t first = (tok0 * p.kv_heads + kvh) * D * 2;
-    const auto rk = make_rsrc(p.k_cache + first, extent);
-    const auto rv = make_rsrc(p.v_cache + first, extent);
+    const u32x4 rk = raw_rsrc(p.k_cache + first, extent);
+    const u32x4 rv = raw_rsrc(p.v_cache + first, extent);
+    const uint32_t slot = ring_base + uint32_t(ti % S) * RG::SLOT;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int i = tid + k * 64 * kPrefillWaves;
-      const uint32_t off = uint32_t(i / (D / 8)) * row_bytes + uint32_t(i % (D / 8)) * 16;
-      pk[k] = buf_load_x4(rk, off);
-      pv[k] = buf_load_x4(rv, off);
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int i = tid + k * 64 * kPrefillWaves;
-      *reinterpret_cast<u32x4 *>(&lds.k[buf][i / (D / 8)][(i % (D / 8)) * 8]) = pk[k];
-      *reinterpret_cast<u32x4 *>(&lds.v[buf][i / (D / 8)][(i % (D / 8)) * 8]) = pv[k];
+    for (int k = 0; k < RG::NIW; ++k) {
+      const int n = kPrefillWaves * k + w;
+      const bool is_v = n >= RG::CH / 2;
+      lds_dma16(is_v ? rv : rk, src[k],
+                slot + (is_v ? uint32_t(RG::TILE) : 0u) + uint32_t(n % (RG::CH / 2)) * 1024u);
     }
   };
 
@@ -197,15 +246,14 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
   }
   const int lim_min = base_lim + row0;  // smallest limit among this tile's rows
 
-  auto compute = [&](int buf, int t0) {
+  // QK^T of one tile (raw scores per column block and 16-token half).
+  auto qk = [&](const uint8_t *kt, f32x4 (&sc)[NB][2]) {
     u32x4 ka[2][D / 32];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int s = 0; s < D / 32; ++s)
-        ka[mt][s] = *reinterpret_cast<const u32x4 *>(&lds.k[buf][16 * mt + c][(D / 4) * g + 8 * s]);
-    u32x4 pb[NB];
-    const bool masked = t0 + kPrefillTile - 1 > lim_min;  // tile crosses some column's limit
+        ka[mt][s] = load_u32x4(kt + RG::at(16 * mt + c, (D / 32) * g + s));
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       f32x4 s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
@@ -214,11 +262,25 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
         s0 = mfma16x16x32(ka[0][s], qv[nb][s], s0);
         s1 = mfma16x16x32(ka[1][s], qv[nb][s], s1);
       }
+      sc[nb][0] = s0;
+      sc[nb][1] = s1;
+    }
+  };
+  // Mask, online softmax and PV of one tile from its scores.
+  auto finish = [&](const uint8_t *vt, int t0, const f32x4 (&sc)[NB][2]) {
+    const __attribute__((address_space(3))) char *vt_lds =
+        (const __attribute__((address_space(3))) char *)(vt);
+    u32x4 pb[NB];
+    const bool masked = t0 + kPrefillTile - 1 > lim_min;  // tile crosses some column's limit
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      // Raw scores; the softmax scale (> 0) is applied inside the exponent's
+      // fused multiply-add, and the max is taken before scaling.
       float x[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[r] = s0[r] * p.scale_log2;
-        x[4 + r] = s1[r] * p.scale_log2;
+        x[r] = sc[nb][0][r];
+        x[4 + r] = sc[nb][1][r];
       }
       if (masked) {
 #pragma unroll
@@ -226,8 +288,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       }
       float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
                          fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-      tmax = wave_max_xor(tmax, 16);
-      tmax = wave_max_xor(tmax, 32);
+      tmax = max_xor16(tmax);
+      tmax = max_xor32(tmax) * p.scale_log2;
       if (__any(tmax > m_run[nb] + 8.0f)) {
         const float m_new = fmaxf(m_run[nb], tmax);
         const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run[nb] - m_new);
@@ -239,79 +301,87 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 1) void varlen_prefill_kernel(P
       const float m_use = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
       float pr[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(x[j] - m_use);
+      for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(x[j], p.scale_log2, -m_use));
       l_run[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
       pb[nb] = u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
                      pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
     }
-    // V^T operands: lane c holds dims c*VPL .. +VPL of its eight tokens.
-    uint32_t vr[8][VPL / 2];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint16_t *src = &lds.v[buf][pf_tile_token(g, j)][c * VPL];
-      if constexpr (VPL == 4) {
-        const u32x2 x = *reinterpret_cast<const u32x2 *>(src);
-        vr[j][0] = x[0];
-        vr[j][1] = x[1];
-      } else {
-#pragma unroll
-        for (int qd = 0; qd < VPL / 2; qd += 4) {
-          const u32x4 x = *reinterpret_cast<const u32x4 *>(src + 2 * qd);
-          vr[j][qd] = x[0];
-          vr[j][qd + 1] = x[1];
-          vr[j][qd + 2] = x[2];
-          vr[j][qd + 3] = x[3];
-        }
-      }
-    }
+    // V^T operand of PV MFMA b (rows = dims 16b .. 16b+15, k = the eight
+    // tokens tile_token(g, 0..7) of the lane's P column) straight from LDS with
+    // two transposing reads (ds_read_b64_tr_b16): in each 16-lane group, lane i
+    // names 4 consecutive dims 16b + 4(i&3) of token tile_token(g, i>>2) (then
+    // of tile_token(g, 4 + (i>>2))), and lane c receives dim 16b + c of those
+    // four tokens.
+    const int tr_dim = 4 * (c & 3);
+    const int tr_row0 = pf_tile_token(g, c >> 2), tr_row1 = pf_tile_token(g, 4 + (c >> 2));
 #pragma unroll
     for (int b = 0; b < VPL; ++b) {
-      const int wd = b >> 1;
-      u32x4 a;
-      if (b & 1)
-        a = u32x4{pack_hi16(vr[0][wd], vr[1][wd]), pack_hi16(vr[2][wd], vr[3][wd]),
-                  pack_hi16(vr[4][wd], vr[5][wd]), pack_hi16(vr[6][wd], vr[7][wd])};
-      else
-        a = u32x4{pack_lo16(vr[0][wd], vr[1][wd]), pack_lo16(vr[2][wd], vr[3][wd]),
-                  pack_lo16(vr[4][wd], vr[5][wd]), pack_lo16(vr[6][wd], vr[7][wd])};
+      const int d = 16 * b + tr_dim;
+      const uint32_t o0 = RG::at(tr_row0, d >> 3) + 2 * (d & 7);
+      const uint32_t o1 = RG::at(tr_row1, d >> 3) + 2 * (d & 7);
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o0));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o1));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) oacc[nb][b] = mfma16x16x32(a, pb[nb], oacc[nb][b]);
     }
   };
 
-  if (range_end > 0) {
-    fetch(0);
-    stash(0);
+  // Ring: tile ti lives in slot ti % S (S >= 4), S-1 tiles ahead are issued.
+  // Iteration ti runs QK^T of tile ti+1 ahead of the softmax and PV of tile
+  // ti, so the MFMAs of the one overlap the VALU work of the other. Its top
+  // waits for tile ti+1, and the barrier both publishes that tile and retires
+  // every wave's reads of tile ti-1, whose slot then receives tile ti+S-1.
+  // The loop is unrolled by S so every slot offset is a compile-time constant
+  // (LDS immediate offsets instead of per-tile address arithmetic) and the
+  // score registers alternate without copies.
+  static_assert(S >= 4 && S % 2 == 0, "tiles ti, ti+1 resident, one in flight; even unroll");
+  const int n_tiles = (range_end + kPrefillTile - 1) / kPrefillTile;
+  if (n_tiles > 0) {
+#pragma unroll
+    for (int i = 0; i < S - 1; ++i)
+      if (i < n_tiles) issue(i);
+    if (S - 2 < n_tiles)
+      lds_dma_wait<(S - 2) * RG::NIW>();
+    else
+      lds_dma_wait<0>();
     __syncthreads();
-    int buf = 0;
-    for (int t0 = 0; t0 < range_end; t0 += kPrefillTile) {
-      const bool more = t0 + kPrefillTile < range_end;
-      if (more) fetch(t0 + kPrefillTile);
-      compute(buf, t0);
-      if (more) stash(buf ^ 1);
-      __syncthreads();
-      buf ^= 1;
+    f32x4 sc[2][NB][2];
+    qk(ring, sc[0]);
+    for (int t = 0; t < n_tiles; t += S) {
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        const int ti = t + u;
+        if (ti < n_tiles) {
+          if (ti + S - 2 < n_tiles)  // tiles ti+2 .. ti+S-2 may stay in flight
+            lds_dma_wait<(S - 3) * RG::NIW>();
+          else
+            lds_dma_wait<0>();
+          __syncthreads();
+          if (ti + S - 1 < n_tiles) issue(ti + S - 1);
+          if (ti + 1 < n_tiles) qk(ring + ((u + 1) % S) * RG::SLOT, sc[(u + 1) & 1]);
+          finish(ring + u * RG::SLOT + RG::TILE, ti * kPrefillTile, sc[u & 1]);
+        }
+      }
     }
   }
 
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    float l_tot = wave_sum_xor(l_run[nb], 16);
-    l_tot = wave_sum_xor(l_tot, 32);
+    float l_tot = sum_xor16(l_run[nb]);
+    l_tot = sum_xor32(l_tot);
     if (!live[nb]) continue;
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    uint16_t *op = p.out + (qrow[nb] * p.q_heads + head[nb]) * D + 4 * g * VPL;
-    // lane holds dims (4g + r)*VPL + b
+    uint16_t *op = p.out + (qrow[nb] * p.q_heads + head[nb]) * D + 4 * g;
+    // PV MFMA b row 4g + r -> dim 16b + 4g + r
 #pragma unroll
-    for (int k = 0; k < D / 32; ++k) {
-      float v[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int idx = 8 * k + i;  // = r*VPL + b
-        v[i] = oacc[nb][idx % VPL][idx / VPL] * inv;
-      }
-      store_u32x4(op + 8 * k, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                    pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])});
+    for (int b = 0; b < VPL; ++b) {
+      const f32x4 v = oacc[nb][b];
+      *reinterpret_cast<u32x2 *>(op + 16 * b) =
+          u32x2{pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
     }
   }
 }
