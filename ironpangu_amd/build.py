@@ -97,6 +97,10 @@ def build(jobs: int | None = None, plugins: bool = True) -> Path:
                   f"-L{PKG}", "-lifattn_hip", "-Wl,-rpath,$ORIGIN", "-o", str(out)])
         with cf.ThreadPoolExecutor(jobs) as ex:
             list(ex.map(one, PLUGINS.items()))
+    driver = CSRC.parent / "driver" / "ifattn_drive.cpp"
+    if driver.exists():
+        _run(["g++", *HOST_FLAGS, f"-I{ROCM}/include", str(driver), f"-L{ROCM}/lib",
+              "-lamdhip64", "-ldl", f"-Wl,-rpath,{ROCM}/lib", "-o", str(PKG / "ifattn_drive")])
     return LIB
 
 
