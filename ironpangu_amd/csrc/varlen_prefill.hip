@@ -13,15 +13,17 @@
 //  * single-row sequences (decode rows of a mixed batch) go to the split-K
 //    paged decode kernels through a q-row indirection;
 //  * longer chunks are cut into query tiles of 256/G rows (G = q heads per kv
-//    head); a workgroup (4 waves) owns one (sequence, query tile, kv head).
-//    The MFMA N dimension packs (query row, grouped head) columns, so all G
-//    heads of a kv head reuse every K/V tile. Each wave owns 4 column blocks
-//    of 16 (2 for head_dim 256).
-//  * K/V 32-token tiles stream through double-buffered LDS (rows padded by
-//    16 B so the 16-byte MFMA operand reads are bank-conflict free), fetched
-//    with buffer loads one tile ahead. QK^T runs transposed (tokens in M,
-//    columns in N) so the score tile is already the B operand of the PV MFMA;
-//    V^T operands come from 16-byte LDS reads split with v_perm.
+//    head); a workgroup (8 waves, two per SIMD) owns one (sequence, query
+//    tile, kv head), and the kv heads of a query tile are adjacent
+//    workgroups. The MFMA N dimension packs (query row, grouped head)
+//    columns, so all G heads of a kv head reuse every K/V tile. Each wave owns
+//    2 column blocks of 16 (1 for head_dim 256).
+//  * K/V 32-token tiles are copied HBM -> LDS with direct-to-LDS buffer loads
+//    into a ring of 4 slots (16-B chunks XOR-swizzled by row), three tiles
+//    ahead. QK^T runs transposed (tokens in M, columns in N) so the score
+//    tile is already the B operand of the PV MFMA; V^T operands come from
+//    transposing LDS reads. QK^T of the next tile is issued ahead of the
+//    softmax of the current one.
 //  * tiles wholly above the diagonal are never visited; only tiles crossing a
 //    column's limit apply the causal mask.
 //  * query tiles are scheduled longest-first by a device plan kernel.
@@ -130,19 +132,15 @@ struct PrefillRing {
   static constexpr int SLOT = 2 * TILE;
   static constexpr int NIW = CH / kPrefillWaves;    // direct-to-LDS loads per wave per tile
   static_assert(CH % kPrefillWaves == 0, "every wave moves the same number of chunks");
-#ifndef IFATTN_PF_ABL
-#define IFATTN_PF_ABL 0
-#endif
-#ifndef IFATTN_PF_SWZ
-#define IFATTN_PF_SWZ 0
-#endif
-  static __device__ __forceinline__ int swz(int row) {
-    return IFATTN_PF_SWZ == 1 ? 0 : (IFATTN_PF_SWZ == 2 ? ((row >> 1) & SW) : (row & SW));
-  }
+  static __device__ __forceinline__ int swz(int row) { return row & SW; }
   static __device__ __forceinline__ uint32_t at(int row, int chunk) {
     return uint32_t(row) * (D * 2) + 16u * uint32_t(chunk ^ swz(row));
   }
 };
+
+// s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left at their
+// maxima (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr unsigned kVmcntZero = 0x0F70u;
 
 template <int D, int G>
 __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(PrefillParams p) {
@@ -153,10 +151,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
   constexpr int S = prefill_stages(D);
   __shared__ __align__(16) uint8_t ring[S * RG::SLOT];
 
-  if (int(blockIdx.x) >= *p.n_items) return;
-  const uint32_t e = p.items[blockIdx.x];
+  // The kv heads of one query tile are adjacent workgroups, so the halves of
+  // every cache row are fetched at about the same time (DRAM page hits).
+  const int it = int(blockIdx.x) / p.kv_heads;
+  const int kvh = int(blockIdx.x) - it * p.kv_heads;
+  if (it >= *p.n_items) return;
+  const uint32_t e = p.items[it];
   const int seq = int(e >> 12), qt = int(e & 0xfffu);
-  const int kvh = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = uniform(int(tid >> 6));
   const int c = lane & 15, g = lane >> 4;
   const int q0 = p.cu[seq];
@@ -216,6 +217,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
     if (bi >= win0 + 64) {
       win0 = bi;
       lane_blk = win0 + lane < n_blocks ? table_row[win0 + lane] : 0;
+      // Wait here, once per 64 blocks, with a wait the compiler accounts for:
+      // otherwise it cannot prove the id load complete at the readlane below
+      // and drains every in-flight tile load (vmcnt(0)) on every tile.
+      __builtin_amdgcn_s_waitcnt(kVmcntZero);
     }
     int blk = __builtin_amdgcn_readlane(lane_blk, bi - win0);
     blk = blk < 0 ? 0 : (blk >= p.num_blocks ? int(p.num_blocks - 1) : blk);
@@ -390,7 +395,7 @@ namespace {
 
 template <int D>
 void launch_prefill(const PrefillParams &p, int grid, hipStream_t s) {
-  const dim3 g(grid, p.kv_heads);
+  const dim3 g(grid * p.kv_heads);
   switch (p.group) {
     case 1: varlen_prefill_kernel<D, 1><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
     case 2: varlen_prefill_kernel<D, 2><<<g, 64 * kPrefillWaves, 0, s>>>(p); break;
