@@ -115,8 +115,9 @@ __device__ __forceinline__ int pf_tile_token(int g, int j) {
 
 // K/V tile staging: a ring of kPrefillStages slots, each holding a 32-token
 // K tile and V tile (rows of D bf16, no padding). The 16-byte chunks of a row
-// are XOR-swizzled by the row index so that the 16 rows one K read touches, and
-// the 16 chunks one V read touches, fall in different banks.
+// are XOR-swizzled by a key derived from the row index so that K operand reads
+// and transposing V reads are free of bank conflicts (SQ_LDS_BANK_CONFLICT
+// reads 0).
 #ifndef IFATTN_PF_STAGES
 #define IFATTN_PF_STAGES 4
 #endif
@@ -132,7 +133,15 @@ struct PrefillRing {
   static constexpr int SLOT = 2 * TILE;
   static constexpr int NIW = CH / kPrefillWaves;    // direct-to-LDS loads per wave per tile
   static_assert(CH % kPrefillWaves == 0, "every wave moves the same number of chunks");
-  static __device__ __forceinline__ int swz(int row) { return row & SW; }
+  static constexpr int SWB = SW == 15 ? 4 : (SW == 7 ? 3 : (SW == 3 ? 2 : 1));  // mask bits
+  // XOR key: the row rotated left by one bit within the mask. The 16 rows of
+  // a K operand read get 16 distinct keys, and so do the eight consecutive
+  // rows of two 16-lane groups of a transposing V read, whose lanes touch
+  // chunk pairs {2b, 2b+1}: keys that differ only in bit 0 (rows r, r^1 under
+  // a plain row key) would map both rows' pairs to the same banks.
+  static __device__ __forceinline__ int swz(int row) {
+    return ((row << 1) | ((row >> (SWB - 1)) & 1)) & SW;
+  }
   static __device__ __forceinline__ uint32_t at(int row, int chunk) {
     return uint32_t(row) * (D * 2) + 16u * uint32_t(chunk ^ swz(row));
   }
