@@ -196,11 +196,16 @@ struct MlaRow {
   static constexpr int NI = C8 ? 6 : 9;
   static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
   static constexpr int STAGES = C8 ? 6 : 4;
-  // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B, a multiple of
-  // 128) XOR the chunk index with the row's low 3 bits so the 16 rows that one
-  // K read touches spread over the banks; C8 rows (656 B) are not swizzled.
+  // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B: odd rows
+  // start half a bank period in) XOR the latent chunk index with the row's low
+  // 4 bits, which puts the 16 rows of one K read on 16 distinct bank groups;
+  // the 8 rope chunks (j >= 64) use the low 3 bits to stay inside the row.
+  // C8 rows (656 B) are not swizzled.
+  static __device__ __forceinline__ uint32_t key(uint32_t r, uint32_t j) {
+    return j < 64 ? (r & 15) : (r & 7);
+  }
   static __device__ __forceinline__ uint32_t chunk(uint32_t r, uint32_t j) {
-    return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ (r & 7));
+    return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ key(r, j));
   }
 };
 static_assert(MlaRow<false>::SLOT * MlaRow<false>::STAGES + 4 * 64 * 32 + 4 * kSparsePart <= 160 * 1024, "LDS");
@@ -393,7 +398,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     const uint32_t l = uint32_t((k * 4 + w) * 64 + lane);
     lrow[k] = l / R::CHUNKS;
     const uint32_t jj = l % R::CHUNKS;
-    lcol[k] = 16 * (C8 ? jj : (jj ^ (lrow[k] & 7)));
+    lcol[k] = 16 * (C8 ? jj : (jj ^ R::key(lrow[k], jj)));
   }
 
   int lane_blocks = 0;
