@@ -19,11 +19,12 @@
 //    columns, so all G heads of a kv head reuse every K/V tile. Each wave owns
 //    2 column blocks of 16 (1 for head_dim 256).
 //  * K/V 32-token tiles are copied HBM -> LDS with direct-to-LDS buffer loads
-//    into a ring of 4 slots (16-B chunks XOR-swizzled by row), three tiles
-//    ahead. QK^T runs transposed (tokens in M, columns in N) so the score
-//    tile is already the B operand of the PV MFMA; V^T operands come from
-//    transposing LDS reads. QK^T of the next tile is issued ahead of the
-//    softmax of the current one.
+//    into a ring of 3 steps of two tiles each (16-B chunks XOR-swizzled by a
+//    row key), two steps ahead; a loop step waits, synchronises and runs the
+//    softmax bookkeeping once per 64 keys. QK^T runs transposed (tokens in M,
+//    columns in N) so the score tile is already the B operand of the PV MFMA;
+//    V^T operands come from transposing LDS reads. The two waves of a SIMD
+//    overlap one's MFMAs with the other's softmax.
 //  * tiles wholly above the diagonal are never visited; only tiles crossing a
 //    column's limit apply the causal mask.
 //  * query tiles are scheduled longest-first by a device plan kernel.
@@ -119,11 +120,20 @@ __device__ __forceinline__ int pf_tile_token(int g, int j) {
 // and transposing V reads are free of bank conflicts (SQ_LDS_BANK_CONFLICT
 // reads 0).
 #ifndef IFATTN_PF_STAGES
-#define IFATTN_PF_STAGES 4
+#define IFATTN_PF_STAGES 3
 #endif
-// Ring depth: up to 128 KiB of staged tiles (16 KiB per stage at head_dim 128).
+// 32-key tiles per loop step: the per-step costs (wait, barrier, row max,
+// rescale check) are paid once per 64 keys where the ring has room for it.
+#ifndef IFATTN_PF_KT
+#define IFATTN_PF_KT 2
+#endif
+constexpr int prefill_kt(int d) { return d <= 128 ? IFATTN_PF_KT : 1; }
+// Ring depth in steps: up to 128 KiB of staged tiles (16 KiB per tile at
+// head_dim 128). Three steps (one being read, two in flight) measured best.
 constexpr int prefill_stages(int d) {
-  return IFATTN_PF_STAGES * 4 * 32 * d <= 131072 ? IFATTN_PF_STAGES : 131072 / (4 * 32 * d);
+  return IFATTN_PF_STAGES * prefill_kt(d) * 4 * 32 * d <= 131072
+             ? IFATTN_PF_STAGES
+             : 131072 / (prefill_kt(d) * 4 * 32 * d);
 }
 template <int D>
 struct PrefillRing {
@@ -158,7 +168,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
   constexpr int VPL = D / 16;                        // V dims per lane
   using RG = PrefillRing<D>;
   constexpr int S = prefill_stages(D);
-  __shared__ __align__(16) uint8_t ring[S * RG::SLOT];
+  constexpr int KT = prefill_kt(D);
+  constexpr int STEP = KT * RG::SLOT;  // LDS bytes of one step's tiles
+  __shared__ __align__(16) uint8_t ring[S * STEP];
 
   // The kv heads of one query tile are adjacent workgroups, so the halves of
   // every cache row are fetched at about the same time (DRAM page hits).
@@ -220,8 +232,21 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
   int win0 = 0;
   int lane_blk = lane < n_blocks ? table_row[lane] : 0;
   const uint32_t ring_base = lds_addr(ring);
+  // Tile ti goes to ring slot ti % (S * KT). Tiles past the range (the second
+  // tile of a last, half-used step) move no bytes and land as zeros.
   auto issue = [&](int ti) {
     const int t0 = ti * kPrefillTile;
+    if (t0 >= range_end) {
+      const u32x4 rz = raw_rsrc(p.k_cache, 0u);
+      const uint32_t slot = ring_base + uint32_t(ti % (S * KT)) * RG::SLOT;
+#pragma unroll
+      for (int k = 0; k < RG::NIW; ++k) {
+        const int n = kPrefillWaves * k + w;
+        const bool is_v = n >= RG::CH / 2;
+        lds_dma16(rz, src[k], slot + (is_v ? uint32_t(RG::TILE) : 0u) + uint32_t(n % (RG::CH / 2)) * 1024u);
+      }
+      return;
+    }
     const int bi = t0 / p.block_size;
     if (bi >= win0 + 64) {
       win0 = bi;
@@ -239,7 +264,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
     const int64_t first = (tok0 * p.kv_heads + kvh) * D * 2;
     const u32x4 rk = raw_rsrc(p.k_cache + first, extent);
     const u32x4 rv = raw_rsrc(p.v_cache + first, extent);
-    const uint32_t slot = ring_base + uint32_t(ti % S) * RG::SLOT;
+    const uint32_t slot = ring_base + uint32_t(ti % (S * KT)) * RG::SLOT;
 #pragma unroll
     for (int k = 0; k < RG::NIW; ++k) {
       const int n = kPrefillWaves * k + w;
@@ -260,48 +285,55 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
   }
   const int lim_min = base_lim + row0;  // smallest limit among this tile's rows
 
-  // QK^T of one tile (raw scores per column block and 16-token half).
-  auto qk = [&](const uint8_t *kt, f32x4 (&sc)[NB][2]) {
-    u32x4 ka[2][D / 32];
+  // QK^T of one step's KT tiles (raw scores per tile, column block and
+  // 16-token half).
+  auto qk = [&](const uint8_t *step, f32x4 (&sc)[KT][NB][2]) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int h = 0; h < KT; ++h) {
+      const uint8_t *kt = step + h * RG::SLOT;
+      // One 16-token half at a time keeps 16 operand registers live.
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s)
-        ka[mt][s] = load_u32x4(kt + RG::at(16 * mt + c, (D / 32) * g + s));
+      for (int mt = 0; mt < 2; ++mt) {
+        u32x4 ka[D / 32];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      f32x4 s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
+        for (int s = 0; s < D / 32; ++s)
+          ka[s] = load_u32x4(kt + RG::at(16 * mt + c, (D / 32) * g + s));
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) {
-        s0 = mfma16x16x32(ka[0][s], qv[nb][s], s0);
-        s1 = mfma16x16x32(ka[1][s], qv[nb][s], s1);
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+          for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32(ka[s], qv[nb][s], acc);
+          sc[h][nb][mt] = acc;
+        }
       }
-      sc[nb][0] = s0;
-      sc[nb][1] = s1;
     }
   };
-  // Mask, online softmax and PV of one tile from its scores.
-  auto finish = [&](const uint8_t *vt, int t0, const f32x4 (&sc)[NB][2]) {
-    const __attribute__((address_space(3))) char *vt_lds =
-        (const __attribute__((address_space(3))) char *)(vt);
-    u32x4 pb[NB];
-    const bool masked = t0 + kPrefillTile - 1 > lim_min;  // tile crosses some column's limit
+  // Mask, online softmax and PV of one step from its scores.
+  auto finish = [&](const uint8_t *step, int t0, const f32x4 (&sc)[KT][NB][2]) {
+    u32x4 pb[KT][NB];
+    const bool masked = t0 + KT * kPrefillTile - 1 > lim_min;  // step crosses some column's limit
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       // Raw scores; the softmax scale (> 0) is applied inside the exponent's
       // fused multiply-add, and the max is taken before scaling.
-      float x[8];
+      float x[KT * 8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = sc[nb][0][r];
-        x[4 + r] = sc[nb][1][r];
-      }
+      for (int h = 0; h < KT; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[8 * h + r] = sc[h][nb][0][r];
+          x[8 * h + 4 + r] = sc[h][nb][1][r];
+        }
       if (masked) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = t0 + pf_tile_token(g, j) <= lim[nb] ? x[j] : -INFINITY;
+        for (int h = 0; h < KT; ++h)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            x[8 * h + j] = t0 + kPrefillTile * h + pf_tile_token(g, j) <= lim[nb] ? x[8 * h + j] : -INFINITY;
       }
-      float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                         fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      float tmax = x[0];
+#pragma unroll
+      for (int j = 1; j < KT * 8; ++j) tmax = fmaxf(tmax, x[j]);
       tmax = max_xor16(tmax);
       tmax = max_xor32(tmax) * p.scale_log2;
       if (__any(tmax > m_run[nb] + 8.0f)) {
@@ -313,12 +345,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
         for (int b = 0; b < VPL; ++b) oacc[nb][b] *= alpha;
       }
       const float m_use = m_run[nb] == -INFINITY ? 0.0f : m_run[nb];
-      float pr[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(x[j], p.scale_log2, -m_use));
-      l_run[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
-      pb[nb] = u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                     pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+      for (int h = 0; h < KT; ++h) {
+        float pr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(x[8 * h + j], p.scale_log2, -m_use));
+        l_run[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+        pb[h][nb] = u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                          pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+      }
     }
     // V^T operand of PV MFMA b (rows = dims 16b .. 16b+15, k = the eight
     // tokens tile_token(g, 0..7) of the lane's P column) straight from LDS with
@@ -329,55 +364,60 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
     const int tr_dim = 4 * (c & 3);
     const int tr_row0 = pf_tile_token(g, c >> 2), tr_row1 = pf_tile_token(g, 4 + (c >> 2));
 #pragma unroll
-    for (int b = 0; b < VPL; ++b) {
-      const int d = 16 * b + tr_dim;
-      const uint32_t o0 = RG::at(tr_row0, d >> 3) + 2 * (d & 7);
-      const uint32_t o1 = RG::at(tr_row1, d >> 3) + 2 * (d & 7);
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
-      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o0));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o1));
-      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-      const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    for (int h = 0; h < KT; ++h) {
+      const __attribute__((address_space(3))) char *vt_lds =
+          (const __attribute__((address_space(3))) char *)(step + h * RG::SLOT + RG::TILE);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) oacc[nb][b] = mfma16x16x32(a, pb[nb], oacc[nb][b]);
+      for (int b = 0; b < VPL; ++b) {
+        const int d = 16 * b + tr_dim;
+        const uint32_t o0 = RG::at(tr_row0, d >> 3) + 2 * (d & 7);
+        const uint32_t o1 = RG::at(tr_row1, d >> 3) + 2 * (d & 7);
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o0));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o1));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = u32x4{l2[0], l2[1], h2[0], h2[1]};
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) oacc[nb][b] = mfma16x16x32(a, pb[h][nb], oacc[nb][b]);
+      }
     }
   };
 
-  // Ring: tile ti lives in slot ti % S (S >= 4), S-1 tiles ahead are issued.
-  // Iteration ti runs QK^T of tile ti+1 ahead of the softmax and PV of tile
-  // ti, so the MFMAs of the one overlap the VALU work of the other. Its top
-  // waits for tile ti+1, and the barrier both publishes that tile and retires
-  // every wave's reads of tile ti-1, whose slot then receives tile ti+S-1.
-  // The loop is unrolled by S so every slot offset is a compile-time constant
-  // (LDS immediate offsets instead of per-tile address arithmetic) and the
-  // score registers alternate without copies.
-  static_assert(S >= 4 && S % 2 == 0, "tiles ti, ti+1 resident, one in flight; even unroll");
+  // Ring: step si (tiles KT*si .. KT*si+KT-1) lives in step slot si % S, and
+  // S-1 steps ahead are issued (every step issues KT*NIW loads per wave, dead
+  // tiles included, so the wait counts are exact). The top of iteration si
+  // waits for step si, and the barrier both publishes it and retires every
+  // wave's reads of step si-1, whose slot then receives step si+S-1. The two
+  // waves of a SIMD overlap one's MFMAs with the other's softmax. The loop is
+  // unrolled by S so every slot offset is a compile-time constant (LDS
+  // immediate offsets instead of per-step address arithmetic).
+  static_assert(S >= 2, "one step resident, one in flight");
+  constexpr int PER_STEP = KT * RG::NIW;  // direct-to-LDS loads per wave per step
   const int n_tiles = (range_end + kPrefillTile - 1) / kPrefillTile;
-  if (n_tiles > 0) {
+  const int n_steps = (n_tiles + KT - 1) / KT;
+  auto issue_step = [&](int si) {
+#pragma unroll
+    for (int h = 0; h < KT; ++h) issue(si * KT + h);
+  };
+  if (n_steps > 0) {
 #pragma unroll
     for (int i = 0; i < S - 1; ++i)
-      if (i < n_tiles) issue(i);
-    if (S - 2 < n_tiles)
-      lds_dma_wait<(S - 2) * RG::NIW>();
-    else
-      lds_dma_wait<0>();
-    __syncthreads();
-    f32x4 sc[2][NB][2];
-    qk(ring, sc[0]);
-    for (int t = 0; t < n_tiles; t += S) {
+      if (i < n_steps) issue_step(i);
+    f32x4 sc[KT][NB][2];
+    for (int t = 0; t < n_steps; t += S) {
 #pragma unroll
       for (int u = 0; u < S; ++u) {
-        const int ti = t + u;
-        if (ti < n_tiles) {
-          if (ti + S - 2 < n_tiles)  // tiles ti+2 .. ti+S-2 may stay in flight
-            lds_dma_wait<(S - 3) * RG::NIW>();
+        const int si = t + u;
+        if (si < n_steps) {
+          if (si + S - 2 < n_steps)  // steps si+1 .. si+S-2 may stay in flight
+            lds_dma_wait<(S - 2) * PER_STEP>();
           else
             lds_dma_wait<0>();
           __syncthreads();
-          if (ti + S - 1 < n_tiles) issue(ti + S - 1);
-          if (ti + 1 < n_tiles) qk(ring + ((u + 1) % S) * RG::SLOT, sc[(u + 1) & 1]);
-          finish(ring + u * RG::SLOT + RG::TILE, ti * kPrefillTile, sc[u & 1]);
+          if (si + S - 1 < n_steps) issue_step(si + S - 1);
+          qk(ring + u * STEP, sc);
+          finish(ring + u * STEP, si * KT * kPrefillTile, sc);
         }
       }
     }
