@@ -48,7 +48,10 @@ constexpr int kTile = 32;
 #ifndef IFATTN_DECODE_STAGES
 #define IFATTN_DECODE_STAGES 3
 #endif
-constexpr int kStages = IFATTN_DECODE_STAGES;  // tile buffers per wave (kStages-1 tiles prefetched)
+// Tile buffers per wave (stages-1 tiles prefetched). head_dim 256 holds two:
+// three 256-dim tiles (128 registers each) would not fit one wave's registers.
+template <int D>
+constexpr int decode_stages() { return D > 128 ? 2 : IFATTN_DECODE_STAGES; }
 
 // Token of k-slot j (0..7) for lane group g within a 32-token tile.
 __device__ __forceinline__ int tile_token(int g, int j) {
@@ -304,6 +307,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   // Ring of kStages tile buffers: tiles t+1 .. t+kStages-1 are in flight while
   // tile t is reduced. Tiles past the partition end reload the last tile (a
   // cache hit) so every iteration has the same shape.
+  constexpr int kStages = decode_stages<D>();
   TileRegs<D, C8> tr[kStages];
   auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (kTile - 1)); };
 #pragma unroll
