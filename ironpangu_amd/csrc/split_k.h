@@ -48,16 +48,17 @@ __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
   return !p.cu_seqlens || p.cu_seqlens[seq + 1] - p.cu_seqlens[seq] == 1;
 }
 
-// Exclusive prefix of bucket[0..nb] (nb < 320) offset by `start`, by the first
-// wave (5 buckets per lane, a shuffle scan across lanes); returns the total to
-// lane 0 of that wave. Replaces a serial loop of LDS round trips.
+// Exclusive prefix of bucket[0..nb] (nb < 64 * PL) offset by `start`, by the
+// first wave (PL buckets per lane, a shuffle scan across lanes); returns the
+// total to lane 0 of that wave. Replaces a serial loop of LDS round trips.
+template <int PL = 5>
 __device__ __forceinline__ int bucket_prefix(int *bucket, int nb, int start, int tid) {
   int total = 0;
   if (tid < 64) {
-    int c[5], sum = 0;
+    int c[PL], sum = 0;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int b = 5 * tid + i;
+    for (int i = 0; i < PL; ++i) {
+      const int b = PL * tid + i;
       c[i] = b <= nb ? bucket[b] : 0;
       sum += c[i];
     }
@@ -69,8 +70,8 @@ __device__ __forceinline__ int bucket_prefix(int *bucket, int nb, int start, int
     }
     int run = start + x - sum;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int b = 5 * tid + i;
+    for (int i = 0; i < PL; ++i) {
+      const int b = PL * tid + i;
       if (b <= nb) bucket[b] = run;
       run += c[i];
     }

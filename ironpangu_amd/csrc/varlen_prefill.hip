@@ -88,14 +88,10 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
     for (int qt = 0; qt * QT < count; ++qt) atomicAdd(&bucket[cost_bucket(kv, qt, count)], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int b = 0; b < nbk; ++b) {
-      const int c = bucket[b];
-      bucket[b] = run;
-      run += c;
-    }
-    *p.n_items = run;
+  {
+    static_assert(kBuckets <= 64 * 17, "bucket_prefix covers 17 buckets per lane");
+    const int run = bucket_prefix<17>(bucket, nbk - 1, 0, tid);
+    if (tid == 0) *p.n_items = run;
   }
   __syncthreads();
   for (int seq = tid; seq < p.num_seqs; seq += 1024) {
