@@ -54,8 +54,21 @@ def test_decode_shapes(hq, hkv, hd, bs):
     assert_close(bf16_host(out), exp)
 
 
+def test_decode_head_dim_256_split_k():
+    # head_dim 256 (two-stage register ring) over several split-K partitions
+    lens = [1, 33, 2047, 2048, 2049, 6000]
+    case = W.decode_host_case(11, num_seqs=len(lens), lo=1, hi=6000, dist="uniform", q_heads=8,
+                              kv_heads=2, head_dim=256, block_size=128, pool_blocks=300)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(6), case.seq_lens, 128, 300,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(len(lens)), 128)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
 def test_decode_partition_edges_and_long():
-    # lengths around the 256-token split-K partition and 32-token tile edges
+    # lengths around the 2048-token split-K partition and 32-token tile edges
     lens = [31, 32, 33, 255, 256, 257, 511, 512, 513, 4095, 8193]
     case = W.decode_host_case(3, num_seqs=len(lens), lo=1, hi=8193, dist="uniform", q_heads=16,
                               kv_heads=2, head_dim=128, block_size=128, pool_blocks=720)
