@@ -44,16 +44,18 @@ namespace ifattn {
 // a workgroup never needs more than one wave per SIMD, so each wave may use
 // the whole register file (deep prefetch ring).
 constexpr int max_decode_waves(int) { return 4; }
-constexpr int kTile = 32;
+// Tokens per tile: 32, or 16 at head_dim 256, where a 32-token tile takes 128
+// registers and only two would fit; 16-token tiles keep four in the ring.
+constexpr int decode_tile(int d) { return d > 128 ? 16 : 32; }
 #ifndef IFATTN_DECODE_STAGES
 #define IFATTN_DECODE_STAGES 3
 #endif
-// Tile buffers per wave (stages-1 tiles prefetched). head_dim 256 holds two:
-// three 256-dim tiles (128 registers each) would not fit one wave's registers.
+// Tile buffers per wave (stages-1 tiles prefetched).
 template <int D>
-constexpr int decode_stages() { return D > 128 ? 2 : IFATTN_DECODE_STAGES; }
+constexpr int decode_stages() { return D > 128 ? 4 : IFATTN_DECODE_STAGES; }
 
-// Token of k-slot j (0..7) for lane group g within a 32-token tile.
+// Token of k-slot j (0..7) for lane group g within a 32-token tile (j < 4 in a
+// 16-token tile).
 __device__ __forceinline__ int tile_token(int g, int j) {
   return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
 }
@@ -69,14 +71,17 @@ struct VSlice {
 
 template <int D, bool C8>
 struct TileRegs {
+  static constexpr int TT = decode_tile(D);  // tokens per tile
+  static constexpr int MT = TT / 16;         // 16-token row blocks of QK^T
+  static constexpr int TPL = TT / 4;         // V tokens per lane
   // K A-operands: [mt][kstep] (bf16: 16 B each; C8: 8 B each stored in .xy)
-  u32x4 k[2][D / 32];
+  u32x4 k[MT][D / 32];
   // V: [token j][dword]: dims c*VPL .. c*VPL+VPL-1 of token tile_token(g, j)
-  uint32_t v[8][VSlice<D, C8>::DW];
-  float ks[C8 ? 8 : 1], vs[C8 ? 8 : 1];  // C8 scales for the lane's 8 tokens
+  uint32_t v[TPL][VSlice<D, C8>::DW];
+  float ks[C8 ? TPL : 1], vs[C8 ? TPL : 1];  // C8 scales for the lane's tokens
 };
 
-// Per-lane byte offsets inside a 32-token tile; identical for every tile, so
+// Per-lane byte offsets inside a tile; identical for every tile, so
 // they are computed once per work item and the per-tile cost is one scalar
 // buffer descriptor per cache.
 struct LaneOffsets {
@@ -93,10 +98,11 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
                                           int lane_blocks, int t_begin, int kvh, int t0,
                                           int t_end, const LaneOffsets &o) {
   constexpr int EB = C8 ? 1 : 2;  // element bytes
+  constexpr int TT = TileRegs<D, C8>::TT;
   const int bs = p.block_size;
   const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 - (t_begin & ~(bs - 1))) / bs);
   const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
-  const int n_live = t_end - t0 < kTile ? t_end - t0 : kTile;
+  const int n_live = t_end - t0 < TT ? t_end - t0 : TT;
   const uint32_t row_bytes = uint32_t(p.kv_heads) * D * EB;
   // Rows past the live tokens read as zero (buffer range check), which masks
   // V of a partial tile without any per-lane selects.
@@ -105,7 +111,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
   const auto rk = make_rsrc(p.k_cache + first, extent);
   const auto rv = make_rsrc(p.v_cache + first, extent);
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int mt = 0; mt < TileRegs<D, C8>::MT; ++mt) {
     if constexpr (!C8) {
 #pragma unroll
       for (int s = 0; s < D / 32; ++s) t.k[mt][s] = buf_load_x4(rk, o.k[mt] + 16 * s);
@@ -120,7 +126,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
   }
   constexpr int DW = VSlice<D, C8>::DW;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < TileRegs<D, C8>::TPL; ++j) {
     if constexpr (DW == 1) {
       t.v[j][0] = buf_load_x1(rv, o.v[j]);
     } else if constexpr (DW == 2) {
@@ -144,7 +150,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
     const auto rks = make_rsrc(p.k_scale + s0, sext);
     const auto rvs = make_rsrc(p.v_scale + s0, sext);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < TileRegs<D, C8>::TPL; ++j) {
       t.ks[j] = buf_load_f32(rks, o.sc[j]);
       t.vs[j] = buf_load_f32(rvs, o.sc[j]);
     }
@@ -227,38 +233,41 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   for (int i = 0; i < NV; ++i) oacc[i] = f32x4{0, 0, 0, 0};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  auto compute = [&](const TileRegs<D, C8> &t, int t0) {
-    f32x4 s0 = {0, 0, 0, 0}, s1 = {0, 0, 0, 0};
+  using TR = TileRegs<D, C8>;
+  constexpr int TT = TR::TT, TPL = TR::TPL;
+  auto compute = [&](const TR &t, int t0) {
+    // Scores: row block mt gives tokens 16 mt + 4g + r of head c.
+    f32x4 sacc[TR::MT];
+#pragma unroll
+    for (int mt = 0; mt < TR::MT; ++mt) sacc[mt] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
-      u32x4 a0, a1;
-      if constexpr (!C8) {
-        a0 = t.k[0][s];
-        a1 = t.k[1][s];
-      } else {
-        a0 = i8x8_to_bf16x8(t.k[0][s][0], t.k[0][s][1]);
-        a1 = i8x8_to_bf16x8(t.k[1][s][0], t.k[1][s][1]);
-      }
-      s0 = mfma16x16x32(a0, qv[s], s0);
-      s1 = mfma16x16x32(a1, qv[s], s1);
-    }
-    float x[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[r] = s0[r] * p.scale_log2;
-      x[4 + r] = s1[r] * p.scale_log2;
+      for (int mt = 0; mt < TR::MT; ++mt) {
+        u32x4 a;
+        if constexpr (!C8)
+          a = t.k[mt][s];
+        else
+          a = i8x8_to_bf16x8(t.k[mt][s][0], t.k[mt][s][1]);
+        sacc[mt] = mfma16x16x32(a, qv[s], sacc[mt]);
+      }
     }
+    float x[TPL];
+#pragma unroll
+    for (int mt = 0; mt < TR::MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[4 * mt + r] = sacc[mt][r] * p.scale_log2;
     if constexpr (C8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] *= t.ks[j];
+      for (int j = 0; j < TPL; ++j) x[j] *= t.ks[j];
     }
-    if (t_end - t0 < kTile) {  // partial last tile (wave-uniform branch)
+    if (t_end - t0 < TT) {  // partial last tile (wave-uniform branch)
       const int n_live = t_end - t0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = tile_token(g, j) < n_live ? x[j] : -INFINITY;
+      for (int j = 0; j < TPL; ++j) x[j] = tile_token(g, j) < n_live ? x[j] : -INFINITY;
     }
-    float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    if constexpr (TPL == 8) tmax = fmaxf(tmax, fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
     if (__any(tmax > m_run + kRescaleSlack)) {
@@ -269,38 +278,41 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 #pragma unroll
       for (int i = 0; i < NV; ++i) oacc[i] *= alpha;
     }
-    float pr[8];
+    float pr[TPL];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(x[j] - m_run);
-    l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    for (int j = 0; j < TPL; ++j) pr[j] = fast_exp2(x[j] - m_run);
+    float psum = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    if constexpr (TPL == 8) psum += (pr[4] + pr[5]) + (pr[6] + pr[7]);
+    l_run += psum;
     if constexpr (C8) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[j] *= t.vs[j];
+      for (int j = 0; j < TPL; ++j) pr[j] *= t.vs[j];
     }
-    const u32x4 pb = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                      pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
+    uint32_t pb[TPL / 2];
+#pragma unroll
+    for (int i = 0; i < TPL / 2; ++i) pb[i] = pack_bf16x2(pr[2 * i], pr[2 * i + 1]);
     // PV: MFMA b produces O^T rows m = c <-> dim c*VPL + b; its A operand is
-    // element b of the lane's eight tokens, paired into bf16x2 words.
+    // element b of the lane's tokens, paired into bf16x2 words (16x16x32 for
+    // 32-token tiles, 16x16x16 for 16-token tiles).
     constexpr int VPL = VSlice<D, C8>::VPL;
 #pragma unroll
     for (int b = 0; b < VPL; ++b) {
-      u32x4 a;
-      if constexpr (!C8) {
-        const int w = b >> 1;
-        if (b & 1)
-          a = u32x4{pack_hi16(t.v[0][w], t.v[1][w]), pack_hi16(t.v[2][w], t.v[3][w]),
-                    pack_hi16(t.v[4][w], t.v[5][w]), pack_hi16(t.v[6][w], t.v[7][w])};
-        else
-          a = u32x4{pack_lo16(t.v[0][w], t.v[1][w]), pack_lo16(t.v[2][w], t.v[3][w]),
-                    pack_lo16(t.v[4][w], t.v[5][w]), pack_lo16(t.v[6][w], t.v[7][w])};
-      } else {
-        const int w = b >> 2, y = b & 3;
-        a = u32x4{i8pair_to_bf16x2(i8_at(t.v[0][w], y), i8_at(t.v[1][w], y)),
-                  i8pair_to_bf16x2(i8_at(t.v[2][w], y), i8_at(t.v[3][w], y)),
-                  i8pair_to_bf16x2(i8_at(t.v[4][w], y), i8_at(t.v[5][w], y)),
-                  i8pair_to_bf16x2(i8_at(t.v[6][w], y), i8_at(t.v[7][w], y))};
+      uint32_t a[TPL / 2];
+#pragma unroll
+      for (int i = 0; i < TPL / 2; ++i) {
+        if constexpr (!C8) {
+          const int w = b >> 1;
+          a[i] = (b & 1) ? pack_hi16(t.v[2 * i][w], t.v[2 * i + 1][w])
+                         : pack_lo16(t.v[2 * i][w], t.v[2 * i + 1][w]);
+        } else {
+          const int w = b >> 2, y = b & 3;
+          a[i] = i8pair_to_bf16x2(i8_at(t.v[2 * i][w], y), i8_at(t.v[2 * i + 1][w], y));
+        }
       }
-      oacc[b] = mfma16x16x32(a, pb, oacc[b]);
+      if constexpr (TPL == 8)
+        oacc[b] = mfma16x16x32(u32x4{a[0], a[1], a[2], a[3]}, u32x4{pb[0], pb[1], pb[2], pb[3]}, oacc[b]);
+      else
+        oacc[b] = mfma16x16x16(u32x2{a[0], a[1]}, u32x2{pb[0], pb[1]}, oacc[b]);
     }
   };
 
@@ -309,21 +321,21 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   // cache hit) so every iteration has the same shape.
   constexpr int kStages = decode_stages<D>();
   TileRegs<D, C8> tr[kStages];
-  auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (kTile - 1)); };
+  auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (TT - 1)); };
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i)
-    load_tile<D, C8>(tr[i], p, lane_blocks, t_begin, kvh, clamp_tile(t_begin + i * kTile), t_end, o);
+    load_tile<D, C8>(tr[i], p, lane_blocks, t_begin, kvh, clamp_tile(t_begin + i * TT), t_end, o);
   int t0 = t_begin;
   while (true) {
 #pragma unroll
     for (int i = 0; i < kStages; ++i) {
       load_tile<D, C8>(tr[(i + kStages - 1) % kStages], p, lane_blocks, t_begin, kvh,
-                       clamp_tile(t0 + (kStages - 1) * kTile), t_end, o);
+                       clamp_tile(t0 + (kStages - 1) * TT), t_end, o);
       // Keep the prefetch issued ahead of this tile's math (the scheduler would
       // otherwise sink it below the QK^T MFMAs and shrink the loads in flight).
       __builtin_amdgcn_sched_barrier(0);
       compute(tr[i], t0);
-      t0 += kTile;
+      t0 += TT;
       if (t0 >= t_end) break;
     }
     if (t0 >= t_end) break;
