@@ -9,26 +9,29 @@
 // (grouping kh = h / (q_heads/kv_heads) at :226). slot(b,j) = table[b][j/bs]*bs + j%bs
 // (native/src/page_binding.h:56-59).
 //
-// Work decomposition (one launch, grid = seqs x partitions x kv-head groups):
+// Work decomposition: a prologue kernel lists (sequence, partition) items
+// longest first; a persistent grid (two workgroups per CU) pulls them from a
+// device queue:
 //  * a workgroup owns a `part_tokens` slice of one sequence; each of its waves
 //    owns one kv head, so the two waves of a 2-kv-head model stream the two
 //    halves of the same 512-byte cache rows at the same time;
-//  * a wave walks 32-token tiles. QK^T is one MFMA 16x16x32 bf16 per (16 tokens,
-//    32 dims): A = K rows straight from HBM (16 B per lane), B = the group's q
-//    heads (n = head, zero-padded to 16). The score tile lands with lane
-//    (c = lane%16, g = lane/16) holding tokens 4g..4g+3 and 16+4g..16+4g+3 of
-//    head c, so P never leaves registers: it is exactly the B operand of the
-//    PV MFMA once those eight tokens are declared the lane's k-slots;
-//  * PV is O^T = V^T P^T: the A operand needs eight tokens of one dimension,
-//    fetched as dword gathers (two adjacent dims) and split into even/odd dims
+//  * a wave walks 32-token tiles (16-token tiles at head_dim 256). QK^T is one
+//    MFMA 16x16x32 bf16 per (16 tokens, 32 dims): A = K rows straight from HBM
+//    (16 B per lane), B = the group's q heads (n = head, zero-padded to 16).
+//    The score tile lands with lane (c = lane%16, g = lane/16) holding tokens
+//    4g..4g+3 (and 16+4g..16+4g+3) of head c, so P never leaves registers: it
+//    is exactly the B operand of the PV MFMA once those tokens are declared
+//    the lane's k-slots;
+//  * PV is O^T = V^T P^T: the A operand needs the lane's tokens of one
+//    dimension, fetched as 16-byte token loads and split into even/odd dims
 //    with v_perm, so V is never staged or transposed through LDS;
-//  * online softmax in the exp2 domain; max/sum across the four lane groups by
-//    two xor shuffles per tile;
+//  * online softmax in the exp2 domain with lazy rescaling; max/sum across
+//    the four lane groups by permlane swaps;
 //  * sequences longer than one partition write (m, l, unnormalised O) partials
 //    and a second kernel merges them (split-K); single-partition sequences
 //    write bf16 output directly.
-//  * the next tile's loads are issued before the current tile's math (register
-//    double buffering), keeping ~16 KiB in flight per wave.
+//  * a register ring of decode_stages() tiles keeps the next tiles' loads in
+//    flight while the current tile is reduced.
 // C8: K/V int8 with an fp32 scale per (token, kv head). int8 -> bf16 is exact,
 // so QK^T runs on the integer codes and the K scale multiplies the score; the
 // V scale is folded into the probability before the PV MFMA.
