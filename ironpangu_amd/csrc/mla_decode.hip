@@ -104,6 +104,10 @@ __device__ __forceinline__ MlaSpan mla_span(const MlaParams &p, int row, int seq
   }
   return s;
 }
+// Partition field of a row's sink item. With sinks a row has at most 4095
+// partition slots, the last for the sinks, so partitions stay below it.
+constexpr uint32_t kSinkItem = 0xFFFu;
+
 __device__ __forceinline__ int mla_parts(const MlaSpan &s, int pt) {
   return s.hi > s.lo ? (s.hi - s.base + pt - 1) / pt : 0;
 }
@@ -119,7 +123,7 @@ __device__ __forceinline__ int mla_part_size(const MlaSpan &s, int pt, int k) {
 __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
   constexpr int kBuckets = 257;
   __shared__ int bucket[kBuckets];
-  __shared__ int carry;
+  __shared__ int carry, sink_base;
   __shared__ int wave_tot[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int PT = p.part_tokens;
@@ -171,10 +175,15 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     const int run = bucket_prefix(bucket, nb, carry, tid);
     if (tid == 0) {
       p.queue[0] = p.static_items;
-      p.queue[1] = run;
+      p.queue[1] = run + (p.n_sinks > 0 ? p.num_rows : 0);
+      sink_base = run;
     }
   }
   __syncthreads();
+  // One sink item per row after every partition item.
+  if (p.n_sinks > 0)
+    for (int row = tid; row < p.num_rows; row += 1024)
+      p.items[sink_base + row] = (uint32_t(row) << 12) | kSinkItem;
   for (int base = 0; base < p.num_rows; base += 1024) {
     const int row = base + tid;
     if (row >= p.num_rows) continue;
@@ -574,40 +583,14 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   }
 }
 
-template <bool C8, bool SPARSE>
-__global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaParams p) {
-  __shared__ __align__(16) uint8_t ring[kMlaLds];
-  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
-  __shared__ uint32_t slot_list[SPARSE ? kSparsePart : 1];
-  // The item index travels through the score buffer, idle between items.
-  int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
-  const int lane = threadIdx.x & 63;
-  const int w = uniform(int(threadIdx.x >> 6));
-  // Item blockIdx.x first (the plan starts the queue after the static items);
-  // each item pops its successor up front, so the queue round trip overlaps the
-  // item's own loads.
-  const int total = p.queue[1];
-  int it = blockIdx.x;
-  while (it < total) {
-    int next = 0;
-    if (threadIdx.x == 0) next = atomicAdd(p.queue, 1);
-    const uint32_t e = uniform(p.items[it]);
-    mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
-    __syncthreads();  // every wave is done with xbuf (and the ring)
-    if (threadIdx.x == 0) *item_slot = next;
-    __syncthreads();
-    it = uniform(*item_slot);
-  }
-}
-
 // Learned sink rows of one query row (keys [n, 576], values [n, 512] bf16,
 // shared by every row, so they are read from L2): the same tile math as the
 // cache keys, four waves per row, heads in the MFMA N dimension. The (m, l, O)
-// partial of the sinks alone goes to the row's last partial slot.
-__global__ __launch_bounds__(64 * kMlaWaves) void mla_sink_kernel(MlaParams p) {
-  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
-  const int row = blockIdx.x, lane = threadIdx.x & 63;
-  const int w = uniform(int(threadIdx.x >> 6));
+// partial of the sinks alone goes to the row's last partial slot. Runs as one
+// item of the attention kernel's queue (after every partition item, so these
+// short items fill the tail).
+__device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int w,
+                                              int lane) {
   const int c = lane & 15, g = lane >> 4, n = p.n_sinks;
   const bool head_live = c < p.heads;
   u32x4 qv[5];
@@ -655,6 +638,35 @@ __global__ __launch_bounds__(64 * kMlaWaves) void mla_sink_kernel(MlaParams p) {
         f32x4{acc.o[b][r], acc.o[b + 1][r], acc.o[b + 2][r], acc.o[b + 3][r]};
   }
   if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
+}
+
+template <bool C8, bool SPARSE>
+__global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaParams p) {
+  __shared__ __align__(16) uint8_t ring[kMlaLds];
+  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
+  __shared__ uint32_t slot_list[SPARSE ? kSparsePart : 1];
+  // The item index travels through the score buffer, idle between items.
+  int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(int(threadIdx.x >> 6));
+  // Item blockIdx.x first (the plan starts the queue after the static items);
+  // each item pops its successor up front, so the queue round trip overlaps the
+  // item's own loads.
+  const int total = p.queue[1];
+  int it = blockIdx.x;
+  while (it < total) {
+    int next = 0;
+    if (threadIdx.x == 0) next = atomicAdd(p.queue, 1);
+    const uint32_t e = uniform(p.items[it]);
+    if (p.n_sinks > 0 && (e & 0xfffu) == kSinkItem)
+      mla_sink_item(p, xbuf, int(e >> 12), w, lane);
+    else
+      mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
+    __syncthreads();  // every wave is done with xbuf (and the ring)
+    if (threadIdx.x == 0) *item_slot = next;
+    __syncthreads();
+    it = uniform(*item_slot);
+  }
 }
 
 // Combine one (row, head): the row's partition partials and, with sinks, the
@@ -826,7 +838,6 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   p.static_items = device_cus();  // the attention grid
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
-  if (c.n_sinks > 0) mla_sink_kernel<<<c.num_rows, 64 * kMlaWaves, 0, s>>>(p);
   const int grid = device_cus();
   if (c.c8) {
     if (sparse) mla_attention_kernel<true, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
