@@ -271,11 +271,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
   };
 
   f32x4 oacc[NB][VPL];
-  float m_run[NB], l_run[NB];
+  // Softmax denominators: an extra PV MFMA with an all-ones A operand sums
+  // the bf16 probabilities of each column over every key (all four rows of
+  // lacc hold the same sum), instead of per-lane VALU adds and a cross-lane
+  // reduction; the sum is of exactly the values the numerator used.
+  f32x4 lacc[NB];
+  float m_run[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     m_run[nb] = -INFINITY;
-    l_run[nb] = 0.0f;
+    lacc[nb] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int b = 0; b < VPL; ++b) oacc[nb][b] = f32x4{0, 0, 0, 0};
   }
@@ -336,7 +341,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
         const float m_new = fmaxf(m_run[nb], tmax);
         const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run[nb] - m_new);
         m_run[nb] = m_new;
-        l_run[nb] *= alpha;
+        lacc[nb] *= alpha;
 #pragma unroll
         for (int b = 0; b < VPL; ++b) oacc[nb][b] *= alpha;
       }
@@ -346,7 +351,6 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
         float pr[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) pr[j] = fast_exp2(__builtin_fmaf(x[8 * h + j], p.scale_log2, -m_use));
-        l_run[nb] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
         pb[h][nb] = u32x4{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
                           pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
       }
@@ -377,6 +381,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) oacc[nb][b] = mfma16x16x32(a, pb[h][nb], oacc[nb][b]);
       }
+      const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) lacc[nb] = mfma16x16x32(ones, pb[h][nb], lacc[nb]);
     }
   };
 
@@ -421,8 +428,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
 
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    float l_tot = sum_xor16(l_run[nb]);
-    l_tot = sum_xor32(l_tot);
+    const float l_tot = lacc[nb][0];
     if (!live[nb]) continue;
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t *op = p.out + (qrow[nb] * p.q_heads + head[nb]) * D + 4 * g;
