@@ -736,8 +736,9 @@ struct MlaCall {
 
 // Partition size of a call: the default (sparse lists: kSparsePart entries),
 // shrunk for small calls so that the largest possible key count still makes
-// about two items per workgroup (the rows' key counts are only known on the
-// device), and never below 256 keys. A dense partition starting on a 32-token
+// about one item per workgroup (the rows' key counts are only known on the
+// device; two per workgroup measured 5-13% slower on 128-row window and
+// sparse calls, whose rows are all full), and never below 256 keys. A dense partition starting on a 32-token
 // tile spans 1 + ceil((PT - 32) / bs) blocks, at most the 64 one wave holds:
 // PT <= 63 * bs + 32.
 inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int window,
@@ -748,7 +749,7 @@ inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int 
     pt = pt < cap ? pt : cap;
   }
   const int64_t keys = sparse ? topk : (window > 0 && window < max_context ? window : max_context);
-  const int64_t fit = keys * rows / (2 * int64_t(device_cus()) * wgs_mla());
+  const int64_t fit = keys * rows / (int64_t(device_cus()) * wgs_mla());
   const int64_t want = fit < 256 ? 256 : (fit & ~int64_t(31));
   return want < pt ? int(want) : pt;
 }
