@@ -470,9 +470,8 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   p.table_stride = table_stride;
   p.block_size = block_size;
   p.max_context = max_context;
-  p.part_tokens = part_tokens();
-
-  p.max_parts = max_parts_for(max_context);
+  p.part_tokens = part_tokens(c8);
+  p.max_parts = max_parts_for(max_context, c8);
   p.scale_log2 = scale * kLog2e;
   if (p.max_parts > 4096) return fail(IFATTN_EINVAL, "paged decode: max_context above 1M tokens");
   if (p.part_tokens > 64 * block_size)

@@ -279,18 +279,31 @@ inline void launch_merge(const DecodeParams &p, hipStream_t s) {
 
 constexpr uint64_t kQueueBytes = 64;
 
-// Tokens per split-K partition (a multiple of the 32-token tile). The
-// IFATTN_DECODE_PART_TOKENS environment variable overrides it for tuning.
-inline int part_tokens() {
+// Tokens per split-K partition (a multiple of the 32-token tile): 2048 for
+// bf16 caches, 1536 for C8 caches. The longest-first list ends with the
+// partial partitions filling the workgroups' tails, and how well they fit
+// depends on the partition size: C8 over 256 sequences of U[1024, 16384]
+// tokens measured 234 us at 1536 against 253 us at 1024, 2048, 3072 and 4096;
+// bf16 over log-uniform [128, 32768] measured 2048 and 1792 alike, 1216 and
+// 2560 slower. The IFATTN_DECODE_PART_TOKENS environment variable overrides
+// both for tuning.
+inline int part_tokens(bool c8 = false) {
   static int v = [] {
     const char *e = getenv("IFATTN_DECODE_PART_TOKENS");
     int x = e ? atoi(e) : 0;
-    return (x >= 32 && x <= 8192 && x % 32 == 0) ? x : 2048;
+    return (x >= 32 && x <= 8192 && x % 32 == 0) ? x : 0;
   }();
-  return v;
+  return v ? v : (c8 ? 1536 : 2048);
 }
 
-inline int max_parts_for(int max_context) { return (max_context + part_tokens() - 1) / part_tokens(); }
+inline int max_parts_for(int max_context, bool c8 = false) {
+  return (max_context + part_tokens(c8) - 1) / part_tokens(c8);
+}
+// Partition count the workspace is sized for (either cache type).
+inline int max_parts_any(int max_context) {
+  const int a = max_parts_for(max_context, false), b = max_parts_for(max_context, true);
+  return a > b ? a : b;
+}
 
 inline uint64_t align16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
 
@@ -323,7 +336,7 @@ inline int wgs_per_cu() {
 
 // Workspace layout: queue words | items | partial O | partial (m, l).
 inline uint64_t split_k_workspace_bytes(int num_seqs, int heads, int dims, int max_context) {
-  const uint64_t items = uint64_t(num_seqs) * uint64_t(max_parts_for(max_context));
+  const uint64_t items = uint64_t(num_seqs) * uint64_t(max_parts_any(max_context));
   const uint64_t partials = items > uint64_t(num_seqs)  // single-partition calls keep no partials
                                 ? items * heads * (uint64_t(dims) + 2) * sizeof(float)
                                 : 0;
