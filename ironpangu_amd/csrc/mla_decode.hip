@@ -42,7 +42,6 @@ constexpr int kMlaWaves = 4;
 constexpr int kMlaTile = 32;
 constexpr int kSparsePart = 1024;  // index-list entries per sparse partition
 constexpr int kMaxSinks = 128;
-inline int wgs_mla() { return 1; }  // persistent workgroups per CU (LDS-bound)
 
 struct MlaParams {
   const uint16_t *q;            // [rows, heads, 576]
@@ -204,7 +203,6 @@ struct MlaRow {
   // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16) / 1312 (C8) 16-byte chunks.
   static constexpr int NI = C8 ? 6 : 9;
   static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
-  static constexpr int STAGES = C8 ? 6 : 4;
   // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B: odd rows
   // start half a bank period in) XOR the latent chunk index with the row's low
   // 4 bits, which puts the 16 rows of one K read on 16 distinct bank groups;
@@ -217,16 +215,25 @@ struct MlaRow {
     return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ key(r, j));
   }
 };
-static_assert(MlaRow<false>::SLOT * MlaRow<false>::STAGES + 4 * 64 * 32 + 4 * kSparsePart <= 160 * 1024, "LDS");
-static_assert(MlaRow<true>::SLOT * MlaRow<true>::STAGES + 4 * 64 * 32 + 4 * kSparsePart <= 160 * 1024, "LDS");
 static_assert(MlaRow<false>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
 static_assert(18 * 64 == 16 * 72, "bf16 loads 0..17 move exactly tile rows 0..15");
 static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 
-constexpr int kMlaLds =
-    MlaRow<false>::SLOT * MlaRow<false>::STAGES > MlaRow<true>::SLOT * MlaRow<true>::STAGES
-        ? MlaRow<false>::SLOT * MlaRow<false>::STAGES
-        : MlaRow<true>::SLOT * MlaRow<true>::STAGES;
+// Ring depth and persistent workgroups per CU of each kernel variant. One
+// workgroup of four waves holds a tile in flight per wave-slot of LDS; the
+// C8 dense variant runs two workgroups per CU (two waves per SIMD) because its
+// 21-KB tiles arrive faster than one workgroup's tile math retires them (one
+// workgroup with 6 stages: 582 us on 128 rows of log-uniform [1024, 65536]
+// keys, two with 3 stages each: see the measurements in the notes).
+template <bool C8, bool SPARSE>
+struct MlaCfg {
+  static constexpr int WGS = (C8 && !SPARSE) ? 2 : 1;
+  static constexpr int STAGES = !C8 ? 4 : (SPARSE ? 6 : 3);
+  static constexpr int RING = MlaRow<C8>::SLOT * STAGES;
+  static constexpr int LDS = RING + kMlaWaves * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
+  static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
+};
+inline int wgs_mla(bool c8, bool sparse) { return (c8 && !sparse) ? 2 : 1; }
 
 constexpr uint32_t kNoRow = 0xFFFFFFFFu;  // sparse slot list: no key
 
@@ -364,7 +371,7 @@ template <bool C8, bool SPARSE>
 __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
                                          uint32_t *slot_list, int row, int part, int w, int lane) {
   using R = MlaRow<C8>;
-  constexpr int S = R::STAGES;
+  constexpr int S = MlaCfg<C8, SPARSE>::STAGES;
   constexpr int DV = 512;
   const int PT = p.part_tokens;
   const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
@@ -641,10 +648,16 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
 }
 
 template <bool C8, bool SPARSE>
-__global__ __launch_bounds__(64 * kMlaWaves, 1) void mla_attention_kernel(MlaParams p) {
-  __shared__ __align__(16) uint8_t ring[kMlaLds];
+__global__ __launch_bounds__(64 * kMlaWaves, (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
+  __shared__ __align__(16) uint8_t ring[MlaCfg<C8, SPARSE>::RING];
   __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
-  __shared__ uint32_t slot_list[SPARSE ? kSparsePart : 1];
+  // The sparse slot list lives in the workgroup's LDS only for sparse calls
+  // (the dense C8 variant fits two workgroups per CU exactly).
+  uint32_t *slot_list = nullptr;
+  if constexpr (SPARSE) {
+    __shared__ uint32_t sparse_slots[kSparsePart];
+    slot_list = sparse_slots;
+  }
   // The item index travels through the score buffer, idle between items.
   int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
   const int lane = threadIdx.x & 63;
@@ -754,7 +767,7 @@ inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int 
     pt = pt < cap ? pt : cap;
   }
   const int64_t keys = sparse ? topk : (window > 0 && window < max_context ? window : max_context);
-  const int64_t fit = keys * rows / (int64_t(device_cus()) * wgs_mla());
+  const int64_t fit = keys * rows / int64_t(device_cus());
   const int64_t want = fit < 256 ? 256 : (fit & ~int64_t(31));
   return want < pt ? int(want) : pt;
 }
@@ -842,9 +855,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_o = partials ? reinterpret_cast<float *>(ws) : nullptr;
   p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
-  p.static_items = device_cus();  // the attention grid
+  const int grid = device_cus() * wgs_mla(c.c8, sparse);
+  p.static_items = grid;  // the attention grid takes the first items by index
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
-  const int grid = device_cus();
   if (c.c8) {
     if (sparse) mla_attention_kernel<true, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
     else mla_attention_kernel<true, false><<<grid, 64 * kMlaWaves, 0, s>>>(p);
