@@ -219,21 +219,23 @@ static_assert(MlaRow<false>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
 static_assert(18 * 64 == 16 * 72, "bf16 loads 0..17 move exactly tile rows 0..15");
 static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 
-// Ring depth and persistent workgroups per CU of each kernel variant. One
-// workgroup of four waves holds a tile in flight per wave-slot of LDS; the
-// C8 dense variant runs two workgroups per CU (two waves per SIMD) because its
-// 21-KB tiles arrive faster than one workgroup's tile math retires them (one
-// workgroup with 6 stages: 582 us on 128 rows of log-uniform [1024, 65536]
-// keys, two with 3 stages each: see the measurements in the notes).
+// Ring depth and persistent workgroups per CU of each kernel variant. bf16
+// runs one workgroup of four waves per CU with a 4-tile ring (its 36-KB tiles
+// keep HBM busy while the tile math runs). C8 runs two workgroups per CU (two
+// waves per SIMD): its 21-KB tiles arrive faster than one workgroup's tile
+// math retires them, and a second workgroup overlaps that math. Measured on
+// 128 rows: C8 decode over log-uniform [1024, 65536] keys 582 us with one
+// workgroup and 6 stages, 456 us with two and 3 stages; sparse top-2048
+// 95.9 us with one workgroup and 6 stages, 75.9 us with two and 2 stages.
 template <bool C8, bool SPARSE>
 struct MlaCfg {
-  static constexpr int WGS = (C8 && !SPARSE) ? 2 : 1;
-  static constexpr int STAGES = !C8 ? 4 : (SPARSE ? 6 : 3);
+  static constexpr int WGS = C8 ? 2 : 1;
+  static constexpr int STAGES = !C8 ? 4 : (SPARSE ? 2 : 3);
   static constexpr int RING = MlaRow<C8>::SLOT * STAGES;
   static constexpr int LDS = RING + kMlaWaves * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
-inline int wgs_mla(bool c8, bool sparse) { return (c8 && !sparse) ? 2 : 1; }
+inline int wgs_mla(bool c8) { return c8 ? 2 : 1; }
 
 constexpr uint32_t kNoRow = 0xFFFFFFFFu;  // sparse slot list: no key
 
@@ -754,26 +756,28 @@ constexpr int kMlaDensePart = 3072;
 
 // Partition size of a call: the default (sparse lists: kSparsePart entries),
 // shrunk for small calls so that the largest possible key count still makes
-// about one item per workgroup (the rows' key counts are only known on the
-// device; two per workgroup measured 5-13% slower on 128-row window and
-// sparse calls, whose rows are all full), and never below 256 keys. A dense partition starting on a 32-token
-// tile spans 1 + ceil((PT - 32) / bs) blocks, at most the 64 one wave holds:
-// PT <= 63 * bs + 32.
+// about one item per workgroup of the `wgs`-per-CU grid (the rows' key counts
+// are only known on the device; two items per workgroup measured 5-13% slower
+// on 128-row window and sparse calls, whose rows are all full), and never
+// below 256 keys. A dense partition starting on a 32-token tile spans
+// 1 + ceil((PT - 32) / bs) blocks, at most the 64 one wave holds:
+// PT <= 63 * bs + 32. Workspace sizes assume the smaller partitions of the
+// two-workgroup grid, which covers either cache type.
 inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int window,
-                           int max_context) {
+                           int max_context, int wgs) {
   int pt = sparse ? kSparsePart : kMlaDensePart;
   if (!sparse) {
     const int cap = (63 * block_size + 32) & ~31;
     pt = pt < cap ? pt : cap;
   }
   const int64_t keys = sparse ? topk : (window > 0 && window < max_context ? window : max_context);
-  const int64_t fit = keys * rows / int64_t(device_cus());
+  const int64_t fit = keys * rows / (int64_t(device_cus()) * wgs);
   const int64_t want = fit < 256 ? 256 : (fit & ~int64_t(31));
   return want < pt ? int(want) : pt;
 }
 inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size,
-                             int rows) {
-  const int pt = mla_part_tokens(sparse, block_size, rows, topk, window, max_context);
+                             int rows, int wgs) {
+  const int pt = mla_part_tokens(sparse, block_size, rows, topk, window, max_context, wgs);
   if (sparse) return (topk + pt - 1) / pt;
   const int full = (max_context + pt - 1) / pt;
   if (window <= 0) return full;
@@ -812,8 +816,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
     return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
-  const int pt = mla_part_tokens(sparse, c.block_size, c.num_rows, c.topk, c.window, c.max_context);
-  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, c.num_rows) +
+  const int wgs = wgs_mla(c.c8);
+  const int pt = mla_part_tokens(sparse, c.block_size, c.num_rows, c.topk, c.window, c.max_context, wgs);
+  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, c.num_rows, wgs) +
                   (c.n_sinks > 0 ? 1 : 0);  // sinks: one more partial slot per row
   if (ppr > 4096) return fail(IFATTN_EINVAL, what, "more than 4096 partitions per row");
   const bool partials = ppr > 1 || c.n_sinks > 0;
@@ -855,7 +860,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_o = partials ? reinterpret_cast<float *>(ws) : nullptr;
   p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
-  const int grid = device_cus() * wgs_mla(c.c8, sparse);
+  const int grid = device_cus() * wgs;
   p.static_items = grid;  // the attention grid takes the first items by index
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
@@ -901,7 +906,7 @@ using namespace ifattn;
 extern "C" uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads,
                                                      int32_t max_context, int32_t block_size) {
   if (num_seqs <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
-  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size, num_seqs);
+  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size, num_seqs, 2);
   return mla_workspace(num_seqs, heads, ppr, ppr > 1);
 }
 
@@ -936,7 +941,7 @@ extern "C" uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_
   if (num_rows <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
   const bool sparse = topk > 0;
   const int ppr =
-      mla_parts_per_row(sparse, topk, window, max_context, block_size, num_rows) + (n_sinks > 0 ? 1 : 0);
+      mla_parts_per_row(sparse, topk, window, max_context, block_size, num_rows, 2) + (n_sinks > 0 ? 1 : 0);
   return mla_workspace(num_rows, heads, ppr, ppr > 1 || n_sinks > 0);
 }
 
