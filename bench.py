@@ -518,16 +518,19 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # HIP events on the stream the kernels are launched on (torch's current
+    # stream, which ops.* passes to the library), around the timed region.
+    launch_stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    start.record(launch_stream)
     for _ in range(args.steps):
         step()
-    end.record()
+    end.record(launch_stream)
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / args.steps
 
-    # Operator duration (prologue with the row writes + decode with the fused
-    # split-K merge), bracketed by HIP events on the stream the kernels run on.
+    # Also each step bracketed by its own event pair (includes the event
+    # packets between steps); reported beside the timed-region figure.
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -540,7 +543,7 @@ def main():
     nbytes = W.decode_bytes(case.seq_lens, case.q_heads, case.kv_heads, case.head_dim,
                             case.block_size)
     value = nbytes["total"] / (ms_step * 1e-3) / 1e9
-    achieved = nbytes["total"] / (attn_avg * 1e-3) / 1e9
+    achieved = value  # operator launches over the timed region, per step
     res = {
         "metric": "paged-decode attention GB/s (% of 8 TB/s HBM) + decode tokens/s, 256 ragged seqs",
         "value": round(value, 2),
@@ -569,7 +572,10 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "traffic_note": "HBM bytes per decode-kernel launch, rocprofv3 FETCH_SIZE x2.0 + "
                                      "WRITE_SIZE x1.0 (profiles/hbm_traffic_decode_kernels.md)",
-                     "avg_ms": round(attn_avg, 5),
+                     "avg_ms": round(ms_step, 5),
+                     "avg_ms_note": "HIP events on the launch stream around the timed steps / steps; "
+                                    "the three kernels run back to back (rocprof: prologue + decode + merge)",
+                     "isolated_step_ms": round(attn_avg, 5),
                      "algorithmic_bytes": nbytes["total"]},
     }
     if not args.no_cpu_baseline:
