@@ -73,6 +73,26 @@ def test_c8_decode(hd, bs):
     assert_close(bf16_host(out), exp)
 
 
+def test_c8_decode_many_partitions():
+    # more than 16 split-K partitions (1536-token partitions for C8 caches)
+    import torch
+    from ironpangu_amd import ops
+    case = W.decode_host_case(10, num_seqs=2, lo=1, hi=30000, dist="uniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=128, pool_blocks=480, c8=True)
+    case.seq_lens[:] = [30000, 24577]
+    case.block_tables = W.block_tables_for(np.random.default_rng(9), case.seq_lens, 128, 480,
+                                           case.block_tables.shape[1])
+    kc, vc, ks, vs = _quantize_pool_on_gpu(case)
+    out = ops.paged_decode(to_dev(case.host["q"]), kc, vc, to_dev(case.block_tables),
+                           to_dev(case.seq_lens), case.max_context, case.scale,
+                           k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    exp = oracle.paged_decode(case.host["q"], kc.cpu().numpy(), vc.cpu().numpy(),
+                              case.block_tables, case.seq_lens, 16, 2, 128, 128, case.scale,
+                              k_scale=ks.cpu().numpy(), v_scale=vs.cpu().numpy())
+    assert_close(bf16_host(out), exp)
+
+
 def test_mla_c8_write_bit_exact():
     import torch
     from ironpangu_amd import ops

@@ -67,6 +67,19 @@ def test_decode_head_dim_256_split_k():
     assert_close(bf16_host(out), exp)
 
 
+def test_decode_many_partitions():
+    # more than 16 split-K partitions per sequence: the merge's multi-round path
+    lens = [1, 40000, 70001]
+    case = W.decode_host_case(13, num_seqs=len(lens), lo=1, hi=70001, dist="uniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=128, pool_blocks=1800)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(8), case.seq_lens, 128, 1800,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(len(lens)), 128)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
 def test_decode_partition_edges_and_long():
     # lengths around the 2048-token split-K partition and 32-token tile edges
     lens = [31, 32, 33, 255, 256, 257, 511, 512, 513, 4095, 8193]
