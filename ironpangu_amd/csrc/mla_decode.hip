@@ -41,6 +41,7 @@ namespace ifattn {
 constexpr int kMlaWaves = 4;
 constexpr int kMlaTile = 32;
 constexpr int kSparsePart = 1024;  // index-list entries per sparse partition
+
 constexpr int kMaxSinks = 128;
 
 struct MlaParams {
@@ -230,12 +231,26 @@ static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 template <bool C8, bool SPARSE>
 struct MlaCfg {
   static constexpr int WGS = C8 ? 2 : 1;
+  // Waves per workgroup. Eight waves with 64-dim slices measured slower for
+  // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
+  // the score exchange then sums eight partials per tile.
+  static constexpr int NW = kMlaWaves;
   static constexpr int STAGES = !C8 ? 4 : (SPARSE ? 2 : 3);
   static constexpr int RING = MlaRow<C8>::SLOT * STAGES;
-  static constexpr int LDS = RING + kMlaWaves * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
+  static constexpr int LDS = RING + NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
 inline int wgs_mla(bool c8) { return c8 ? 2 : 1; }
+// Wave geometry of a workgroup of NW waves: wave w owns the latent dims
+// [DPW w, DPW w + DPW) for QK^T and PV (KS k-steps of 32), waves 0 and 1 add
+// 32 rope dims each; a lane holds EPL dims of each of its eight V tokens and
+// the wave runs EPL PV MFMAs (16 dims each).
+template <int NW>
+struct MlaGeo {
+  static constexpr int DPW = 512 / NW;
+  static constexpr int KS = DPW / 32;
+  static constexpr int EPL = DPW / 16;
+};
 
 constexpr uint32_t kNoRow = 0xFFFFFFFFu;  // sparse slot list: no key
 
@@ -258,20 +273,24 @@ __device__ __forceinline__ u32x4 mla_i8x8(uint32_t lo, uint32_t hi) {
 // keys. The four waves' partial scores are summed through xbuf (one barrier;
 // every wave finished reading xbuf before the barrier that began this tile).
 // Keys whose bit is clear in `live` get probability 0.
+template <int EPL>
 struct MlaAcc {
-  f32x4 o[8];
+  f32x4 o[EPL];
   float m, l;
 };
 
-template <bool C8>
-__device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5], const u32x4 (&v)[8],
-                                              const float *sk, const u32x4 (&qv)[5],
+template <bool C8, int NW>
+__device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
+                                              const u32x4 (&k)[2][MlaGeo<NW>::KS + 1],
+                                              const u32x4 (&v)[8], const float *sk,
+                                              const u32x4 (&qv)[MlaGeo<NW>::KS + 1],
                                               float (*xbuf)[8], uint32_t live, float scale_log2,
                                               int w, int lane) {
+  constexpr int KS = MlaGeo<NW>::KS, EPL = MlaGeo<NW>::EPL;
   const int g = lane >> 4;
   f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < KS; ++s) {
     if constexpr (C8) {
       a0 = mfma16x16x32(mla_i8x8(k[0][s][0], k[0][s][1]), qv[s], a0);
       a1 = mfma16x16x32(mla_i8x8(k[1][s][0], k[1][s][1]), qv[s], a1);
@@ -291,22 +310,22 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5
     for (int j = 0; j < 8; ++j) part_s[j] *= sk[j];
   }
   if (w < 2) {
-    f32x4 r0 = mfma16x16x32(k[0][4], qv[4], f32x4{0, 0, 0, 0});
-    f32x4 r1 = mfma16x16x32(k[1][4], qv[4], f32x4{0, 0, 0, 0});
+    f32x4 r0 = mfma16x16x32(k[0][KS], qv[KS], f32x4{0, 0, 0, 0});
+    f32x4 r1 = mfma16x16x32(k[1][KS], qv[KS], f32x4{0, 0, 0, 0});
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       part_s[r] += r0[r];
       part_s[4 + r] += r1[r];
     }
   }
-  // Sum the four waves' partial scores. The buffer is free again: every wave
+  // Sum the waves' partial scores. The buffer is free again: every wave
   // finished reading it before the barrier that starts this tile.
   *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
   *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
   __syncthreads();
   float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int u = 0; u < kMlaWaves; ++u) {
+  for (int u = 0; u < NW; ++u) {
     const f32x4 lo = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][0]);
     const f32x4 hi = *reinterpret_cast<const f32x4 *>(&xbuf[u * 64 + lane][4]);
 #pragma unroll
@@ -331,7 +350,7 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5
     acc.m = m_new;
     acc.l *= alpha;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc.o[i] *= alpha;
+    for (int i = 0; i < EPL; ++i) acc.o[i] *= alpha;
   }
   float pr[8];
 #pragma unroll
@@ -344,7 +363,7 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc &acc, const u32x4 (&k)[2][5
   const u32x4 pb = {pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
                     pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])};
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
+  for (int b = 0; b < EPL; ++b) {
     u32x4 a;
     if constexpr (C8) {
       const int wd = b >> 2, y = b & 3;
@@ -374,6 +393,9 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
                                          uint32_t *slot_list, int row, int part, int w, int lane) {
   using R = MlaRow<C8>;
   constexpr int S = MlaCfg<C8, SPARSE>::STAGES;
+  constexpr int NW = MlaCfg<C8, SPARSE>::NW;
+  using Geo = MlaGeo<NW>;
+  constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   constexpr int DV = 512;
   const int PT = p.part_tokens;
   const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
@@ -385,21 +407,21 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   if (nparts == 0) {  // no keys: zeros, or nothing when the merge adds sinks
     if (head_live && !partials) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        store_u32x4(p.out + (int64_t(row) * p.heads + c) * DV + 128 * w + 32 * g + 8 * k,
+      for (int k = 0; k < DPW / 32; ++k)
+        store_u32x4(p.out + (int64_t(row) * p.heads + c) * DV + DPW * w + (DPW / 4) * g + 8 * k,
                     u32x4{0, 0, 0, 0});
     }
     return;
   }
 
-  // Q operand: latent dims 128w + 32s + 8g (s < 4), rope dims 32w + 8g (w < 2).
-  u32x4 qv[5];
+  // Q operand: latent dims DPW w + 32s + 8g (s < KS), rope dims 32w + 8g (w < 2).
+  u32x4 qv[KS + 1];
   {
     const uint16_t *qp = p.q + (int64_t(row) * p.heads + (head_live ? c : 0)) * 576;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      qv[s] = head_live ? load_u32x4(qp + 128 * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
-    qv[4] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s)
+      qv[s] = head_live ? load_u32x4(qp + DPW * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+    qv[KS] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
   }
 
   const int tile0 = sp.base + part * PT;
@@ -424,7 +446,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     // Physical rows of this partition's index entries (kNoRow for padding or
     // out-of-table positions).
     const int n = t_end - tile0;
-    for (int i = threadIdx.x; i < n; i += 64 * kMlaWaves) {
+    for (int i = threadIdx.x; i < n; i += 64 * NW) {
       const int pos = p.indices[int64_t(row) * p.topk + tile0 + i];
       uint32_t slot = kNoRow;
       if (pos >= 0 && pos / bs < p.table_stride) {
@@ -443,7 +465,9 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   }
 
   const uint32_t ring_base = lds_addr(ring);
+  // Waves 0..3 move the tiles (NI loads each); further waves only compute.
   auto issue = [&](int ti) {
+    if (NW > kMlaWaves && w >= kMlaWaves) return;
     const int t0 = tile0 + ti * kMlaTile;
     const uint32_t dst = ring_base + uint32_t(ti % S) * R::SLOT + uint32_t(w) * 1024;
     if constexpr (SPARSE) {
@@ -486,9 +510,9 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     }
   };
 
-  MlaAcc acc;
+  MlaAcc<EPL> acc;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
+  for (int i = 0; i < EPL; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
   acc.m = -INFINITY;
   acc.l = 0.0f;
 
@@ -503,45 +527,55 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       const int upper = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
       live = (upper >= 32 ? 0xFFFFFFFFu : ((1u << upper) - 1u)) & ~((1u << lower) - 1u);
     }
-    // K operand: token 16mt + c, latent dims 128w + 32s + 8g (+ rope dims 32(w&1) + 8g).
-    u32x4 k[2][5];
+    // K operand: token 16mt + c, latent dims DPW w + 32s + 8g (+ rope dims 32(w&1) + 8g).
+    u32x4 k[2][KS + 1];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const uint32_t r = uint32_t(16 * mt + c);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
+      for (int s = 0; s < KS; ++s) {
         if constexpr (C8) {
-          const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + 128 * w + 32 * s + 8 * g);
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + DPW * w + 32 * s + 8 * g);
           k[mt][s] = u32x4{x[0], x[1], 0u, 0u};
         } else {
-          k[mt][s] = load_u32x4(tile + R::chunk(r, uint32_t(16 * w + 4 * s + g)));
+          k[mt][s] = load_u32x4(tile + R::chunk(r, uint32_t((DPW / 8) * w + 4 * s + g)));
         }
       }
       if (w < 2) {
         if constexpr (C8)
-          k[mt][4] = load_u32x4(tile + r * R::BYTES + 512 + 64 * (w & 1) + 16 * g);
+          k[mt][KS] = load_u32x4(tile + r * R::BYTES + 512 + 64 * (w & 1) + 16 * g);
         else
-          k[mt][4] = load_u32x4(tile + R::chunk(r, uint32_t(64 + 4 * (w & 1) + g)));
+          k[mt][KS] = load_u32x4(tile + R::chunk(r, uint32_t(64 + 4 * (w & 1) + g)));
       } else {
-        k[mt][4] = u32x4{0, 0, 0, 0};
+        k[mt][KS] = u32x4{0, 0, 0, 0};
       }
     }
-    // V operand rows: token tile_token(g, j), latent dims 128w + 8c .. +8.
+    // V operand rows: token tile_token(g, j), latent dims DPW w + EPL c .. + EPL.
     u32x4 v[8];
     float sk[C8 ? 8 : 1];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t r = uint32_t(mla_tile_token(g, j));
       if constexpr (C8) {
-        const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + 128 * w + 8 * c);
-        v[j] = u32x4{x[0], x[1], 0u, 0u};
-        sk[j] = *reinterpret_cast<const float *>(tile + r * R::BYTES + 640 + 4 * w);
+        if constexpr (EPL == 8) {
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + DPW * w + 8 * c);
+          v[j] = u32x4{x[0], x[1], 0u, 0u};
+        } else {
+          v[j] = u32x4{*reinterpret_cast<const uint32_t *>(tile + r * R::BYTES + DPW * w + 4 * c), 0u, 0u, 0u};
+        }
+        sk[j] = *reinterpret_cast<const float *>(tile + r * R::BYTES + 640 + 4 * ((DPW * w) / 128));
       } else {
-        v[j] = load_u32x4(tile + R::chunk(r, uint32_t(16 * w + c)));
+        if constexpr (EPL == 8) {
+          v[j] = load_u32x4(tile + R::chunk(r, uint32_t(16 * w + c)));
+        } else {
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(
+              tile + R::chunk(r, uint32_t((DPW / 8) * w + (c >> 1))) + 8 * (c & 1));
+          v[j] = u32x4{x[0], x[1], 0u, 0u};
+        }
       }
     }
 
-    mla_tile_math<C8>(acc, k, v, sk, qv, xbuf, live, p.scale_log2, w, lane);
+    mla_tile_math<C8, NW>(acc, k, v, sk, qv, xbuf, live, p.scale_log2, w, lane);
   };
 
   // Ring: tile ti lives in slot ti % S. Tiles 0..S-2 are issued up front; the
@@ -564,18 +598,19 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  // Lane holds rows m = 4g + r of MFMA b -> dim 128w + 8(4g + r) + b.
-  float ov[32];
+  // Lane holds rows m = 4g + r of MFMA b -> dim DPW w + EPL(4g + r) + b: the
+  // 4 EPL consecutive dims from DPW w + 4 EPL g.
+  float ov[4 * EPL];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int b = 0; b < 8; ++b) ov[8 * r + b] = acc.o[b][r];
-  const int d0 = 128 * w + 32 * g;
+    for (int b = 0; b < EPL; ++b) ov[EPL * r + b] = acc.o[b][r];
+  const int d0 = DPW * w + 4 * EPL * g;
   if (!partials) {
     const float inv = 1.0f / l_tot;
     uint16_t *op = p.out + (int64_t(row) * p.heads + c) * DV + d0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < EPL / 2; ++k) {
       const float *v = ov + 8 * k;
       store_u32x4(op + 8 * k, u32x4{pack_bf16x2(v[0] * inv, v[1] * inv),
                                     pack_bf16x2(v[2] * inv, v[3] * inv),
@@ -586,7 +621,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     const int64_t prow = (int64_t(row) * p.parts_per_row + part) * p.heads + c;
     float *po = p.part_o + prow * DV + d0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < EPL; ++k)
       *reinterpret_cast<f32x4 *>(po + 4 * k) = f32x4{ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]};
     if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
   }
@@ -598,21 +633,24 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 // partial of the sinks alone goes to the row's last partial slot. Runs as one
 // item of the attention kernel's queue (after every partition item, so these
 // short items fill the tail).
+template <int NW>
 __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int w,
                                               int lane) {
+  using Geo = MlaGeo<NW>;
+  constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   const int c = lane & 15, g = lane >> 4, n = p.n_sinks;
   const bool head_live = c < p.heads;
-  u32x4 qv[5];
+  u32x4 qv[KS + 1];
   {
     const uint16_t *qp = p.q + (int64_t(row) * p.heads + (head_live ? c : 0)) * 576;
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      qv[s] = head_live ? load_u32x4(qp + 128 * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
-    qv[4] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s)
+      qv[s] = head_live ? load_u32x4(qp + DPW * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+    qv[KS] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
   }
-  MlaAcc acc;
+  MlaAcc<EPL> acc;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
+  for (int i = 0; i < EPL; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
   acc.m = -INFINITY;
   acc.l = 0.0f;
   for (int t0 = 0; t0 < n; t0 += kMlaTile) {
@@ -620,29 +658,36 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
     // Rows past the last sink read as zero (buffer extent).
     const auto rk = make_rsrc(p.sink_k + int64_t(t0) * 576, uint32_t(live_n) * 1152u);
     const auto rv = make_rsrc(p.sink_v + int64_t(t0) * 512, uint32_t(live_n) * 1024u);
-    u32x4 k[2][5], v[8];
+    u32x4 k[2][KS + 1], v[8];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const uint32_t r = uint32_t(16 * mt + c) * 1152u;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) k[mt][s] = buf_load_x4(rk, r + 2 * (128 * w + 32 * s + 8 * g));
-      k[mt][4] = w < 2 ? buf_load_x4(rk, r + 1024 + 2 * (32 * (w & 1) + 8 * g)) : u32x4{0, 0, 0, 0};
+      for (int s = 0; s < KS; ++s) k[mt][s] = buf_load_x4(rk, r + 2 * (DPW * w + 32 * s + 8 * g));
+      k[mt][KS] = w < 2 ? buf_load_x4(rk, r + 1024 + 2 * (32 * (w & 1) + 8 * g)) : u32x4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      v[j] = buf_load_x4(rv, uint32_t(mla_tile_token(g, j)) * 1024u + 2 * (128 * w + 8 * c));
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t off = uint32_t(mla_tile_token(g, j)) * 1024u + 2 * (DPW * w + EPL * c);
+      if constexpr (EPL == 8) {
+        v[j] = buf_load_x4(rv, off);
+      } else {
+        const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0));
+        v[j] = u32x4{x[0], x[1], 0u, 0u};
+      }
+    }
     const uint32_t live = live_n >= 32 ? 0xFFFFFFFFu : ((1u << live_n) - 1u);
-    mla_tile_math<false>(acc, k, v, nullptr, qv, xbuf, live, p.scale_log2, w, lane);
+    mla_tile_math<false, NW>(acc, k, v, nullptr, qv, xbuf, live, p.scale_log2, w, lane);
     __syncthreads();  // xbuf is rewritten by the next tile
   }
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
   const int64_t prow = (int64_t(row) * p.parts_per_row + p.parts_per_row - 1) * p.heads + c;
-  float *po = p.part_o + prow * 512 + 128 * w + 32 * g;
+  float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int r = (4 * k) / 8, b = (4 * k) % 8;  // ov index 4k -> row r, mfma b
+  for (int k = 0; k < EPL; ++k) {
+    const int r = (4 * k) / EPL, b = (4 * k) % EPL;  // dims EPL r + b .. + 3 of the lane's run
     *reinterpret_cast<f32x4 *>(po + 4 * k) =
         f32x4{acc.o[b][r], acc.o[b + 1][r], acc.o[b + 2][r], acc.o[b + 3][r]};
   }
@@ -650,9 +695,10 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
 }
 
 template <bool C8, bool SPARSE>
-__global__ __launch_bounds__(64 * kMlaWaves, (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
+__global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
+  constexpr int NW = MlaCfg<C8, SPARSE>::NW;
   __shared__ __align__(16) uint8_t ring[MlaCfg<C8, SPARSE>::RING];
-  __shared__ __align__(16) float xbuf[kMlaWaves * 64][8];
+  __shared__ __align__(16) float xbuf[NW * 64][8];
   // The sparse slot list lives in the workgroup's LDS only for sparse calls
   // (the dense C8 variant fits two workgroups per CU exactly).
   uint32_t *slot_list = nullptr;
@@ -674,7 +720,7 @@ __global__ __launch_bounds__(64 * kMlaWaves, (MlaCfg<C8, SPARSE>::WGS)) void mla
     if (threadIdx.x == 0) next = atomicAdd(p.queue, 1);
     const uint32_t e = uniform(p.items[it]);
     if (p.n_sinks > 0 && (e & 0xfffu) == kSinkItem)
-      mla_sink_item(p, xbuf, int(e >> 12), w, lane);
+      mla_sink_item<NW>(p, xbuf, int(e >> 12), w, lane);
     else
       mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
     __syncthreads();  // every wave is done with xbuf (and the ring)
@@ -864,11 +910,11 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.static_items = grid;  // the attention grid takes the first items by index
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
-    if (sparse) mla_attention_kernel<true, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
-    else mla_attention_kernel<true, false><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+    if (sparse) mla_attention_kernel<true, true><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
+    else mla_attention_kernel<true, false><<<grid, 64 * MlaCfg<true, false>::NW, 0, s>>>(p);
   } else {
-    if (sparse) mla_attention_kernel<false, true><<<grid, 64 * kMlaWaves, 0, s>>>(p);
-    else mla_attention_kernel<false, false><<<grid, 64 * kMlaWaves, 0, s>>>(p);
+    if (sparse) mla_attention_kernel<false, true><<<grid, 64 * MlaCfg<false, true>::NW, 0, s>>>(p);
+    else mla_attention_kernel<false, false><<<grid, 64 * MlaCfg<false, false>::NW, 0, s>>>(p);
   }
   if (partials) mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
   return launch_status(what);
