@@ -68,11 +68,11 @@ constexpr int prefill_q_tile(int d, int g) { return kPrefillWaves * prefill_nb(d
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
   constexpr int kBuckets = 1025;
   __shared__ int bucket[kBuckets];
-  const int tid = threadIdx.x;
+  __shared__ int s_count[1024], s_kv[1024];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int QT = p.q_tile;
   const int nbk = (p.max_kv + 255) / 256 + 1;  // <= kBuckets (host-checked)
   for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
-  __syncthreads();
   // Bucket of query tile qt: the key tokens it visits, most work first.
   auto cost_bucket = [&](int kv, int qt, int count) {
     const int rows_end = (qt + 1) * QT < count ? (qt + 1) * QT : count;
@@ -80,30 +80,37 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
     reach = reach < 0 ? 0 : (reach > p.max_kv ? p.max_kv : reach);
     return nbk - 1 - reach / 256;
   };
-  for (int seq = tid; seq < p.num_seqs; seq += 1024) {
-    const int count = p.cu[seq + 1] - p.cu[seq];
-    if (count <= 1) continue;
-    int kv = p.kv_lens[seq];
-    kv = kv > p.max_kv ? p.max_kv : kv;
-    for (int qt = 0; qt * QT < count; ++qt) atomicAdd(&bucket[cost_bucket(kv, qt, count)], 1);
-  }
+  // Sequences are staged 1024 at a time (one parallel load each); the query
+  // tiles of a sequence are then spread over the lanes of one wave, so a long
+  // chunk costs one LDS atomic per lane instead of a serial loop in one thread.
+  auto for_each_tile = [&](auto &&fn) {
+    for (int base = 0; base < p.num_seqs; base += 1024) {
+      __syncthreads();  // the previous chunk's staged values are no longer read
+      if (base + tid < p.num_seqs) {
+        const int seq = base + tid;
+        s_count[tid] = p.cu[seq + 1] - p.cu[seq];
+        const int kv = p.kv_lens[seq];
+        s_kv[tid] = kv > p.max_kv ? p.max_kv : kv;
+      }
+      __syncthreads();
+      const int n = p.num_seqs - base < 1024 ? p.num_seqs - base : 1024;
+      for (int i = wave; i < n; i += 16) {
+        const int count = s_count[i];
+        if (count <= 1) continue;
+        for (int qt = lane; qt * QT < count; qt += 64) fn(base + i, qt, cost_bucket(s_kv[i], qt, count));
+      }
+    }
+  };
+  for_each_tile([&](int, int, int b) { atomicAdd(&bucket[b], 1); });
   __syncthreads();
   {
     static_assert(kBuckets <= 64 * 17, "bucket_prefix covers 17 buckets per lane");
     const int run = bucket_prefix<17>(bucket, nbk - 1, 0, tid);
     if (tid == 0) *p.n_items = run;
   }
-  __syncthreads();
-  for (int seq = tid; seq < p.num_seqs; seq += 1024) {
-    const int count = p.cu[seq + 1] - p.cu[seq];
-    if (count <= 1) continue;
-    int kv = p.kv_lens[seq];
-    kv = kv > p.max_kv ? p.max_kv : kv;
-    for (int qt = 0; qt * QT < count; ++qt) {
-      const int slot = atomicAdd(&bucket[cost_bucket(kv, qt, count)], 1);
-      p.items[slot] = (uint32_t(seq) << 12) | uint32_t(qt);
-    }
-  }
+  for_each_tile([&](int seq, int qt, int b) {
+    p.items[atomicAdd(&bucket[b], 1)] = (uint32_t(seq) << 12) | uint32_t(qt);
+  });
 }
 
 __device__ __forceinline__ int pf_tile_token(int g, int j) {
