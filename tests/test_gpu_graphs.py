@@ -6,6 +6,7 @@ metadata bit for bit (the plans are read on the device, no host reads)."""
 import numpy as np
 import pytest
 
+import oracle
 from helpers import to_dev
 from ironpangu_amd import workloads as W
 
@@ -137,3 +138,41 @@ def test_graph_norm_rope_write():
         return ref
 
     _replays(write, update, eager)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_graph_legacy_quantize_position_replay(bits):
+    """if_cache_quantize captured once: each replay reads the device position
+    written before it and fills that row (cache_quantization_probe.cpp:23-34
+    replays with a changed position); rows written by earlier replays stay."""
+    import torch
+    from ironpangu_amd import ops
+    width, rows = 576, 64
+    rng = np.random.default_rng(41)
+    xs = [W.bf16_randn(rng, (width,)) for _ in range(3)]
+    x = torch.empty(width, dtype=torch.bfloat16, device="cuda")
+    packed = torch.zeros((rows * width * bits // 8,), dtype=torch.uint8, device="cuda")
+    scales = torch.ones(rows, dtype=torch.float32, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int64, device="cuda")
+    x.copy_(to_dev(xs[0]))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.cache_quantize(x, packed, scales, pos, bits)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.cache_quantize(x, packed, scales, pos, bits)
+    placed = {}
+    for i, row in enumerate((5, 17, 63)):
+        x.copy_(to_dev(xs[i]))
+        pos.fill_(row)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        placed[row] = oracle.quant_legacy(xs[i], bits)
+        p = packed.cpu().numpy().reshape(rows, -1)
+        sc = scales.cpu().numpy()
+        for r, (ref_packed, ref_scale) in placed.items():
+            assert np.array_equal(p[r], ref_packed), f"replay {i}: row {r}"
+            assert sc[r] == np.float32(ref_scale)
