@@ -224,6 +224,88 @@ def bench_c8(seed, steps, warmup):
     return res
 
 
+def bench_decode_hd256(seed, steps, warmup):
+    """GQA decode at the reference Qwen path's head shape (8 q / 2 kv heads,
+    head_dim 256; native/src/inferfabric_acl.cpp:1343-1430) over config 2's
+    ragged lengths: 256 seqs, log-uniform [128, 32768], block 128."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    rng_lens = W.decode_meta(seed, **W.CONFIGS["decode"]).seq_lens
+    need = int(((rng_lens.astype(np.int64) + 127) // 128).sum())
+    case = W.decode_meta(seed, num_seqs=256, lo=128, hi=32768, dist="loguniform", q_heads=8,
+                         kv_heads=2, head_dim=256, block_size=128, pool_blocks=need + 64)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 7)
+    shape = (case.pool_blocks, 128, 2, 256)
+    kc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    fill_randn(kc, g)
+    fill_randn(vc, g)
+    q = torch.randn((256, 8, 256), generator=g, device=dev).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    ws = ops.decode_workspace(256, 8, 256, case.max_context)
+    out = torch.empty_like(q)
+
+    def attn():
+        ops.paged_decode(q, kc, vc, tables, lens, case.max_context, 1.0 / 16.0, out=out, workspace=ws)
+
+    ms = timed(attn, steps, warmup)
+    b = W.decode_bytes(case.seq_lens, 8, 2, 256, 128)
+    res = {"workload": "GQA paged decode, Qwen head shape 8q/2kv/256, 256 seqs, L log-uniform [128,32768]",
+           "value": round(b["attention"] / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
+           "roofline": {"bound": "hbm", "kernel": "paged_decode bf16 operator (head_dim 256)",
+                        "achieved": round(b["attention"] / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(b["attention"] / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": b["attention"]}}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_mla_c8(seed, steps, warmup):
+    """Config 5's rows and lengths over packed C8 latent rows (656 B per key)."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    case = W.mla_meta(seed)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 6)
+    n = case.pool_blocks * case.block_size
+    cache = torch.empty((case.pool_blocks, case.block_size, 656), dtype=torch.uint8, device=dev)
+    src = torch.empty((1 << 16, 576), dtype=torch.bfloat16, device=dev)
+    for r0 in range(0, n, 1 << 16):
+        fill_randn(src, g, std=0.5)
+        m = min(1 << 16, n - r0)
+        ops.mla_cache_write_c8(src[:m], cache, torch.arange(r0, r0 + m, dtype=torch.int64, device=dev))
+    del src
+    q = (torch.randn((case.num_seqs, case.heads, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    ws = ops.mla_workspace(case.num_seqs, case.heads, case.max_context, case.block_size)
+    out = torch.empty((case.num_seqs, case.heads, 512), dtype=torch.bfloat16, device=dev)
+
+    def attn():
+        ops.mla_decode(q, cache, tables, lens, case.max_context, case.scale, out=out, workspace=ws)
+
+    ms = timed(attn, steps, warmup)
+    L = case.seq_lens.astype(np.int64)
+    nbytes = int(L.sum()) * 656 + case.num_seqs * case.heads * (576 + 512) * 2 + \
+        int(((L + 63) // 64).sum()) * 4 + case.num_seqs * 4
+    res = {"workload": "packed-MLA latent decode over C8 rows, config-5 rows and lengths",
+           "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
+           "roofline": {"bound": "hbm", "kernel": "mla_decode c8 operator",
+                        "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes}}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_mla(seed, steps, warmup):
     """Config 5: packed-MLA latent decode, 128 seqs, L log-uniform [1024,65536],
     16 heads, 576-wide bf16 rows, block 64, N(0,0.5)."""
@@ -585,6 +667,8 @@ def main():
         torch.cuda.empty_cache()
         res["secondary"] = {"c8_decode": bench_c8(args.seed, args.steps, args.warmup),
                             "mla_decode": bench_mla(args.seed, args.steps, args.warmup),
+                            "mla_decode_c8": bench_mla_c8(args.seed, args.steps, args.warmup),
+                            "gqa_decode_hd256": bench_decode_hd256(args.seed, args.steps, args.warmup),
                             "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup),
                             "mla_window_attention": bench_mla_rows(args.seed, args.steps, args.warmup, False),
                             "mla_sparse_attention": bench_mla_rows(args.seed, args.steps, args.warmup, True),
