@@ -235,9 +235,9 @@ struct MlaCfg {
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
   static constexpr int NW = kMlaWaves;
-  static constexpr int STAGES = !C8 ? 4 : (SPARSE ? 2 : 3);
+  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : 4);
   static constexpr int RING = MlaRow<C8>::SLOT * STAGES;
-  static constexpr int LDS = RING + NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
+  static constexpr int LDS = RING + 2 * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
 inline int wgs_mla(bool c8) { return c8 ? 2 : 1; }
@@ -279,15 +279,14 @@ struct MlaAcc {
   float m, l;
 };
 
+// QK^T partial scores of the wave's dims for one 32-key tile, written to xbuf
+// (row w * 64 + lane); the caller publishes them with a workgroup barrier.
 template <bool C8, int NW>
-__device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
-                                              const u32x4 (&k)[2][MlaGeo<NW>::KS + 1],
-                                              const u32x4 (&v)[8], const float *sk,
-                                              const u32x4 (&qv)[MlaGeo<NW>::KS + 1],
-                                              float (*xbuf)[8], uint32_t live, float scale_log2,
-                                              int w, int lane) {
-  constexpr int KS = MlaGeo<NW>::KS, EPL = MlaGeo<NW>::EPL;
-  const int g = lane >> 4;
+__device__ __forceinline__ void mla_tile_scores(const u32x4 (&k)[2][MlaGeo<NW>::KS + 1],
+                                                const float *sk,
+                                                const u32x4 (&qv)[MlaGeo<NW>::KS + 1],
+                                                float (*xbuf)[8], int w, int lane) {
+  constexpr int KS = MlaGeo<NW>::KS;
   f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -318,11 +317,19 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
       part_s[4 + r] += r1[r];
     }
   }
-  // Sum the waves' partial scores. The buffer is free again: every wave
-  // finished reading it before the barrier that starts this tile.
   *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][0]) = f32x4{part_s[0], part_s[1], part_s[2], part_s[3]};
   *reinterpret_cast<f32x4 *>(&xbuf[w * 64 + lane][4]) = f32x4{part_s[4], part_s[5], part_s[6], part_s[7]};
-  __syncthreads();
+}
+
+// Sum of the waves' partial scores (published in xbuf), online softmax and PV
+// of one 32-key tile.
+template <bool C8, int NW>
+__device__ __forceinline__ void mla_tile_softmax_pv(MlaAcc<MlaGeo<NW>::EPL> &acc,
+                                                    const u32x4 (&v)[8], const float *sk,
+                                                    const float (*xbuf)[8], uint32_t live,
+                                                    float scale_log2, int lane) {
+  constexpr int EPL = MlaGeo<NW>::EPL;
+  const int g = lane >> 4;
   float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < NW; ++u) {
@@ -382,6 +389,19 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
     }
     acc.o[b] = mfma16x16x32(a, pb, acc.o[b]);
   }
+}
+
+// Both halves with the barrier between them (sink items, one buffer).
+template <bool C8, int NW>
+__device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
+                                              const u32x4 (&k)[2][MlaGeo<NW>::KS + 1],
+                                              const u32x4 (&v)[8], const float *sk,
+                                              const u32x4 (&qv)[MlaGeo<NW>::KS + 1],
+                                              float (*xbuf)[8], uint32_t live, float scale_log2,
+                                              int w, int lane) {
+  mla_tile_scores<C8, NW>(k, sk, qv, xbuf, w, lane);
+  __syncthreads();
+  mla_tile_softmax_pv<C8, NW>(acc, v, sk, xbuf, live, scale_log2, lane);
 }
 
 // One (row, partition) item. Tiles of the partition go HBM -> LDS once by
@@ -516,9 +536,11 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   acc.m = -INFINITY;
   acc.l = 0.0f;
 
-  auto compute = [&](const uint8_t *tile, int t0) {
+  // Stage 1 of a tile: operands from LDS (V kept in registers for stage 2)
+  // and the wave's partial scores into xb.
+  auto score = [&](const uint8_t *tile, int t0, u32x4 (&v)[8], float (&sk)[C8 ? 8 : 1],
+                   uint32_t &live, float (*xb)[8]) {
     // Live rows of this tile (wave-uniform mask).
-    uint32_t live;
     if constexpr (SPARSE) {
       const bool ok = lane < 32 && t0 + lane < t_end && slot_list[t0 - tile0 + lane] != kNoRow;
       live = uint32_t(__ballot(ok));
@@ -551,8 +573,6 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
     }
     // V operand rows: token tile_token(g, j), latent dims DPW w + EPL c .. + EPL.
-    u32x4 v[8];
-    float sk[C8 ? 8 : 1];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t r = uint32_t(mla_tile_token(g, j));
@@ -575,24 +595,37 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
     }
 
-    mla_tile_math<C8, NW>(acc, k, v, sk, qv, xbuf, live, p.scale_log2, w, lane);
+    mla_tile_scores<C8, NW>(k, sk, qv, xb, w, lane);
   };
 
-  // Ring: tile ti lives in slot ti % S. Tiles 0..S-2 are issued up front; the
-  // top of iteration ti waits for tile ti (S-2 newer tiles may stay in flight,
-  // fewer near the end), then a barrier both publishes it and retires every
-  // wave's reads of tile ti-1, whose slot receives tile ti+S-1.
+  // Ring: tile ti lives in slot ti % S; tiles 0..S-1 are issued up front. In
+  // iteration ti every wave reads tile ti's operands (V stays in registers)
+  // and writes its partial scores to xbuf half ti & 1; one barrier then
+  // publishes those scores and tile ti+1 and retires the reads of tile ti,
+  // whose slot receives tile ti+S before the softmax and PV of tile ti run.
+  // One barrier per tile: the other half of xbuf is still being read by
+  // slower waves while faster ones write the next tile's scores.
 #pragma unroll
-  for (int i = 0; i < S - 1; ++i)
+  for (int i = 0; i < S; ++i)
     if (i < n_tiles) issue(i);
+  if (S - 1 < n_tiles)  // tile 0; tiles 1 .. S-1 may stay in flight
+    lds_dma_wait<(S - 1) * R::NI>();
+  else
+    lds_dma_wait<0>();
+  __syncthreads();
   for (int ti = 0; ti < n_tiles; ++ti) {
-    if (ti + S - 2 < n_tiles)
+    float (*xb)[8] = xbuf + (ti & 1) * NW * 64;
+    u32x4 v[8];
+    float sk[C8 ? 8 : 1];
+    uint32_t live;
+    score(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile, v, sk, live, xb);
+    if (ti + S - 1 < n_tiles)  // tile ti+1; tiles ti+2 .. ti+S-1 may stay in flight
       lds_dma_wait<(S - 2) * R::NI>();
     else
       lds_dma_wait<0>();
     __syncthreads();
-    if (ti + S - 1 < n_tiles) issue(ti + S - 1);
-    compute(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile);
+    if (ti + S < n_tiles) issue(ti + S);
+    mla_tile_softmax_pv<C8, NW>(acc, v, sk, xb, live, p.scale_log2, lane);
   }
 
   float l_tot = sum_xor16(acc.l);
@@ -698,7 +731,7 @@ template <bool C8, bool SPARSE>
 __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
   constexpr int NW = MlaCfg<C8, SPARSE>::NW;
   __shared__ __align__(16) uint8_t ring[MlaCfg<C8, SPARSE>::RING];
-  __shared__ __align__(16) float xbuf[NW * 64][8];
+  __shared__ __align__(16) float xbuf[2 * NW * 64][8];  // score exchange, two halves
   // The sparse slot list lives in the workgroup's LDS only for sparse calls
   // (the dense C8 variant fits two workgroups per CU exactly).
   uint32_t *slot_list = nullptr;
