@@ -80,6 +80,15 @@ def test_decode_many_partitions():
     assert_close(bf16_host(out), exp)
 
 
+def test_decode_many_sequences():
+    # a large ragged batch of short sequences (more items than workgroups, and
+    # sequence ids beyond 4096 in the work-item encoding)
+    case = W.decode_host_case(17, num_seqs=5000, lo=1, hi=300, dist="uniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=32, pool_blocks=5000 * 10 + 8)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
 def test_decode_partition_edges_and_long():
     # lengths around the 2048-token split-K partition and 32-token tile edges
     lens = [31, 32, 33, 255, 256, 257, 511, 512, 513, 4095, 8193]
