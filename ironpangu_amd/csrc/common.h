@@ -103,6 +103,57 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// 16x16x32 fp16 MFMA, same operand layout as the bf16 one.
+__device__ __forceinline__ f32x4 mfma16x16x32_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+// Additive offset of i8x4_to_f16_biased: code c reads as c + kI8Bias.
+constexpr float kI8Bias = 1152.0f;
+// Four int8 codes (one dword, code i in byte i) -> four fp16 values code + 1152,
+// exactly, as two packed pairs: with its sign bit flipped a code c is the
+// unsigned byte c + 128, and as the low mantissa byte of 0x6400 (fp16 1024.0,
+// whose ulp is 1) it reads 1024 + c + 128. Three VALU ops per four codes,
+// against a convert per code for the bf16 route.
+__device__ __forceinline__ u32x2 i8x4_to_f16_biased(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  return u32x2{perm_b32(0x64646464u, u, 0x05010400u), perm_b32(0x64646464u, u, 0x05030402u)};
+}
+__device__ __forceinline__ u32x4 i8x8_to_f16_biased(uint32_t lo, uint32_t hi) {
+  const u32x2 a = i8x4_to_f16_biased(lo), b = i8x4_to_f16_biased(hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+// Eight bf16 values -> fp16 times qs (a power of two), summed into *sum as the
+// fp16 values read back (so a biased product sum can drop kI8Bias * sum).
+__device__ __forceinline__ u32x4 bf16x8_to_f16(u32x4 v, float qs, float *sum) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 h = {_Float16(bf16_bits_to_f32(v[i] & 0xFFFFu) * qs),
+                     _Float16(bf16_bits_to_f32(v[i] >> 16) * qs)};
+    *sum += float(h[0]) + float(h[1]);
+    r[i] = __builtin_bit_cast(uint32_t, h);
+  }
+  return r;
+}
+// Largest |bf16| of eight packed values.
+__device__ __forceinline__ float bf16x8_absmax(u32x4 v) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(v[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(v[i] >> 16))));
+  return m;
+}
+// Power of two 2^-e (e >= 0) that brings amax below 2^15, inside fp16's range
+// with room for the biased product sums.
+__device__ __forceinline__ float f16_range_scale(float amax) {
+  int e = int((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 14;
+  e = e > 0 ? e : 0;
+  return __uint_as_float(uint32_t(127 - e) << 23);
+}
+
 // 16x16x16 bf16 MFMA: lane l holds row (l & 15) of A and column (l & 15) of B,
 // k = 4(l >> 4) .. 4(l >> 4) + 3, as two packed bf16 pairs each.
 __device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {

@@ -30,7 +30,9 @@
 // the same online softmax. With C8 the wave's 128 dims are exactly one scale
 // tile, so the per-token tile scale multiplies the wave's partial score and is
 // folded into its probabilities for PV. MFMA 16x16x32 bf16 with the heads in
-// the N dimension. Rows split over several partitions, and rows with sinks,
+// the N dimension; C8 latent scores use the fp16 MFMA on the codes biased by
+// 1152 (three VALU ops per four codes instead of a convert per code), with q
+// in fp16 and the bias term removed per head. Rows split over several partitions, and rows with sinks,
 // write (m, l, O) partials; a merge kernel adds the sink rows and combines.
 #include "common.h"
 #include "ifattn_internal.h"
@@ -262,10 +264,6 @@ __device__ __forceinline__ uint32_t mla_i8pair(int a, int b) {
   return perm_b32(__float_as_uint(float(b)), __float_as_uint(float(a)), 0x07060302u);
 }
 __device__ __forceinline__ int mla_i8(uint32_t x, int b) { return (int32_t(x) << (24 - 8 * b)) >> 24; }
-__device__ __forceinline__ u32x4 mla_i8x8(uint32_t lo, uint32_t hi) {
-  return u32x4{mla_i8pair(mla_i8(lo, 0), mla_i8(lo, 1)), mla_i8pair(mla_i8(lo, 2), mla_i8(lo, 3)),
-               mla_i8pair(mla_i8(hi, 0), mla_i8(hi, 1)), mla_i8pair(mla_i8(hi, 2), mla_i8(hi, 3))};
-}
 
 // Scores, online softmax and PV of one 32-key tile, from the operands already
 // in registers: k = keys 16mt + c of the wave's dims (+ rope), v = keys
@@ -285,14 +283,15 @@ template <bool C8, int NW>
 __device__ __forceinline__ void mla_tile_scores(const u32x4 (&k)[2][MlaGeo<NW>::KS + 1],
                                                 const float *sk,
                                                 const u32x4 (&qv)[MlaGeo<NW>::KS + 1],
-                                                float (*xbuf)[8], int w, int lane) {
+                                                float (*xbuf)[8], int w, int lane,
+                                                float k_corr = 0.0f, float q_unscale = 1.0f) {
   constexpr int KS = MlaGeo<NW>::KS;
   f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     if constexpr (C8) {
-      a0 = mfma16x16x32(mla_i8x8(k[0][s][0], k[0][s][1]), qv[s], a0);
-      a1 = mfma16x16x32(mla_i8x8(k[1][s][0], k[1][s][1]), qv[s], a1);
+      a0 = mfma16x16x32_f16(i8x8_to_f16_biased(k[0][s][0], k[0][s][1]), qv[s], a0);
+      a1 = mfma16x16x32_f16(i8x8_to_f16_biased(k[1][s][0], k[1][s][1]), qv[s], a1);
     } else {
       a0 = mfma16x16x32(k[0][s], qv[s], a0);
       a1 = mfma16x16x32(k[1][s], qv[s], a1);
@@ -306,7 +305,7 @@ __device__ __forceinline__ void mla_tile_scores(const u32x4 (&k)[2][MlaGeo<NW>::
   }
   if constexpr (C8) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) part_s[j] *= sk[j];
+    for (int j = 0; j < 8; ++j) part_s[j] = (part_s[j] - k_corr) * (sk[j] * q_unscale);
   }
   if (w < 2) {
     f32x4 r0 = mfma16x16x32(k[0][KS], qv[KS], f32x4{0, 0, 0, 0});
@@ -443,6 +442,22 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       qv[s] = head_live ? load_u32x4(qp + DPW * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
     qv[KS] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
   }
+  // C8: the latent QK^T runs in fp16 on the biased codes (code + kI8Bias,
+  // exact); the wave's q slice is scaled per head by a power of two into fp16
+  // range, and kI8Bias * sum(q slice) leaves each partial score.
+  float k_corr = 0.0f, q_unscale = 1.0f;
+  if constexpr (C8) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) amax = fmaxf(amax, bf16x8_absmax(qv[s]));
+    amax = max_xor32(max_xor16(amax));
+    const float qs = f16_range_scale(amax);
+    float qsum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qv[s] = bf16x8_to_f16(qv[s], qs, &qsum);
+    k_corr = kI8Bias * sum_xor32(sum_xor16(qsum));
+    q_unscale = 1.0f / qs;
+  }
 
   const int tile0 = sp.base + part * PT;
   const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
@@ -485,6 +500,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   }
 
   const uint32_t ring_base = lds_addr(ring);
+  const int bs_log2 = __builtin_ctz(uint32_t(bs));  // block_size: host-checked power of two
   // Waves 0..3 move the tiles (NI loads each); further waves only compute.
   auto issue = [&](int ti) {
     if (NW > kMlaWaves && w >= kMlaWaves) return;
@@ -515,7 +531,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
         if (hb < halves) {
           const int r0 = hb * (kMlaTile / halves), r1 = r0 + kMlaTile / halves;
           const int a = lower > r0 ? lower : r0, b = upper < r1 ? upper : r1;
-          const int blk = __builtin_amdgcn_readlane(lane_blocks, t0 / bs - tile0 / bs + hb);
+          const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 >> bs_log2) - (tile0 >> bs_log2) + hb);
           const int64_t tok = int64_t(blk) * bs + (t0 & (bs - 1)) + (a - r0);
           rc[hb] = raw_rsrc(p.cache + tok * R::BYTES, b > a ? uint32_t(b - a) * R::BYTES : 0u);
           first_row[hb] = uint32_t(a);
@@ -595,7 +611,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
     }
 
-    mla_tile_scores<C8, NW>(k, sk, qv, xb, w, lane);
+    mla_tile_scores<C8, NW>(k, sk, qv, xb, w, lane, k_corr, q_unscale);
   };
 
   // Ring: tile ti lives in slot ti % S; tiles 0..S-1 are issued up front. In

@@ -85,3 +85,31 @@ def test_varlen_prefill_edges():
                              head_dim=128, block_size=128)
     out, exp = _prefill(case)
     assert_close(bf16_host(out), exp)
+
+
+def test_mla_decode_c8_q_range():
+    """C8 latent scores run in fp16 with q rescaled per head by a power of two:
+    heads with |q| far beyond fp16's range (2^17 times the usual values, softmax
+    scale shrunk to match) and heads with |q| near 2^-21 must match the oracle."""
+    import torch
+    from ironpangu_amd import ops
+    heads = 16
+    case = W.mla_host_case(4, num_seqs=4, lo=1, hi=3000, dist="loguniform", heads=heads,
+                           block_size=64, fixed={0: 2500, 1: 33})
+    h = case.host
+    nb, bs = case.pool_blocks, case.block_size
+    pool = h["pool"].copy()
+    oracle.kv_write(h["row_new"], pool, case.slot_mapping)
+    qf = (h["q"].astype(np.uint32) << 16).view(np.float32).copy()
+    qf[:, : heads // 2] *= np.float32(2.0 ** 17)
+    qf[:, heads // 2:] *= np.float32(2.0 ** -20)
+    q = (qf.view(np.uint32) >> 16).astype(np.uint16)  # power-of-two scaling: still exact bf16
+    scale = case.scale * 2.0 ** -17
+    cache = torch.zeros((nb, bs, 656), dtype=torch.uint8, device="cuda")
+    ops.mla_cache_write_c8(to_dev(pool), cache, torch.arange(nb * bs, dtype=torch.int64, device="cuda"))
+    out = ops.mla_decode(to_dev(q), cache, to_dev(case.block_tables), to_dev(case.seq_lens),
+                         case.max_context, scale)
+    torch.cuda.synchronize()
+    exp = oracle.mla_decode(q, oracle.mla_pack_c8(pool), case.block_tables, case.seq_lens, heads,
+                            bs, scale, c8=True)
+    assert_close(bf16_host(out), exp)
