@@ -59,13 +59,15 @@ struct MlaParams {
   int32_t *queue;               // [0] next item (atomic), [1] item count
   uint32_t *items;              // (row << 12 | partition)
   int32_t *row_seq;             // [rows] sequence of each row (plan output)
-  float *part_o;                // [rows, parts_per_row, heads, 512]
-  float *part_ml;               // [rows, parts_per_row, heads, 2]
+  int32_t *row_pt;              // [rows] partition size of each row (plan output)
+  int32_t *row_slot;            // [rows] first partial slot of each row (plan output)
+  float *part_o;                // [slots, heads, 512]
+  float *part_ml;               // [slots, heads, 2]
   int64_t num_blocks;
   uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
   int static_items;      // items 0..static_items-1 go to workgroups by index; the queue starts after
   int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks,
-      part_tokens, parts_per_row;
+      part_tokens, items_per_wg;
   float scale_log2;
 };
 
@@ -118,83 +120,132 @@ __device__ __forceinline__ int mla_part_size(const MlaSpan &s, int pt, int k) {
   return (s.hi < b ? s.hi : b) - (s.lo > a ? s.lo : a);
 }
 
-// Work list on the device (graph-safe: lengths are read at run time), in
-// longest-processing-time order: full partitions first (row order), then the
-// partial ones by decreasing size (32-token buckets), rows without keys last.
-// Also records each row's sequence. One workgroup of 1024 threads.
+// Smallest partition the plan picks (a row shorter than this is one item).
+constexpr int kMinPart = 256;
+
+// Work list on the device (graph-safe: lengths are read at run time). The
+// partition size adapts to the call: with T keys over all rows and W
+// persistent workgroups it is S = T / (items_per_wg * W) keys (32-multiple,
+// clamped to [kMinPart, part_tokens]); rows are cut into partitions of S keys
+// from their tile-aligned start, the last one shorter. Items go out in
+// longest-processing-time order (counting sort over 32-key buckets): the full
+// partitions, then the shorter last ones, which fill the tail; rows without
+// keys last, sink items after every partition item. (Cutting each row into
+// equal parts instead measured slower: no short pieces are left for the
+// tail.) Also records each row's sequence, partition size and first partial
+// slot (the sink partial first, when there are sinks, then the partitions;
+// rows are packed by a scan, so at most items_per_wg * W + rows * (partitions
+// at part_tokens + 1) slots are used). One workgroup of 1024 threads.
 __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
   constexpr int kBuckets = 257;
   __shared__ int bucket[kBuckets];
-  __shared__ int carry, sink_base;
-  __shared__ int wave_tot[16];
+  __shared__ int carry_full, carry_slot, sink_base, part_sh;
+  __shared__ unsigned long long total_keys;
+  __shared__ int wave_full[16], wave_slot[16];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int PT = p.part_tokens;
-  const int nb = PT / 32;  // bucket b: sizes in (PT - 32(b+1), PT - 32b]; nb: no keys
+  const int SMAX = p.part_tokens;
+  const int nb = SMAX / 32;  // bucket b: sizes in (SMAX - 32(b+1), SMAX - 32b]; nb: no keys
+  const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
-  if (tid == 0) carry = 0;
+  if (tid == 0) {
+    carry_full = carry_slot = 0;
+    total_keys = 0ull;
+  }
   __syncthreads();
-  // The span of each thread's first row stays in registers for the later
-  // passes (calls with more than 1024 rows recompute the others).
+  // Pass 1: sequence of each row and the call's key count. The span of each
+  // thread's first row stays in registers for the later passes (calls with
+  // more than 1024 rows recompute the others).
   MlaSpan first{0, 0, 0, 0};
+  unsigned long long keys = 0ull;
+  for (int row = tid; row < p.num_rows; row += 1024) {
+    const int seq = mla_seq_of(p, row);
+    p.row_seq[row] = seq;
+    const MlaSpan s = mla_span(p, row, seq);
+    if (row == tid) first = s;
+    if (s.hi > s.lo) keys += uint64_t(s.hi - s.base);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) keys += __shfl_xor(keys, off, 64);
+  if (lane == 0) atomicAdd(&total_keys, keys);
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned long long per = uint64_t(p.items_per_wg) * uint64_t(p.static_items);
+    unsigned long long t = (total_keys + per - 1) / per;
+    t = (t + 31) & ~31ull;
+    part_sh = t < uint64_t(kMinPart) ? kMinPart : (t > uint64_t(SMAX) ? SMAX : int(t));
+  }
+  __syncthreads();
+  const int S = part_sh;
+  // Pass 2: full partitions go first in row order (positions by a scan),
+  // shorter ones are counted into their buckets; partial slots by a scan.
   for (int base = 0; base < p.num_rows; base += 1024) {
     const int row = base + tid;
-    int nfull = 0;
+    int nfull = 0, slots = 0, np = 0;
+    MlaSpan s{0, 0, 0, 0};
     if (row < p.num_rows) {
-      const int seq = mla_seq_of(p, row);
-      p.row_seq[row] = seq;
-      const MlaSpan s = mla_span(p, row, seq);
-      if (base == 0) first = s;
-      const int np = mla_parts(s, PT);
+      s = base == 0 ? first : mla_span(p, row, p.row_seq[row]);
+      p.row_pt[row] = S;
+      np = mla_parts(s, S);
       if (np == 0) atomicAdd(&bucket[nb], 1);
       for (int k = 0; k < np; ++k) {
-        const int sz = mla_part_size(s, PT, k);
-        if (sz == PT) ++nfull;
-        else atomicAdd(&bucket[(PT - sz) / 32], 1);
+        const int sz = mla_part_size(s, S, k);
+        if (sz == S) ++nfull;
+        else atomicAdd(&bucket[(SMAX - sz) / 32], 1);
       }
+      slots = np + sinks;
     }
-    int x = nfull;  // inclusive scan: shuffles within the wave, then across waves
+    int xf = nfull, xs = slots;  // inclusive scans: shuffles within the wave, then across waves
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(x, off, 64);
-      x += lane >= off ? y : 0;
+      const int yf = __shfl_up(xf, off, 64), ys = __shfl_up(xs, off, 64);
+      xf += lane >= off ? yf : 0;
+      xs += lane >= off ? ys : 0;
     }
-    if (lane == 63) wave_tot[wv] = x;
-    __syncthreads();
-    int at = carry;
-    for (int w2 = 0; w2 < wv; ++w2) at += wave_tot[w2];
-    at += x - nfull;
-    if (nfull > 0) {
-      const MlaSpan s = base == 0 ? first : mla_span(p, row, mla_seq_of(p, row));
-      const int np = mla_parts(s, PT);
-      for (int k = 0; k < np; ++k)
-        if (mla_part_size(s, PT, k) == PT) p.items[at++] = (uint32_t(row) << 12) | uint32_t(k);
+    if (lane == 63) {
+      wave_full[wv] = xf;
+      wave_slot[wv] = xs;
     }
     __syncthreads();
-    if (tid == 1023) carry = at;
+    int at = carry_full, slot = carry_slot;
+    for (int w2 = 0; w2 < wv; ++w2) {
+      at += wave_full[w2];
+      slot += wave_slot[w2];
+    }
+    at += xf - nfull;
+    slot += xs - slots;
+    if (row < p.num_rows) {
+      p.row_slot[row] = slot;
+      for (int k = 0; k < np && nfull > 0; ++k)
+        if (mla_part_size(s, S, k) == S) p.items[at++] = (uint32_t(row) << 12) | uint32_t(k);
+    }
+    __syncthreads();
+    if (tid == 1023) {
+      carry_full = at;
+      carry_slot = slot + slots;
+    }
     __syncthreads();
   }
   {
-    const int run = bucket_prefix(bucket, nb, carry, tid);
+    const int run = bucket_prefix(bucket, nb, carry_full, tid);
     if (tid == 0) {
       p.queue[0] = p.static_items;
-      p.queue[1] = run + (p.n_sinks > 0 ? p.num_rows : 0);
+      p.queue[1] = run + (sinks ? p.num_rows : 0);
       sink_base = run;
     }
   }
   __syncthreads();
   // One sink item per row after every partition item.
-  if (p.n_sinks > 0)
+  if (sinks)
     for (int row = tid; row < p.num_rows; row += 1024)
       p.items[sink_base + row] = (uint32_t(row) << 12) | kSinkItem;
-  for (int base = 0; base < p.num_rows; base += 1024) {
-    const int row = base + tid;
-    if (row >= p.num_rows) continue;
-    const MlaSpan s = base == 0 ? first : mla_span(p, row, mla_seq_of(p, row));
-    const int np = mla_parts(s, PT);
+  // Pass 3: place the shorter partitions and the rows without keys.
+  for (int row = tid; row < p.num_rows; row += 1024) {
+    const MlaSpan s = row == tid ? first : mla_span(p, row, p.row_seq[row]);
+    const int np = mla_parts(s, S);
     if (np == 0) p.items[atomicAdd(&bucket[nb], 1)] = uint32_t(row) << 12;
     for (int k = 0; k < np; ++k) {
-      const int sz = mla_part_size(s, PT, k);
-      if (sz != PT) p.items[atomicAdd(&bucket[(PT - sz) / 32], 1)] = (uint32_t(row) << 12) | uint32_t(k);
+      const int sz = mla_part_size(s, S, k);
+      if (sz != S) p.items[atomicAdd(&bucket[(SMAX - sz) / 32], 1)] = (uint32_t(row) << 12) | uint32_t(k);
     }
   }
 }
@@ -416,7 +467,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   using Geo = MlaGeo<NW>;
   constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   constexpr int DV = 512;
-  const int PT = p.part_tokens;
+  const int PT = p.row_pt[row];
   const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
   const int nparts = mla_parts(sp, PT);
   const int c = lane & 15, g = lane >> 4;
@@ -667,7 +718,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
                                     pack_bf16x2(v[6] * inv, v[7] * inv)});
     }
   } else {
-    const int64_t prow = (int64_t(row) * p.parts_per_row + part) * p.heads + c;
+    const int64_t prow = (int64_t(p.row_slot[row]) + (p.n_sinks > 0 ? 1 : 0) + part) * p.heads + c;
     float *po = p.part_o + prow * DV + d0;
 #pragma unroll
     for (int k = 0; k < EPL; ++k)
@@ -679,7 +730,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 // Learned sink rows of one query row (keys [n, 576], values [n, 512] bf16,
 // shared by every row, so they are read from L2): the same tile math as the
 // cache keys, four waves per row, heads in the MFMA N dimension. The (m, l, O)
-// partial of the sinks alone goes to the row's last partial slot. Runs as one
+// partial of the sinks alone goes to the row's first partial slot. Runs as one
 // item of the attention kernel's queue (after every partition item, so these
 // short items fill the tail).
 template <int NW>
@@ -732,7 +783,7 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  const int64_t prow = (int64_t(row) * p.parts_per_row + p.parts_per_row - 1) * p.heads + c;
+  const int64_t prow = int64_t(p.row_slot[row]) * p.heads + c;  // the row's first slot
   float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
   for (int k = 0; k < EPL; ++k) {
@@ -780,15 +831,16 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>:
 }
 
 // Combine one (row, head): the row's partition partials and, with sinks, the
-// sink partial in the row's last slot. Each thread owns 2 output dims.
+// sink partial in the row's first slot. Each thread owns 2 output dims.
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
-  const int np = mla_parts(sp, p.part_tokens);
+  const int np = mla_parts(sp, p.row_pt[row]);
   if (p.n_sinks == 0 && np <= 1) return;
-  const int64_t prow0 = int64_t(row) * p.parts_per_row * p.heads + h;
-  auto part_at = [&](int k) {  // k == np: the sink slot
-    return prow0 + int64_t(k < np ? k : p.parts_per_row - 1) * p.heads;
+  const int sinks = p.n_sinks > 0 ? 1 : 0;
+  const int64_t prow0 = int64_t(p.row_slot[row]) * p.heads + h;
+  auto part_at = [&](int k) {  // k == np: the sink slot (the row's first)
+    return prow0 + int64_t(k < np ? sinks + k : 0) * p.heads;
   };
   const int total = np + (p.n_sinks > 0 ? 1 : 0);
   // Largest partial max: threads stride over the partials, then a
@@ -844,45 +896,57 @@ struct MlaCall {
   void *stream;
 };
 
-// Default dense partition: 3072 keys measured best on 128 decode rows of
-// log-uniform [1024, 65536] keys (520 us; 2048: 529, 2560: 525, 4064: 569),
-// where the longest-first list then ends in pieces that fill the tail.
+// Largest dense partition (the plan picks smaller ones when a call has
+// fewer keys than items_per_wg items per workgroup of that size).
 constexpr int kMlaDensePart = 3072;
-
-// Partition size of a call: the default (sparse lists: kSparsePart entries),
-// shrunk for small calls so that the largest possible key count still makes
-// about one item per workgroup of the `wgs`-per-CU grid (the rows' key counts
-// are only known on the device; two items per workgroup measured 5-13% slower
-// on 128-row window and sparse calls, whose rows are all full), and never
-// below 256 keys. A dense partition starting on a 32-token tile spans
-// 1 + ceil((PT - 32) / bs) blocks, at most the 64 one wave holds:
-// PT <= 63 * bs + 32. Workspace sizes assume the smaller partitions of the
-// two-workgroup grid, which covers either cache type.
-inline int mla_part_tokens(bool sparse, int block_size, int rows, int topk, int window,
-                           int max_context, int wgs) {
-  int pt = sparse ? kSparsePart : kMlaDensePart;
-  if (!sparse) {
-    const int cap = (63 * block_size + 32) & ~31;
-    pt = pt < cap ? pt : cap;
-  }
-  const int64_t keys = sparse ? topk : (window > 0 && window < max_context ? window : max_context);
-  const int64_t fit = keys * rows / (int64_t(device_cus()) * wgs);
-  const int64_t want = fit < 256 ? 256 : (fit & ~int64_t(31));
-  return want < pt ? int(want) : pt;
+// Target items per persistent workgroup (the plan's partition size is
+// T / (items_per_wg * workgroups)), and the most the workspace allows for.
+constexpr int kMlaItemsMax = 4;
+inline int mla_items_per_wg(bool c8, bool sparse) {
+  static const int v1 = [] { const char *e = getenv("IFATTN_MLA_K"); return e ? atoi(e) : 1; }();
+  static const int v2 = [] { const char *e = getenv("IFATTN_MLA_K_C8"); return e ? atoi(e) : 2; }();
+  const int k = c8 && !sparse ? v2 : v1;
+  return k < 1 ? 1 : (k > kMlaItemsMax ? kMlaItemsMax : k);
 }
+inline int mla_dense_cap() {
+  static const int v = [] { const char *e = getenv("IFATTN_MLA_PART"); return e ? atoi(e) : kMlaDensePart; }();
+  return v;
+}
+
+// Largest partition of a call: kSparsePart index entries, or the dense
+// default capped so that a partition starting on a 32-token tile spans at
+// most the 64 blocks one wave holds: 1 + ceil((PT - 32) / bs) <= 64, i.e.
+// PT <= 63 * bs + 32.
+inline int mla_part_cap(bool sparse, int block_size) {
+  if (sparse) return kSparsePart;
+  const int cap = (63 * block_size + 32) & ~31;
+  const int d = mla_dense_cap();
+  return d < cap ? d : cap;
+}
+// Partitions of the longest possible row at partition size pt (default: the
+// largest).
 inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size,
-                             int rows, int wgs) {
-  const int pt = mla_part_tokens(sparse, block_size, rows, topk, window, max_context, wgs);
+                             int pt = 0) {
+  if (pt <= 0) pt = mla_part_cap(sparse, block_size);
   if (sparse) return (topk + pt - 1) / pt;
   const int full = (max_context + pt - 1) / pt;
   if (window <= 0) return full;
   const int win = (window + 31 + pt - 1) / pt;
   return win < full ? win : full;
 }
-inline uint64_t mla_workspace(int rows, int heads, int ppr, bool partials) {
-  const uint64_t items = uint64_t(rows) * uint64_t(ppr);
-  uint64_t b = kQueueBytes + align16(items * 4) + align16(uint64_t(rows) * 4);
-  if (partials) b += items * heads * (512 + 2) * sizeof(float);
+// Items (and partial slots) a call can produce: the plan's partitions are
+// either the largest size (at most rows * ppr) or sized for items_per_wg per
+// workgroup (at most kMlaItemsMax * workgroups + rows), and never below
+// kMinPart keys (at most rows * ppr_min); plus one empty or sink item per row.
+inline uint64_t mla_item_cap(int rows, int ppr, int ppr_min) {
+  const uint64_t a = uint64_t(kMlaItemsMax) * uint64_t(device_cus()) * 2u + uint64_t(rows) * uint64_t(ppr + 3);
+  const uint64_t b = uint64_t(rows) * uint64_t(ppr_min + 3);
+  return a < b ? a : b;
+}
+inline uint64_t mla_workspace(int rows, int heads, int ppr, int ppr_min) {
+  const uint64_t items = mla_item_cap(rows, ppr, ppr_min);
+  uint64_t b = kQueueBytes + align16(items * 4) + 3 * align16(uint64_t(rows) * 4);
+  b += items * heads * (512 + 2) * sizeof(float);
   return b;
 }
 
@@ -912,12 +976,14 @@ int32_t mla_run(const MlaCall &c, const char *what) {
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
     return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
   const int wgs = wgs_mla(c.c8);
-  const int pt = mla_part_tokens(sparse, c.block_size, c.num_rows, c.topk, c.window, c.max_context, wgs);
-  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, c.num_rows, wgs) +
-                  (c.n_sinks > 0 ? 1 : 0);  // sinks: one more partial slot per row
-  if (ppr > 4096) return fail(IFATTN_EINVAL, what, "more than 4096 partitions per row");
-  const bool partials = ppr > 1 || c.n_sinks > 0;
-  const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, partials);
+  const int pt = mla_part_cap(sparse, c.block_size);
+  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
+  // Partition indices stay below the 12-bit sink marker: at most ppr at the
+  // largest size, at most items_per_wg * workgroups + 1 at smaller ones.
+  if (ppr >= 4095 || kMlaItemsMax * device_cus() * 2 + 1 >= 4095)
+    return fail(IFATTN_EINVAL, what, "more than 4094 partitions per row");
+  const int ppr_min = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, kMinPart);
+  const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, ppr_min);
   if (!c.workspace || c.workspace_bytes < need || !aligned16(c.workspace))
     return fail(IFATTN_EWORKSPACE, what, "workspace missing, short or misaligned");
   MlaParams p{};
@@ -942,18 +1008,22 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.window = c.window;
   p.n_sinks = c.n_sinks;
   p.part_tokens = pt;
-  p.parts_per_row = ppr;
+  p.items_per_wg = mla_items_per_wg(c.c8, sparse);
   p.scale_log2 = c.scale * kLog2e;
   uint8_t *ws = static_cast<uint8_t *>(c.workspace);
-  const uint64_t items = uint64_t(c.num_rows) * ppr;
+  const uint64_t items = mla_item_cap(c.num_rows, ppr, ppr_min);
   p.queue = reinterpret_cast<int32_t *>(ws);
   ws += kQueueBytes;
   p.items = reinterpret_cast<uint32_t *>(ws);
   ws += align16(items * 4);
   p.row_seq = reinterpret_cast<int32_t *>(ws);
   ws += align16(uint64_t(c.num_rows) * 4);
-  p.part_o = partials ? reinterpret_cast<float *>(ws) : nullptr;
-  p.part_ml = partials ? p.part_o + items * c.heads * 512 : nullptr;
+  p.row_pt = reinterpret_cast<int32_t *>(ws);
+  ws += align16(uint64_t(c.num_rows) * 4);
+  p.row_slot = reinterpret_cast<int32_t *>(ws);
+  ws += align16(uint64_t(c.num_rows) * 4);
+  p.part_o = reinterpret_cast<float *>(ws);
+  p.part_ml = p.part_o + items * c.heads * 512;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   const int grid = device_cus() * wgs;
   p.static_items = grid;  // the attention grid takes the first items by index
@@ -965,7 +1035,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
     if (sparse) mla_attention_kernel<false, true><<<grid, 64 * MlaCfg<false, true>::NW, 0, s>>>(p);
     else mla_attention_kernel<false, false><<<grid, 64 * MlaCfg<false, false>::NW, 0, s>>>(p);
   }
-  if (partials) mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
+  mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
   return launch_status(what);
 }
 
@@ -1001,8 +1071,8 @@ using namespace ifattn;
 extern "C" uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads,
                                                      int32_t max_context, int32_t block_size) {
   if (num_seqs <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
-  const int ppr = mla_parts_per_row(false, 0, 0, max_context, block_size, num_seqs, 2);
-  return mla_workspace(num_seqs, heads, ppr, ppr > 1);
+  return mla_workspace(num_seqs, heads, mla_parts_per_row(false, 0, 0, max_context, block_size),
+                       mla_parts_per_row(false, 0, 0, max_context, block_size, kMinPart));
 }
 
 extern "C" int32_t ifattn_mla_decode_bf16(const void *q, const void *cache,
@@ -1035,9 +1105,9 @@ extern "C" uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_
                                                         int32_t block_size) {
   if (num_rows <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
   const bool sparse = topk > 0;
-  const int ppr =
-      mla_parts_per_row(sparse, topk, window, max_context, block_size, num_rows, 2) + (n_sinks > 0 ? 1 : 0);
-  return mla_workspace(num_rows, heads, ppr, ppr > 1 || n_sinks > 0);
+  (void)n_sinks;  // sink partials use the slots counted per row
+  return mla_workspace(num_rows, heads, mla_parts_per_row(sparse, topk, window, max_context, block_size),
+                       mla_parts_per_row(sparse, topk, window, max_context, block_size, kMinPart));
 }
 
 extern "C" int32_t ifattn_mla_window_attention_bf16(
