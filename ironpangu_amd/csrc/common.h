@@ -73,12 +73,20 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // see these LDS writes: the caller waits for them with lds_dma_wait<N>() (N =
 // direct loads it may leave in flight) and a workgroup barrier before any wave
 // reads the bytes, and must not let such a load target bytes a wave may still
-// be reading.
+// be reading. NT sets the nontemporal cache policy (streamed bytes that no
+// other workgroup will read again).
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-               :
-               : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
-               : "memory");
+  if constexpr (NT)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
+                 : "memory");
+  else
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
+                 : "memory");
 }
 template <int N>
 __device__ __forceinline__ void lds_dma_wait() {

@@ -570,6 +570,9 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     } else {
       const int lower = t_begin > t0 ? t_begin - t0 : 0;  // rows before the window start
       const int upper = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
+      // Dense bf16 tiles stream with the nontemporal policy (config-5 decode
+      // 506 against 522-528 us; C8 unchanged, sparse gathers and the GQA
+      // decode's register loads measured slower with it).
       // A tile is one block, or two 16-row blocks (bf16 rows only, where load
       // n = 4k + w < 18 moves rows 0..15 and the rest rows 16..31). Each part's
       // base sits at its first live row: earlier rows wrap to offsets past the
@@ -591,7 +594,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
       for (int k = 0; k < R::NI; ++k) {
         const int hb = (halves == 2 && 4 * k + w >= 18) ? 1 : 0;
-        lds_dma16(hb ? rc[1] : rc[0], (lrow[k] - first_row[hb]) * R::BYTES + lcol[k],
+        lds_dma16<!C8>(hb ? rc[1] : rc[0], (lrow[k] - first_row[hb]) * R::BYTES + lcol[k],
                   dst + uint32_t(k) * 4096);
       }
     }
