@@ -17,7 +17,9 @@
 //    halves of the same 512-byte cache rows at the same time;
 //  * a wave walks 32-token tiles (16-token tiles at head_dim 256). QK^T is one
 //    MFMA 16x16x32 bf16 per (16 tokens, 32 dims): A = K rows straight from HBM
-//    (16 B per lane), B = the group's q heads (n = head, zero-padded to 16).
+//    (16 B per lane; bf16 loads cover whole 128-B lines and one DPP lane
+//    rotation puts each chunk at its token's lane), B = the group's q heads
+//    (n = head, zero-padded to 16). K and V loads stream nontemporally.
 //    The score tile lands with lane (c = lane%16, g = lane/16) holding tokens
 //    4g..4g+3 (and 16+4g..16+4g+3) of head c, so P never leaves registers: it
 //    is exactly the B operand of the PV MFMA once those tokens are declared
@@ -53,6 +55,32 @@ constexpr int decode_tile(int d) { return d > 128 ? 16 : 32; }
 #ifndef IFATTN_DECODE_STAGES
 #define IFATTN_DECODE_STAGES 3
 #endif
+// V loads stream with the nontemporal cache policy: each V load instruction
+// covers whole 128-B lines (16 lanes x 16 B of one row), which no other load
+// touches again (config-2 decode 5.58 -> 5.95 TB/s, C8 5.2 -> 5.5). K loads
+// keep the default policy: one K instruction covers half of each line of 16
+// rows and the next one the other half, which the default policy serves from
+// L2 (nontemporal K loads measured 16% slower).
+constexpr int kVPolicy = 2;
+// K loads cover whole lines too: instruction (h, L) of a 16-token row block
+// reads line L (128 B) of the kv head's slice of rows 8h .. 8h+7, lane (c, g)
+// taking 16-B chunk g + 4(c >> 3) of row (c & 7) + 8h, and streams
+// nontemporally. The MFMA operand (lane (c, g) = token c) of chunk column
+// g (+4) is then the lane's own value or that of lane c ^ 8 (DPP row_ror:8), so
+// a k-step's dims are a fixed permutation of the head dims, matched in q
+// (config-2 decode 5.95 -> 6.06 TB/s). bf16 caches with head_dim >= 64 (a kv
+// head's slice of a row is then whole lines); C8 caches keep the
+// half-line loads (the same scheme measured 3% slower on config 4).
+template <int D, bool C8>
+constexpr bool k_lines() { return !C8 && D * 2 >= 128; }
+constexpr int kKPolicy = 2;
+// Lane c of a 16-lane row gets the value of lane (c + 8) % 16 (DPP row_ror:8).
+__device__ __forceinline__ u32x4 row_ror8(u32x4 v) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_update_dpp(0u, v[i], 0x128, 0xF, 0xF, false);
+  return r;
+}
 // Tile buffers per wave (stages-1 tiles prefetched).
 template <int D>
 constexpr int decode_stages() { return D > 128 ? 4 : IFATTN_DECODE_STAGES; }
@@ -88,7 +116,7 @@ struct TileRegs {
 // they are computed once per work item and the per-tile cost is one scalar
 // buffer descriptor per cache.
 struct LaneOffsets {
-  uint32_t k[2];  // row 16*mt + c, dims (D/4)*g ...
+  uint32_t k[2];  // K loads of row block mt (see k_lines)
   uint32_t v[8];  // row tile_token(g, j), dims c*D/16 ..
   uint32_t sc[8]; // C8 scale of row tile_token(g, j)
 };
@@ -117,7 +145,12 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
   for (int mt = 0; mt < TileRegs<D, C8>::MT; ++mt) {
     if constexpr (!C8) {
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) t.k[mt][s] = buf_load_x4(rk, o.k[mt] + 16 * s);
+      for (int s = 0; s < D / 32; ++s) {
+        if constexpr (k_lines<D, C8>())  // t.k[mt][2L + h] = instruction (h, L)
+          t.k[mt][s] = buf_load_x4<kKPolicy>(rk, o.k[mt] + (s & 1) * 8 * row_bytes + 128 * (s >> 1));
+        else
+          t.k[mt][s] = buf_load_x4(rk, o.k[mt] + 16 * s);
+      }
     } else {
 #pragma unroll
       for (int s = 0; s < D / 32; s += 2) {
@@ -133,13 +166,13 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
     if constexpr (DW == 1) {
       t.v[j][0] = buf_load_x1(rv, o.v[j]);
     } else if constexpr (DW == 2) {
-      const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v[j], 0, 0));
+      const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rv, o.v[j], 0, kVPolicy));
       t.v[j][0] = w[0];
       t.v[j][1] = w[1];
     } else {
 #pragma unroll
       for (int q = 0; q < DW; q += 4) {
-        const u32x4 w = buf_load_x4(rv, o.v[j] + 4 * q);
+        const u32x4 w = buf_load_x4<kVPolicy>(rv, o.v[j] + 4 * q);
         t.v[j][q] = w[0];
         t.v[j][q + 1] = w[1];
         t.v[j][q + 2] = w[2];
@@ -200,12 +233,16 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
     return;
   }
 
-  // B operand of QK^T: q[head][(D/4)*g + 8*s + e], zero for padded heads.
+  // B operand of QK^T: q[head][d0(s, g) + e], zero for padded heads.
   u32x4 qv[D / 32];
   {
-    const uint16_t *qp = p.q + (q_row_of(p, seq) * p.q_heads + (head_live ? head : 0)) * D + (D / 4) * g;
+    const uint16_t *qr = p.q + (q_row_of(p, seq) * p.q_heads + (head_live ? head : 0)) * D;
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) qv[s] = head_live ? load_u32x4(qp + 8 * s) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < D / 32; ++s) {
+      // Dims of k-step s, lane group g (matching the K operand).
+      const int d0 = k_lines<D, C8>() ? 32 * s + 8 * g : (D / 4) * g + 8 * s;
+      qv[s] = head_live ? load_u32x4(qr + d0) : u32x4{0, 0, 0, 0};
+    }
   }
 
   LaneOffsets o;
@@ -213,7 +250,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
     constexpr int EB = C8 ? 1 : 2;
     const uint32_t row_bytes = uint32_t(p.kv_heads) * D * EB;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) o.k[mt] = uint32_t(16 * mt + c) * row_bytes + (D / 4) * g * EB;
+    for (int mt = 0; mt < 2; ++mt) {
+      if (k_lines<D, C8>())
+        o.k[mt] = uint32_t(16 * mt + (c & 7)) * row_bytes + 16 * (g + 4 * (c >> 3));
+      else
+        o.k[mt] = uint32_t(16 * mt + c) * row_bytes + (D / 4) * g * EB;
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       o.v[j] = uint32_t(tile_token(g, j)) * row_bytes + c * VSlice<D, C8>::BYTES;
@@ -248,7 +290,19 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 #pragma unroll
       for (int mt = 0; mt < TR::MT; ++mt) {
         u32x4 a;
-        if constexpr (!C8)
+        if constexpr (k_lines<D, C8>()) {
+          // k-step s: chunk column g (s even) or g + 4 (s odd) of line s >> 1,
+          // from instructions (0, s >> 1) and (1, s >> 1).
+          const u32x4 A = t.k[mt][s & ~1], B = t.k[mt][s | 1];
+          const bool lo = c < 8;
+          if ((s & 1) == 0) {
+            const u32x4 r = row_ror8(B);
+            a = u32x4{lo ? A[0] : r[0], lo ? A[1] : r[1], lo ? A[2] : r[2], lo ? A[3] : r[3]};
+          } else {
+            const u32x4 r = row_ror8(A);
+            a = u32x4{lo ? r[0] : B[0], lo ? r[1] : B[1], lo ? r[2] : B[2], lo ? r[3] : B[3]};
+          }
+        } else if constexpr (!C8)
           a = t.k[mt][s];
         else
           a = i8x8_to_bf16x8(t.k[mt][s][0], t.k[mt][s][1]);
