@@ -156,3 +156,27 @@ def test_decode_entry_matches_general():
     b = ops.mla_attention(to_dev(q), to_dev(cache), to_dev(table), to_dev(kv), maxc)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("c8,with_sinks,window", [(False, False, 0), (True, True, 0), (False, True, 300)])
+def test_many_rows(c8, with_sinks, window):
+    """More than 1024 query rows: the plan walks the rows in chunks of 1024
+    (partition slots and full-partition positions carried between chunks).
+    C8 rows take index lists (top-300 of their causal keys)."""
+    rng = np.random.default_rng(21)
+    counts = [1] * 1290 + [3, 1, 5]
+    kv = np.concatenate([rng.integers(0, 160, 1290), [2900, 3100, 1700]]).astype(np.int32)
+    kv[:1290:97] = rng.integers(1000, 2600, len(kv[:1290:97]))  # some rows span several partitions
+    q, cache, table, kv, cu, maxc = batch(23, counts, kv, 32, 4, c8)
+    sk, sv = sinks(9, 24) if with_sinks else (None, None)
+    idx = None
+    if c8:
+        topk = 300
+        idx = np.full((int(sum(counts)), topk), -1, np.int32)
+        for s in range(len(counts)):
+            for t in range(cu[s], cu[s + 1]):
+                causal = int(kv[s]) - counts[s] + (t - cu[s]) + 1
+                n = min(max(causal, 0), topk)
+                idx[t, :n] = rng.choice(max(causal, 1), size=n, replace=False)
+    got, exp = run(q, cache, table, kv, maxc, cu=cu, idx=idx, window=window, sk=sk, sv=sv)
+    assert_close(got, exp)
