@@ -66,13 +66,14 @@ struct MlaParams {
   int64_t num_blocks;
   uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
   int static_items;      // items 0..static_items-1 go to workgroups by index; the queue starts after
-  int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks,
-      part_tokens, items_per_wg;
+  int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks;
+  int part_tokens;   // largest partition the plan may pick (row_pt holds the chosen one)
+  int items_per_wg;  // plan target: items per persistent workgroup
   float scale_log2;
 };
 
 // Keys of one row: [lo, hi) are positions (dense) or index-list slots
-// (sparse); partitions of part_tokens start at `base` (lo rounded down to a
+// (sparse); partitions of the row's partition size start at `base` (lo rounded down to a
 // tile), so every tile is 32-aligned and never straddles a block.
 struct MlaSpan {
   int seq, lo, hi, base;
