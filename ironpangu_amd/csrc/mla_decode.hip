@@ -912,8 +912,15 @@ inline int mla_items_per_wg(bool c8, bool sparse) {
   const int k = c8 && !sparse ? v2 : v1;
   return k < 1 ? 1 : (k > kMlaItemsMax ? kMlaItemsMax : k);
 }
+// IFATTN_MLA_PART overrides the largest dense partition for tuning: a
+// multiple of 32 in [kMinPart, 8192] (the plan sorts items into SMAX/32 + 1 of
+// its 257 buckets); other values keep the default.
 inline int mla_dense_cap() {
-  static const int v = [] { const char *e = getenv("IFATTN_MLA_PART"); return e ? atoi(e) : kMlaDensePart; }();
+  static const int v = [] {
+    const char *e = getenv("IFATTN_MLA_PART");
+    const int x = e ? atoi(e) : 0;
+    return (x >= kMinPart && x <= 8192 && x % 32 == 0) ? x : kMlaDensePart;
+  }();
   return v;
 }
 
