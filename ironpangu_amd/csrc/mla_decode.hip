@@ -276,25 +276,40 @@ static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 
 // Ring depth and persistent workgroups per CU of each kernel variant. bf16
 // runs one workgroup of four waves per CU with a 4-tile ring (its 36-KB tiles
-// keep HBM busy while the tile math runs). C8 runs two workgroups per CU (two
-// waves per SIMD): its 21-KB tiles arrive faster than one workgroup's tile
-// math retires them, and a second workgroup overlaps that math. Measured on
+// keep HBM busy while the tile math runs). C8 runs several workgroups per CU
+// (two for sparse, three for dense): its 21-KB tiles arrive faster than one
+// workgroup's tile math retires them, and the others overlap that math. Measured on
 // 128 rows: C8 decode over log-uniform [1024, 65536] keys 582 us with one
 // workgroup and 6 stages, 456 us with two and 3 stages; sparse top-2048
 // 95.9 us with one workgroup and 6 stages, 75.9 us with two and 2 stages.
 template <bool C8, bool SPARSE>
 struct MlaCfg {
-  static constexpr int WGS = C8 ? 2 : 1;
+  // Dense C8 runs three workgroups per CU (three waves per SIMD): 21-KiB ring
+  // slots (the 21 loads a 20992-B tile needs) and one score buffer (two
+  // barriers per tile) fit three in the LDS, and the tile math of one
+  // workgroup hides behind the other two (config-5 shapes 380-386 -> 349-356 us
+  // against two workgroups with double score buffers).
+  static constexpr bool TIGHT = C8 && !SPARSE;
+  static constexpr int WGS = C8 ? (TIGHT ? 3 : 2) : 1;
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
   static constexpr int NW = kMlaWaves;
   static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : 4);
-  static constexpr int RING = MlaRow<C8>::SLOT * STAGES;
-  static constexpr int LDS = RING + 2 * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
+  static constexpr int SLOT = TIGHT ? 21 * 1024 : int(MlaRow<C8>::SLOT);
+  static constexpr int LOADS = TIGHT ? 21 : 4 * MlaRow<C8>::NI;  // 1-KiB loads per tile
+  static constexpr int XB = TIGHT ? 1 : 2;                        // score buffers
+  static constexpr int RING = SLOT * STAGES;
+  static constexpr int LDS = RING + XB * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
-inline int wgs_mla(bool c8) { return c8 ? 2 : 1; }
+// Persistent workgroups per CU of the kernel variant a call runs (the grid is
+// that many per CU, all resident at once).
+inline int wgs_mla(bool c8, bool sparse) {
+  if (!c8) return sparse ? MlaCfg<false, true>::WGS : MlaCfg<false, false>::WGS;
+  return sparse ? MlaCfg<true, true>::WGS : MlaCfg<true, false>::WGS;
+}
+constexpr int kMlaWgsMax = 3;  // most persistent workgroups per CU of any variant
 // Wave geometry of a workgroup of NW waves: wave w owns the latent dims
 // [DPW w, DPW w + DPW) for QK^T and PV (KS k-steps of 32), waves 0 and 1 add
 // 32 rope dims each; a lane holds EPL dims of each of its eight V tokens and
@@ -463,6 +478,7 @@ template <bool C8, bool SPARSE>
 __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
                                          uint32_t *slot_list, int row, int part, int w, int lane) {
   using R = MlaRow<C8>;
+  using Cfg = MlaCfg<C8, SPARSE>;
   constexpr int S = MlaCfg<C8, SPARSE>::STAGES;
   constexpr int NW = MlaCfg<C8, SPARSE>::NW;
   using Geo = MlaGeo<NW>;
@@ -557,7 +573,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   auto issue = [&](int ti) {
     if (NW > kMlaWaves && w >= kMlaWaves) return;
     const int t0 = tile0 + ti * kMlaTile;
-    const uint32_t dst = ring_base + uint32_t(ti % S) * R::SLOT + uint32_t(w) * 1024;
+    const uint32_t dst = ring_base + uint32_t(ti % S) * Cfg::SLOT + uint32_t(w) * 1024;
     if constexpr (SPARSE) {
       // Gather: rows named by the slot list; offsets from the cache base.
       const u32x4 rc = raw_rsrc(p.cache, p.cache_bytes);
@@ -594,6 +610,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
 #pragma unroll
       for (int k = 0; k < R::NI; ++k) {
+        if constexpr (Cfg::TIGHT)
+          if (4 * k + w >= Cfg::LOADS) break;
         const int hb = (halves == 2 && 4 * k + w >= 18) ? 1 : 0;
         lds_dma16<!C8>(hb ? rc[1] : rc[0], (lrow[k] - first_row[hb]) * R::BYTES + lcol[k],
                   dst + uint32_t(k) * 4096);
@@ -679,17 +697,23 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
   for (int i = 0; i < S; ++i)
     if (i < n_tiles) issue(i);
-  if (S - 1 < n_tiles)  // tile 0; tiles 1 .. S-1 may stay in flight
-    lds_dma_wait<(S - 1) * R::NI>();
-  else
+  if (S - 1 < n_tiles) {  // tile 0; tiles 1 .. S-1 may stay in flight
+    // Loads per wave per tile: NI, or NI - 1 for the waves past LOADS.
+    if (!Cfg::TIGHT || w < Cfg::LOADS - 4 * (R::NI - 1))
+      lds_dma_wait<(S - 1) * R::NI>();
+    else
+      lds_dma_wait<(S - 1) * (R::NI - 1)>();
+  } else {
     lds_dma_wait<0>();
+  }
   __syncthreads();
   for (int ti = 0; ti < n_tiles; ++ti) {
-    float (*xb)[8] = xbuf + (ti & 1) * NW * 64;
+    float (*xb)[8] = xbuf + (Cfg::XB == 2 ? (ti & 1) : 0) * NW * 64;
     u32x4 v[8];
     float sk[C8 ? 8 : 1];
     uint32_t live;
-    score(ring + (ti % S) * R::SLOT, tile0 + ti * kMlaTile, v, sk, live, xb);
+    score(ring + (ti % S) * Cfg::SLOT, tile0 + ti * kMlaTile, v, sk, live, xb);
+    static_assert(S == 2 || Cfg::LOADS == 4 * R::NI, "uneven per-wave loads need S == 2");
     if (ti + S - 1 < n_tiles)  // tile ti+1; tiles ti+2 .. ti+S-1 may stay in flight
       lds_dma_wait<(S - 2) * R::NI>();
     else
@@ -697,6 +721,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     __syncthreads();
     if (ti + S < n_tiles) issue(ti + S);
     mla_tile_softmax_pv<C8, NW>(acc, v, sk, xb, live, p.scale_log2, lane);
+    if constexpr (Cfg::XB == 1) __syncthreads();  // xb is rewritten by the next tile
   }
 
   float l_tot = sum_xor16(acc.l);
@@ -802,7 +827,7 @@ template <bool C8, bool SPARSE>
 __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
   constexpr int NW = MlaCfg<C8, SPARSE>::NW;
   __shared__ __align__(16) uint8_t ring[MlaCfg<C8, SPARSE>::RING];
-  __shared__ __align__(16) float xbuf[2 * NW * 64][8];  // score exchange, two halves
+  __shared__ __align__(16) float xbuf[MlaCfg<C8, SPARSE>::XB * NW * 64][8];  // score exchange
   // The sparse slot list lives in the workgroup's LDS only for sparse calls
   // (the dense C8 variant fits two workgroups per CU exactly).
   uint32_t *slot_list = nullptr;
@@ -908,7 +933,7 @@ constexpr int kMlaDensePart = 3072;
 constexpr int kMlaItemsMax = 4;
 inline int mla_items_per_wg(bool c8, bool sparse) {
   static const int v1 = [] { const char *e = getenv("IFATTN_MLA_K"); return e ? atoi(e) : 1; }();
-  static const int v2 = [] { const char *e = getenv("IFATTN_MLA_K_C8"); return e ? atoi(e) : 2; }();
+  static const int v2 = [] { const char *e = getenv("IFATTN_MLA_K_C8"); return e ? atoi(e) : 1; }();
   const int k = c8 && !sparse ? v2 : v1;
   return k < 1 ? 1 : (k > kMlaItemsMax ? kMlaItemsMax : k);
 }
@@ -950,7 +975,7 @@ inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context,
 // workgroup (at most kMlaItemsMax * workgroups + rows), and never below
 // kMinPart keys (at most rows * ppr_min); plus one empty or sink item per row.
 inline uint64_t mla_item_cap(int rows, int ppr, int ppr_min) {
-  const uint64_t a = uint64_t(kMlaItemsMax) * uint64_t(device_cus()) * 2u + uint64_t(rows) * uint64_t(ppr + 3);
+  const uint64_t a = uint64_t(kMlaItemsMax) * uint64_t(device_cus()) * kMlaWgsMax + uint64_t(rows) * uint64_t(ppr + 3);
   const uint64_t b = uint64_t(rows) * uint64_t(ppr_min + 3);
   return a < b ? a : b;
 }
@@ -986,12 +1011,12 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
     return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
-  const int wgs = wgs_mla(c.c8);
+  const int wgs = wgs_mla(c.c8, sparse);
   const int pt = mla_part_cap(sparse, c.block_size);
   const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
   // Partition indices stay below the 12-bit sink marker: at most ppr at the
   // largest size, at most items_per_wg * workgroups + 1 at smaller ones.
-  if (ppr >= 4095 || kMlaItemsMax * device_cus() * 2 + 1 >= 4095)
+  if (ppr >= 4095 || kMlaItemsMax * device_cus() * kMlaWgsMax + 1 >= 4095)
     return fail(IFATTN_EINVAL, what, "more than 4094 partitions per row");
   const int ppr_min = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, kMinPart);
   const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, ppr_min);
