@@ -288,7 +288,8 @@ struct MlaCfg {
   // slots (the 21 loads a 20992-B tile needs) and one score buffer (two
   // barriers per tile) fit three in the LDS, and the tile math of one
   // workgroup hides behind the other two (config-5 shapes 380-386 -> 349-356 us
-  // against two workgroups with double score buffers).
+  // against two workgroups with double score buffers). Sparse C8 keeps two:
+  // three (with 512-entry slot lists) measured 81 against 72 us on top-2048.
   static constexpr bool TIGHT = C8 && !SPARSE;
   static constexpr int WGS = C8 ? (TIGHT ? 3 : 2) : 1;
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
@@ -579,6 +580,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       const u32x4 rc = raw_rsrc(p.cache, p.cache_bytes);
 #pragma unroll
       for (int k = 0; k < R::NI; ++k) {
+        if constexpr (Cfg::TIGHT)
+          if (4 * k + w >= Cfg::LOADS) break;
         const uint32_t r = lrow[k];
         const uint32_t slot = r < 32u && t0 + int(r) < t_end ? slot_list[ti * kMlaTile + r] : kNoRow;
         const uint32_t off = slot == kNoRow ? 0xFFFFFFF0u : slot * R::BYTES + lcol[k];
