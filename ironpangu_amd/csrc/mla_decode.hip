@@ -282,7 +282,7 @@ static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 // 128 rows: C8 decode over log-uniform [1024, 65536] keys 582 us with one
 // workgroup and 6 stages, 456 us with two and 3 stages; sparse top-2048
 // 95.9 us with one workgroup and 6 stages, 75.9 us with two and 2 stages.
-template <bool C8, bool SPARSE>
+template <bool C8, bool SPARSE, bool WIDE = false>
 struct MlaCfg {
   // Dense C8 runs three workgroups per CU (three waves per SIMD): 21-KiB ring
   // slots (the 21 loads a 20992-B tile needs) and one score buffer (two
@@ -291,26 +291,33 @@ struct MlaCfg {
   // against two workgroups with double score buffers). Sparse C8 keeps two:
   // three (with 512-entry slot lists) measured 81 against 72 us on top-2048.
   static constexpr bool TIGHT = C8 && !SPARSE;
-  static constexpr int WGS = C8 ? (TIGHT ? 3 : 2) : 1;
+  // Large dense bf16 calls (WIDE) run two workgroups per CU, each with a
+  // 2-slot ring and one score buffer (exactly 160 KiB): config-5 decode 507-510
+  // -> 489-491 us. Small calls keep one workgroup with a 4-slot ring (window
+  // 2048 over 128 rows: 79 against 83 us with two).
+  static constexpr bool B2 = !C8 && !SPARSE && WIDE;
+  static constexpr int WGS = C8 ? (TIGHT ? 3 : 2) : (B2 ? 2 : 1);
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
   static constexpr int NW = kMlaWaves;
-  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : 4);
+  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : 4));
   static constexpr int SLOT = TIGHT ? 21 * 1024 : int(MlaRow<C8>::SLOT);
   static constexpr int LOADS = TIGHT ? 21 : 4 * MlaRow<C8>::NI;  // 1-KiB loads per tile
-  static constexpr int XB = TIGHT ? 1 : 2;                        // score buffers
+  static constexpr int XB = (TIGHT || B2) ? 1 : 2;                // score buffers
   static constexpr int RING = SLOT * STAGES;
   static constexpr int LDS = RING + XB * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
 // Persistent workgroups per CU of the kernel variant a call runs (the grid is
 // that many per CU, all resident at once).
-inline int wgs_mla(bool c8, bool sparse) {
-  if (!c8) return sparse ? MlaCfg<false, true>::WGS : MlaCfg<false, false>::WGS;
+inline int wgs_mla(bool c8, bool sparse, bool wide) {
+  if (!c8) return sparse ? MlaCfg<false, true>::WGS
+                         : (wide ? MlaCfg<false, false, true>::WGS : MlaCfg<false, false>::WGS);
   return sparse ? MlaCfg<true, true>::WGS : MlaCfg<true, false>::WGS;
 }
 constexpr int kMlaWgsMax = 3;  // most persistent workgroups per CU of any variant
+constexpr int64_t kMlaWideKeys = int64_t(1) << 21;
 // Wave geometry of a workgroup of NW waves: wave w owns the latent dims
 // [DPW w, DPW w + DPW) for QK^T and PV (KS k-steps of 32), waves 0 and 1 add
 // 32 rope dims each; a lane holds EPL dims of each of its eight V tokens and
@@ -475,13 +482,13 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
 // direct-to-LDS loads shared by the four waves through a ring of R::STAGES
 // slots; every wave reads its K operand (keys in rows) and its V operand (dims
 // in rows) from the same LDS bytes.
-template <bool C8, bool SPARSE>
+template <bool C8, bool SPARSE, bool WIDE>
 __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
                                          uint32_t *slot_list, int row, int part, int w, int lane) {
   using R = MlaRow<C8>;
-  using Cfg = MlaCfg<C8, SPARSE>;
-  constexpr int S = MlaCfg<C8, SPARSE>::STAGES;
-  constexpr int NW = MlaCfg<C8, SPARSE>::NW;
+  using Cfg = MlaCfg<C8, SPARSE, WIDE>;
+  constexpr int S = Cfg::STAGES;
+  constexpr int NW = Cfg::NW;
   using Geo = MlaGeo<NW>;
   constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   constexpr int DV = 512;
@@ -826,11 +833,12 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
 }
 
-template <bool C8, bool SPARSE>
-__global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>::WGS)) void mla_attention_kernel(MlaParams p) {
-  constexpr int NW = MlaCfg<C8, SPARSE>::NW;
-  __shared__ __align__(16) uint8_t ring[MlaCfg<C8, SPARSE>::RING];
-  __shared__ __align__(16) float xbuf[MlaCfg<C8, SPARSE>::XB * NW * 64][8];  // score exchange
+template <bool C8, bool SPARSE, bool WIDE>
+__global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SPARSE, WIDE>::WGS)) void mla_attention_kernel(MlaParams p) {
+  using Cfg = MlaCfg<C8, SPARSE, WIDE>;
+  constexpr int NW = Cfg::NW;
+  __shared__ __align__(16) uint8_t ring[Cfg::RING];
+  __shared__ __align__(16) float xbuf[Cfg::XB * NW * 64][8];  // score exchange
   // The sparse slot list lives in the workgroup's LDS only for sparse calls
   // (the dense C8 variant fits two workgroups per CU exactly).
   uint32_t *slot_list = nullptr;
@@ -854,7 +862,7 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE>::NW), (MlaCfg<C8, SPARSE>:
     if (p.n_sinks > 0 && (e & 0xfffu) == kSinkItem)
       mla_sink_item<NW>(p, xbuf, int(e >> 12), w, lane);
     else
-      mla_item<C8, SPARSE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
+      mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
     __syncthreads();  // every wave is done with xbuf (and the ring)
     if (threadIdx.x == 0) *item_slot = next;
     __syncthreads();
@@ -1014,7 +1022,11 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
     return fail(IFATTN_EINVAL, what, "0..128 sink rows with 4-byte aligned keys and values");
-  const int wgs = wgs_mla(c.c8, sparse);
+  // Two-workgroup bf16 layout for large dense calls: at least kMlaWideKeys
+  // keys possible over all rows.
+  const int64_t span = (c.window > 0 && c.window < c.max_context) ? int64_t(c.window) + 31 : c.max_context;
+  const bool wide = !c.c8 && !sparse && int64_t(c.num_rows) * span >= kMlaWideKeys;
+  const int wgs = wgs_mla(c.c8, sparse, wide);
   const int pt = mla_part_cap(sparse, c.block_size);
   const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
   // Partition indices stay below the 12-bit sink marker: at most ppr at the
@@ -1068,11 +1080,12 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.static_items = grid;  // the attention grid takes the first items by index
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
-    if (sparse) mla_attention_kernel<true, true><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
-    else mla_attention_kernel<true, false><<<grid, 64 * MlaCfg<true, false>::NW, 0, s>>>(p);
+    if (sparse) mla_attention_kernel<true, true, false><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
+    else mla_attention_kernel<true, false, false><<<grid, 64 * MlaCfg<true, false>::NW, 0, s>>>(p);
   } else {
-    if (sparse) mla_attention_kernel<false, true><<<grid, 64 * MlaCfg<false, true>::NW, 0, s>>>(p);
-    else mla_attention_kernel<false, false><<<grid, 64 * MlaCfg<false, false>::NW, 0, s>>>(p);
+    if (sparse) mla_attention_kernel<false, true, false><<<grid, 64 * MlaCfg<false, true>::NW, 0, s>>>(p);
+    else if (wide) mla_attention_kernel<false, false, true><<<grid, 64 * MlaCfg<false, false, true>::NW, 0, s>>>(p);
+    else mla_attention_kernel<false, false, false><<<grid, 64 * MlaCfg<false, false>::NW, 0, s>>>(p);
   }
   mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
   return launch_status(what);

@@ -113,3 +113,25 @@ def test_mla_decode_c8_q_range():
     exp = oracle.mla_decode(q, oracle.mla_pack_c8(pool), case.block_tables, case.seq_lens, heads,
                             bs, scale, c8=True)
     assert_close(bf16_host(out), exp)
+
+
+def test_mla_decode_wide_layout():
+    """Dense bf16 calls with at least 2^21 possible keys (rows x max_context)
+    run the two-workgroup layout: 64 rows at max_context 40000 (tables padded
+    to cover it), actual lengths up to 6000."""
+    import torch
+    from ironpangu_amd import ops
+    case = W.mla_host_case(9, num_seqs=64, lo=1, hi=6000, dist="loguniform", heads=16,
+                           block_size=64, fixed={0: 6000, 1: 1, 2: 3072, 3: 3073})
+    h = case.host
+    nb, bs = case.pool_blocks, case.block_size
+    max_context = 40000
+    assert 64 * max_context >= 1 << 21
+    tables = np.zeros((64, (max_context + bs - 1) // bs), np.int32)
+    tables[:, :case.block_tables.shape[1]] = case.block_tables
+    cache = to_dev(h["pool"]).view(nb, bs, 576)
+    out = ops.mla_decode(to_dev(h["q"]), cache, to_dev(tables), to_dev(case.seq_lens), max_context,
+                         case.scale)
+    torch.cuda.synchronize()
+    exp = oracle.mla_decode(h["q"], h["pool"], case.block_tables, case.seq_lens, 16, bs, case.scale)
+    assert_close(bf16_host(out), exp)
