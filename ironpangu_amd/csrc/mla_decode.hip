@@ -32,8 +32,10 @@
 // folded into its probabilities for PV. MFMA 16x16x32 bf16 with the heads in
 // the N dimension; C8 latent scores use the fp16 MFMA on the codes biased by
 // 1152 (three VALU ops per four codes instead of a convert per code), with q
-// in fp16 and the bias term removed per head. Rows split over several partitions, and rows with sinks,
-// write (m, l, O) partials; a merge kernel adds the sink rows and combines.
+// in fp16 and the bias term removed per head. Rows split over several
+// partitions, and rows with sinks, write (m, l, O) partials; a merge kernel
+// adds the sink rows and combines. The plan sizes partitions from the call's
+// key count; how many workgroups share a CU depends on the variant (MlaCfg).
 #include "common.h"
 #include "ifattn_internal.h"
 #include "split_k.h"
