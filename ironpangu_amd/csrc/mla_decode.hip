@@ -291,14 +291,15 @@ struct MlaCfg {
   // barriers per tile) fit three in the LDS, and the tile math of one
   // workgroup hides behind the other two (config-5 shapes 380-386 -> 349-356 us
   // against two workgroups with double score buffers). Sparse C8 keeps two:
-  // three (with 512-entry slot lists) measured 81 against 72 us on top-2048.
+  // three (with 512-entry slot lists) measured 81 against 72 us on top-2048,
+  // and two with 3-slot rings of 21-KiB slots and one score buffer 74 us.
   static constexpr bool TIGHT = C8 && !SPARSE;
   // Large dense bf16 calls (WIDE) run two workgroups per CU, each with a
   // 2-slot ring and one score buffer (exactly 160 KiB): config-5 decode 507-510
   // -> 489-491 us. Small calls keep one workgroup with a 4-slot ring (window
   // 2048 over 128 rows: 79 against 83 us with two).
   static constexpr bool B2 = !C8 && !SPARSE && WIDE;
-  static constexpr int WGS = C8 ? (TIGHT ? 3 : 2) : (B2 ? 2 : 1);
+  static constexpr int WGS = C8 ? ((TIGHT && !SPARSE) ? 3 : 2) : (B2 ? 2 : 1);
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
@@ -725,11 +726,14 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     float sk[C8 ? 8 : 1];
     uint32_t live;
     score(ring + (ti % S) * Cfg::SLOT, tile0 + ti * kMlaTile, v, sk, live, xb);
-    static_assert(S == 2 || Cfg::LOADS == 4 * R::NI, "uneven per-wave loads need S == 2");
-    if (ti + S - 1 < n_tiles)  // tile ti+1; tiles ti+2 .. ti+S-1 may stay in flight
-      lds_dma_wait<(S - 2) * R::NI>();
-    else
+    if (ti + S - 1 < n_tiles) {  // tile ti+1; tiles ti+2 .. ti+S-1 may stay in flight
+      if (!Cfg::TIGHT || w < Cfg::LOADS - 4 * (R::NI - 1))
+        lds_dma_wait<(S - 2) * R::NI>();
+      else
+        lds_dma_wait<(S - 2) * (R::NI - 1)>();
+    } else {
       lds_dma_wait<0>();
+    }
     __syncthreads();
     if (ti + S < n_tiles) issue(ti + S);
     mla_tile_softmax_pv<C8, NW>(acc, v, sk, xb, live, p.scale_log2, lane);
