@@ -195,3 +195,30 @@ def test_decode_step_matches_write_then_decode():
                               bits_host(vc2).reshape(-1, hkv, hd), case.block_tables,
                               case.seq_lens, 16, 2, 128, 128, case.scale)
     assert_close(bf16_host(out1), exp)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_random_shapes(seed):
+    """Seeded random shapes across the K/V load paths (whole-line bf16 K loads
+    with lane rotation at head_dim 64/128/256, 16- and 32-token tiles, group
+    sizes 1..16, block sizes 32..128) with ragged lengths that cross tile,
+    block and split-K partition edges."""
+    rng = np.random.default_rng(1000 + seed)
+    hd = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    group = int(rng.choice([g for g in (1, 2, 4, 8, 16) if g * hkv <= 64]))
+    bs = int(rng.choice([32, 64, 128]))  # a partition spans at most 64 blocks
+    n = int(rng.integers(1, 12))
+    hi = int(rng.choice([40, 700, 2500, 5000]))
+    lens = rng.integers(1, hi + 1, n)
+    lens[0] = hi
+    need = n * ((hi + bs - 1) // bs)  # covers the lengths decode_meta draws and these
+    case = W.decode_host_case(2000 + seed, num_seqs=n, lo=1, hi=hi, dist="uniform",
+                              q_heads=group * hkv, kv_heads=hkv, head_dim=hd, block_size=bs,
+                              pool_blocks=need + 4)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(seed), case.seq_lens, bs, need + 4,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(n), bs)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp, what=f"hd {hd} hkv {hkv} group {group} bs {bs} lens {list(lens)}")
