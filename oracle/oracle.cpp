@@ -78,8 +78,9 @@ void parallel_for(int64_t n, int threads, F &&f) {
 
 int default_threads(int threads) {
   if (threads > 0) return threads;
+  // A GPU box gives one GPU's process a share of 16 host cores.
   unsigned h = std::thread::hardware_concurrency();
-  return h ? int(h) : 1;
+  return h ? int(std::min(h, 16u)) : 1;
 }
 
 // Symmetric RNE quantization of one group; returns the scale.
