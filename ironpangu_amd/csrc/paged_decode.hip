@@ -503,8 +503,9 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   if (max_context <= 0 || num_blocks <= 0 || table_stride <= 0 ||
       int64_t(table_stride) * block_size < max_context)
     return fail(IFATTN_EINVAL, "paged decode: table_stride * block_size must cover max_context");
-  if (num_seqs > 65535 * 64)
-    return fail(IFATTN_EINVAL, "paged decode: too many sequences");
+  // Work items pack (sequence << 12 | partition) into 32 bits.
+  if (num_seqs >= (1 << 20))
+    return fail(IFATTN_EINVAL, "paged decode: num_seqs must be below 2^20");
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
     return fail(IFATTN_EINVAL, "paged decode: q, out and caches must be 16-byte aligned");
   DecodeParams p{};

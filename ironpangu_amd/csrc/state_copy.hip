@@ -9,7 +9,10 @@
 // (nontemporal loads and stores: the bytes are not read again soon; the
 // loads measured copy 381 -> 368 us per GiB). Spans whose offset, size or base
 // are not 16-byte aligned fall back to a byte loop; spans outside the field
-// are skipped.
+// and copy ranges whose source and destination overlap are skipped. The span
+// sizes live on the device, so the second grid dimension is sized from the
+// field's average share per span: a plan mixing one small span into a large
+// field launches idle workgroups for it, which exit at once.
 #include "common.h"
 #include "ifattn_internal.h"
 #include "split_k.h"
@@ -31,6 +34,10 @@ __global__ __launch_bounds__(256) void state_span_kernel(uint8_t *__restrict__ f
   if (bytes == 0 || src > field_bytes || bytes > field_bytes - src || dst > field_bytes ||
       bytes > field_bytes - dst)
     return;
+  // A copy range whose source and destination overlap has no defined result
+  // under a parallel copy; such ranges are skipped (copy plans move pages
+  // between distinct residents, so they never overlap).
+  if (COPY && src < dst + bytes && dst < src + bytes) return;
   const uint64_t lanes = uint64_t(gridDim.y) * blockDim.x;
   const uint64_t me = uint64_t(blockIdx.y) * blockDim.x + threadIdx.x;
   if (((src | dst | bytes | reinterpret_cast<uintptr_t>(field)) & 15u) == 0) {

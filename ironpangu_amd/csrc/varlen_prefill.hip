@@ -48,6 +48,8 @@ struct PrefillParams {
   int32_t *n_items;
   int64_t num_blocks;
   int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_kv, q_tile;
+  int max_q_len;   // rows per sequence beyond this are not scheduled (cu_seqlens is device data)
+  int max_items;   // capacity of `items`
   float scale_log2;
 };
 
@@ -88,7 +90,8 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
       __syncthreads();  // the previous chunk's staged values are no longer read
       if (base + tid < p.num_seqs) {
         const int seq = base + tid;
-        s_count[tid] = p.cu[seq + 1] - p.cu[seq];
+        const int count = p.cu[seq + 1] - p.cu[seq];
+        s_count[tid] = count > p.max_q_len ? p.max_q_len : count;
         const int kv = p.kv_lens[seq];
         s_kv[tid] = kv > p.max_kv ? p.max_kv : kv;
       }
@@ -106,10 +109,11 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(PrefillParams p) {
   {
     static_assert(kBuckets <= 64 * 17, "bucket_prefix covers 17 buckets per lane");
     const int run = bucket_prefix<17>(bucket, nbk - 1, 0, tid);
-    if (tid == 0) *p.n_items = run;
+    if (tid == 0) *p.n_items = run < p.max_items ? run : p.max_items;
   }
   for_each_tile([&](int seq, int qt, int b) {
-    p.items[atomicAdd(&bucket[b], 1)] = (uint32_t(seq) << 12) | uint32_t(qt);
+    const int slot = atomicAdd(&bucket[b], 1);
+    if (slot < p.max_items) p.items[slot] = (uint32_t(seq) << 12) | uint32_t(qt);
   });
 }
 
@@ -494,6 +498,9 @@ extern "C" int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache
   if (num_seqs <= 0 || total_q <= 0 || max_q_len <= 0 || q_heads <= 0 || kv_heads <= 0 ||
       q_heads % kv_heads)
     return fail(IFATTN_EINVAL, "varlen prefill: bad sequence or head counts");
+  // Work items pack (sequence << 12 | query tile) into 32 bits.
+  if (num_seqs >= (1 << 20))
+    return fail(IFATTN_EINVAL, "varlen prefill: num_seqs must be below 2^20");
   const int group = q_heads / kv_heads;
   if (group != 1 && group != 2 && group != 4 && group != 8 && group != 16)
     return fail(IFATTN_EINVAL, "varlen prefill: q_heads / kv_heads must be 1, 2, 4, 8 or 16");
@@ -560,7 +567,11 @@ extern "C" int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache
   p.max_kv = max_kv_len;
   p.q_tile = prefill_q_tile(head_dim, group);
   p.scale_log2 = d.scale_log2;
+  if (int64_t(max_q_len) > int64_t(4096) * p.q_tile)
+    return fail(IFATTN_EINVAL, "varlen prefill: max_q_len above 4096 query tiles per sequence");
+  p.max_q_len = max_q_len;
   const int grid = int(prefill_items_bound(num_seqs, total_q, p.q_tile));
+  p.max_items = grid;
 
   launch_varlen_decode_rows(d, head_dim, s);
   prefill_plan_kernel<<<1, 1024, 0, s>>>(p);

@@ -228,3 +228,21 @@ def test_mla_attention_prepare():
     assert st == 0
     assert p.workspace_bytes == lib.ifattn_mla_attention_workspace_size(4, 16, 65536, 2048, 0, 128, 16)
     k.release(p.state)
+
+
+def test_work_item_encoding_bounds():
+    """Decode and prefill work items pack (sequence << 12 | tile) in 32 bits:
+    2^20 sequences, or more than 4096 query tiles per sequence, are refused on
+    the host (fake device addresses: nothing is launched)."""
+    lib = _native.lib()
+    a = 0x10000
+    st = lib.ifattn_paged_decode_bf16(a, a, a, a, 8, a, a, 1 << 20, 16, 2, 128, 128, 8, 1024,
+                                      0.1, a, 1 << 40, None)
+    assert st == -1 and b"2^20" in lib.ifattn_last_error()
+    st = lib.ifattn_varlen_prefill_bf16(a, a, a, a, 8, a, a, a, 1 << 20, 1 << 20, 1, 1024, 16, 2,
+                                        128, 128, 8, 0.1, a, 1 << 40, None)
+    assert st == -1 and b"2^20" in lib.ifattn_last_error()
+    # head_dim 256, group 16: 8-row query tiles, so 4096 tiles hold 32768 rows
+    st = lib.ifattn_varlen_prefill_bf16(a, a, a, a, 2048, a, a, a, 1, 32769, 32769, 262144, 16, 1,
+                                        256, 128, 2048, 0.1, a, 1 << 40, None)
+    assert st == -1 and b"4096 query tiles" in lib.ifattn_last_error()

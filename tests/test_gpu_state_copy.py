@@ -88,3 +88,19 @@ def test_graph_replay_reads_new_plans():
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(t.cpu().numpy(), exp), rep
+
+
+def test_overlapping_copy_range_is_skipped():
+    """A range whose source and destination overlap is skipped; the other
+    ranges of the same plan are copied."""
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(3)
+    field = rng.integers(0, 256, 1 << 16, dtype=np.uint8)
+    plan = np.array([[0, 4096, 8192], [32768, 49152, 4096]], np.uint64)  # first overlaps itself
+    exp = field.copy()
+    exp[49152:53248] = field[32768:36864]
+    t = dev(field)
+    ops.state_copy(t, dev(plan.view(np.int64)))
+    torch.cuda.synchronize()
+    assert np.array_equal(t.cpu().numpy(), exp)
