@@ -133,6 +133,29 @@ int32_t ifattn_paged_decode_step_bf16(const void *q, const void *k_rows, const v
                                       float scale, void *workspace, uint64_t workspace_bytes,
                                       void *stream);
 
+/* The Qwen-shape paged attention of the reference session ABI
+ * (inferfabric_acl_paged_attention_prepare, native/include/inferfabric_acl.h:103-113;
+ * body native/src/inferfabric_acl.cpp:1343-1430), with device pointers in place
+ * of the session's buffer ids and the same argument order and meaning:
+ *   q [batch, 8, 256] bf16 (kv head major: head h reads kv head h / 4);
+ *   k, v [batch, 512] bf16 rows appended at keys/values[append[b]] (int64);
+ *   keys, values [slots, 512] bf16 caches (2 kv heads x 256);
+ *   table [batch, context] int64: the physical row of every context position;
+ *   mask [batch, context] fp32, added to the scaled scores (-inf drops the
+ *   position, and such positions are never read from the caches);
+ *   gate [batch, 8, 256] bf16, multiplied into the attention output;
+ *   out [batch, 8, 256] bf16.
+ * Scale 1/16 (inferfabric_acl.cpp:1400). Limits as the reference: batch 1..64,
+ * slots 1..2^20, context 1..262144. A request whose positions are all masked
+ * gets a zero output. Workspace: ifattn_gated_paged_attention_workspace_size. */
+uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, int64_t context);
+int32_t ifattn_gated_paged_attention_bf16(const void *q, const void *k, const void *v,
+                                          const void *gate, void *keys, void *values,
+                                          const int64_t *append, const int64_t *table,
+                                          const float *mask, void *out, int64_t batch,
+                                          int64_t slots, int64_t context, void *workspace,
+                                          uint64_t workspace_bytes, void *stream);
+
 /* Same over an int8 cache with fp32 scales per (token, kv head), dequantized in
  * registers (replaces cache_dequantize + bf16 attention, token_executor.h:812-822). */
 int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, const void *v_cache,

@@ -1,0 +1,300 @@
+// Gated paged attention over per-token physical indices (the Qwen-shape decode
+// operation of the reference session ABI, inferfabric_acl_paged_attention_prepare:
+// native/include/inferfabric_acl.h:103-113, body native/src/inferfabric_acl.cpp:1343-1430).
+//
+// Per request b (batch <= 64), q head h (8 heads over 2 kv heads, kh = h / 4),
+// head_dim 256, scale 1/16:
+//   keys[append[b]] = k[b], values[append[b]] = v[b]           (the step's row)
+//   s_j  = scale * q[b,h] . keys[table[b,j], kh] + mask[b,j]    j < context
+//   out  = (sum_j softmax(s)_j values[table[b,j], kh]) * gate[b,h]
+// The table holds one physical token row per context position (int64), the
+// mask is fp32 and additive, and the gate buffer holds the gate the preceding
+// operation produced (its sigmoid, inferfabric_acl.cpp:1335-1340), applied as a
+// product. Accumulation is fp32 (scores, softmax, PV); the reference rounds
+// scores and probabilities to bf16 between its ACLNN calls.
+//
+// Kernel: one wave per (request, kv head, 1024-position partition). The wave
+// reads 64 (mask, index) pairs at a time, one per lane, and compacts the
+// positions that can contribute (mask not -inf, index in range) into an LDS
+// list by ballot; masked positions cost 12 bytes of metadata and no cache
+// traffic. Live rows are processed 16 at a time: QK^T as MFMA 16x16x32 bf16
+// (A = the 16 rows' K slices straight from HBM, B = the group's four q heads),
+// the score tile feeding PV directly as the B operand of MFMA 16x16x16 (A = V
+// rows, 32 bytes of dims per lane and row), online softmax in the exp2 domain.
+// Requests over several partitions write (m, l, O) partials that a merge
+// launch combines and gates.
+#include "common.h"
+#include "ifattn_internal.h"
+
+namespace ifattn {
+namespace {
+
+constexpr int kD = 256;           // head_dim
+constexpr int kGroup = 4;         // q heads per kv head
+constexpr int kKvHeads = 2;
+constexpr int kHeads = kGroup * kKvHeads;
+constexpr int kRowBytes = kKvHeads * kD * 2;  // 1024 B per cache row
+constexpr int kPart = 1024;       // context positions per partition
+constexpr float kScale = 0.0625f; // 1/sqrt(256), inferfabric_acl.cpp:1400
+
+struct GatedParams {
+  const uint16_t *q, *gate;
+  const uint8_t *keys, *values;
+  const int64_t *table;
+  const float *mask;
+  uint16_t *out;
+  float *part_o;   // [batch, parts, heads, D]
+  float *part_ml;  // [batch, parts, heads, 2]
+  int64_t slots;
+  int context, parts;
+};
+
+__global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
+  __shared__ uint32_t s_row[64];
+  __shared__ float s_mask[64];
+  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
+  const bool head_live = c < kGroup;
+  const int head = kvh * kGroup + c;
+  // q as the B operand of QK^T: k-step s, lane group g holds dims 32s + 8g .. +7.
+  u32x4 qv[kD / 32];
+  {
+    const uint16_t *qr = p.q + (int64_t(b) * kHeads + (head_live ? head : 0)) * kD;
+#pragma unroll
+    for (int s = 0; s < kD / 32; ++s)
+      qv[s] = head_live ? load_u32x4(qr + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+  // Whole caches as buffers: rows are < 2^20, so byte offsets fit 32 bits.
+  const auto rk = make_rsrc(p.keys + kvh * kD * 2, uint32_t(p.slots) * kRowBytes);
+  const auto rv = make_rsrc(p.values + kvh * kD * 2, uint32_t(p.slots) * kRowBytes);
+  const float sl2 = kScale * kLog2e;
+
+  f32x4 oacc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) oacc[i] = f32x4{0, 0, 0, 0};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  const int t_begin = part * kPart;
+  const int t_end = t_begin + kPart < p.context ? t_begin + kPart : p.context;
+  const int64_t meta = int64_t(b) * p.context;
+  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+    const int t = t0 + lane;
+    bool live = false;
+    int64_t row = 0;
+    float mk = -INFINITY;
+    if (t < t_end) {
+      mk = p.mask[meta + t];
+      row = p.table[meta + t];
+      live = mk != -INFINITY && row >= 0 && row < p.slots;
+    }
+    const uint64_t ballot = __ballot(live);
+    const int n_live = __popcll(ballot);
+    if (n_live == 0) continue;
+    if (live) {
+      const int at = __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u));
+      s_row[at] = uint32_t(row);
+      s_mask[at] = mk * kLog2e;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    for (int k0 = 0; k0 < n_live; k0 += 16) {
+      // K: lane (c, g) loads row k0 + c, dims 32s + 8g .. +7 for every k-step.
+      const bool kl = k0 + c < n_live;
+      const uint32_t krow = kl ? s_row[k0 + c] : 0u;
+      u32x4 kv[kD / 32];
+#pragma unroll
+      for (int s = 0; s < kD / 32; ++s) kv[s] = buf_load_x4(rk, krow * kRowBytes + 64 * s + 16 * g);
+      // V: lane (c, g) loads rows k0 + 4g + j, dims 16c .. 16c + 15 (32 bytes).
+      uint32_t vw[4][8];
+      float xm[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = k0 + 4 * g + j;
+        const bool vl = e < n_live;
+        const uint32_t vrow = vl ? s_row[e] : 0u;
+        xm[j] = vl ? s_mask[e] : -INFINITY;
+        const u32x4 a = buf_load_x4(rv, vrow * kRowBytes + 32 * c);
+        const u32x4 z = buf_load_x4(rv, vrow * kRowBytes + 32 * c + 16);
+        // A padded row's probability is 0; zero its V too so no stale value
+        // (NaN or inf) can reach the accumulator.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vw[j][i] = vl ? a[i] : 0u;
+          vw[j][4 + i] = vl ? z[i] : 0u;
+        }
+      }
+      f32x4 sacc = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < kD / 32; ++s) sacc = mfma16x16x32(kv[s], qv[s], sacc);
+      // Lane (c, g) holds the scores of rows k0 + 4g + r for head c.
+      float x[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = sacc[r] * sl2 + xm[r];
+      float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      tmax = max_xor16(tmax);
+      tmax = max_xor32(tmax);
+      if (tmax > m_run) {
+        const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax);
+        m_run = tmax;
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[i] *= alpha;
+      }
+      float pr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pr[r] = m_run == -INFINITY ? 0.0f : fast_exp2(x[r] - m_run);
+      l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      const u32x2 pb = u32x2{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])};
+      // PV: MFMA d gives O^T rows m = c <-> dim 16c + d for the lane's head.
+#pragma unroll
+      for (int d = 0; d < 16; ++d) {
+        const int w = d >> 1;
+        const u32x2 a = (d & 1) ? u32x2{pack_hi16(vw[0][w], vw[1][w]), pack_hi16(vw[2][w], vw[3][w])}
+                                : u32x2{pack_lo16(vw[0][w], vw[1][w]), pack_lo16(vw[2][w], vw[3][w])};
+        oacc[d] = mfma16x16x16(a, pb, oacc[d]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the list is rewritten by the next chunk
+  }
+  float l_tot = sum_xor16(l_run);
+  l_tot = sum_xor32(l_tot);
+  if (!head_live) return;
+  // Lane (c, g) holds dims (4g + r) * 16 + d = 64g .. 64g + 63 of head c.
+  if (p.parts == 1) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int64_t o = (int64_t(b) * kHeads + head) * kD + 64 * g;
+    const uint16_t *gp = p.gate + o;
+    uint16_t *op = p.out + o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {  // 8 dims per 16-byte store
+      const u32x4 gw = load_u32x4(gp + 8 * k);
+      u32x4 w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e0 = 8 * k + 2 * i, e1 = e0 + 1;
+        const float v0 = oacc[e0 & 15][e0 >> 4] * inv * bf16_bits_to_f32(gw[i] & 0xffffu);
+        const float v1 = oacc[e1 & 15][e1 >> 4] * inv * bf16_bits_to_f32(gw[i] >> 16);
+        w[i] = pack_bf16x2(v0, v1);
+      }
+      store_u32x4(op + 8 * k, w);
+    }
+  } else {
+    const int64_t prow = (int64_t(b) * p.parts + part) * kHeads + head;
+    float *po = p.part_o + prow * kD + 64 * g;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      f32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * k + i;
+        v[i] = oacc[e & 15][e >> 4];
+      }
+      *reinterpret_cast<f32x4 *>(po + 4 * k) = v;
+    }
+    if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
+  }
+}
+
+// One wave per (request, head): combine the partitions' (m, l, O), normalise,
+// apply the gate. Lane l owns dims 4l .. 4l + 3.
+__global__ __launch_bounds__(64) void gated_merge_kernel(GatedParams p) {
+  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+  const int64_t base = int64_t(b) * p.parts * kHeads + h;
+  float mmax = -INFINITY;
+  for (int k = lane; k < p.parts; k += 64) mmax = fmaxf(mmax, p.part_ml[(base + int64_t(k) * kHeads) * 2]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+  f32x4 acc = f32x4{0, 0, 0, 0};
+  float lsum = 0.0f;
+  if (mmax != -INFINITY) {
+    for (int k = 0; k < p.parts; ++k) {
+      const int64_t r = base + int64_t(k) * kHeads;
+      const float m = p.part_ml[r * 2];
+      if (m == -INFINITY) continue;
+      const float w = fast_exp2(m - mmax);
+      lsum += w * p.part_ml[r * 2 + 1];
+      acc += w * *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane);
+    }
+  }
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  const int64_t o = (int64_t(b) * kHeads + h) * kD + 4 * lane;
+  const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o);
+  *reinterpret_cast<u32x2 *>(p.out + o) =
+      u32x2{pack_bf16x2(acc[0] * inv * bf16_bits_to_f32(gw[0] & 0xffffu),
+                        acc[1] * inv * bf16_bits_to_f32(gw[0] >> 16)),
+            pack_bf16x2(acc[2] * inv * bf16_bits_to_f32(gw[1] & 0xffffu),
+                        acc[3] * inv * bf16_bits_to_f32(gw[1] >> 16))};
+}
+
+// The step's K/V rows: keys[append[b]] = k[b] (1024 B), the same for values.
+__global__ __launch_bounds__(256) void gated_append_kernel(const uint8_t *k, const uint8_t *v,
+                                                           uint8_t *keys, uint8_t *values,
+                                                           const int64_t *append, int batch,
+                                                           int64_t slots) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte vector
+  constexpr int kVecs = kRowBytes / 16;
+  if (i >= batch * kVecs * 2) return;
+  const bool val = i >= batch * kVecs;
+  const int j = val ? i - batch * kVecs : i;
+  const int r = j / kVecs, c = j % kVecs;
+  const int64_t slot = append[r];
+  if (slot < 0 || slot >= slots) return;
+  store_u32x4((val ? values : keys) + (slot * kVecs + c) * 16,
+              load_u32x4((val ? v : k) + (int64_t(r) * kVecs + c) * 16));
+}
+
+int parts_for(int64_t context) { return int((context + kPart - 1) / kPart); }
+
+}  // namespace
+}  // namespace ifattn
+
+using namespace ifattn;
+
+extern "C" uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, int64_t context) {
+  if (batch <= 0 || context <= 0) return 0;
+  const uint64_t parts = uint64_t(parts_for(context));
+  if (parts == 1) return 16;
+  return uint64_t(batch) * parts * kHeads * (kD + 2) * sizeof(float);
+}
+
+extern "C" int32_t ifattn_gated_paged_attention_bf16(
+    const void *q, const void *k, const void *v, const void *gate, void *keys, void *values,
+    const int64_t *append, const int64_t *table, const float *mask, void *out, int64_t batch,
+    int64_t slots, int64_t context, void *workspace, uint64_t workspace_bytes, void *stream) {
+  if (batch <= 0 || batch > 64 || slots <= 0 || slots > 1048576 || context <= 0 ||
+      context > 262144)
+    return fail(IFATTN_EINVAL, "gated paged attention: batch 1..64, slots 1..2^20, context 1..262144");
+  if (!q || !k || !v || !gate || !keys || !values || !append || !table || !mask || !out)
+    return fail(IFATTN_EINVAL, "gated paged attention: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(gate) || !aligned16(keys) ||
+      !aligned16(values) || !aligned16(out) || !aligned8(append) || !aligned8(table) ||
+      !aligned4(mask))
+    return fail(IFATTN_EINVAL, "gated paged attention: misaligned tensor");
+  const uint64_t need = ifattn_gated_paged_attention_workspace_size(batch, context);
+  GatedParams p{};
+  p.q = static_cast<const uint16_t *>(q);
+  p.gate = static_cast<const uint16_t *>(gate);
+  p.keys = static_cast<const uint8_t *>(keys);
+  p.values = static_cast<const uint8_t *>(values);
+  p.table = table;
+  p.mask = mask;
+  p.out = static_cast<uint16_t *>(out);
+  p.slots = slots;
+  p.context = int(context);
+  p.parts = parts_for(context);
+  if (p.parts > 1) {
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+      return fail(IFATTN_EWORKSPACE, "gated paged attention: workspace missing, short or misaligned");
+    p.part_o = static_cast<float *>(workspace);
+    p.part_ml = p.part_o + uint64_t(batch) * p.parts * kHeads * kD;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int vecs = int(batch) * (kRowBytes / 16) * 2;
+  gated_append_kernel<<<(vecs + 255) / 256, 256, 0, s>>>(
+      static_cast<const uint8_t *>(k), static_cast<const uint8_t *>(v),
+      static_cast<uint8_t *>(keys), static_cast<uint8_t *>(values), append, int(batch), slots);
+  gated_decode_kernel<<<dim3(p.parts, kKvHeads, unsigned(batch)), 64, 0, s>>>(p);
+  if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 64, 0, s>>>(p);
+  return launch_status("gated paged attention");
+}

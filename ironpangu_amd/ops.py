@@ -226,6 +226,38 @@ def paged_decode_step(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tab
     return out
 
 
+def gated_paged_attention(q, k, v, gate, keys, values, append, table, mask, out=None,
+                          workspace=None, stream=None):
+    """Qwen-shape session attention (inferfabric_acl_paged_attention_prepare):
+    append k/v [batch, 512] at keys/values[append], then attend q [batch, 8, 256]
+    over the per-position rows ``table`` [batch, context] int64 with the fp32
+    additive ``mask`` [batch, context], times ``gate`` [batch, 8, 256]."""
+    _dev(q, k, v, gate, keys, values, append, table, mask, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3 and tuple(q.shape[1:]) == (8, 256),
+         "q: bf16 [batch, 8, 256]")
+    batch = q.shape[0]
+    for t, n in ((k, "k"), (v, "v")):
+        _req(t.dtype == torch.bfloat16 and tuple(t.shape) == (batch, 512), f"{n}: bf16 [batch, 512]")
+    _req(gate.dtype == torch.bfloat16 and gate.shape == q.shape, "gate: bf16 like q")
+    _req(keys.dtype == torch.bfloat16 and keys.dim() == 2 and keys.shape[1] == 512
+         and values.shape == keys.shape and values.dtype == keys.dtype, "caches: bf16 [slots, 512]")
+    _req(append.dtype == torch.int64 and append.numel() == batch, "append: int64 [batch]")
+    _req(table.dtype == torch.int64 and table.dim() == 2 and table.shape[0] == batch,
+         "table: int64 [batch, context]")
+    _req(mask.dtype == torch.float32 and mask.shape == table.shape, "mask: fp32 [batch, context]")
+    context = table.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    if workspace is None:
+        n = lib().ifattn_gated_paged_attention_workspace_size(batch, context)
+        workspace = torch.empty(max(int(n), 16), dtype=torch.uint8, device=q.device)
+    check(lib().ifattn_gated_paged_attention_bf16(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(keys), _ptr(values), _ptr(append), _ptr(table),
+        _ptr(mask), _ptr(out), batch, keys.shape[0], context, _ptr(workspace), workspace.numel(),
+        _stream(stream)), "ifattn_gated_paged_attention_bf16")
+    return out
+
+
 # ---------------------------------------------------------------- varlen prefill
 
 def prefill_workspace(num_seqs, total_q, q_heads, head_dim, max_kv_len, device="cuda"):

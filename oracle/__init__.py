@@ -46,10 +46,12 @@ def lib():
         l.oracle_mla_decode.argtypes = [vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, f32, i32]
         l.oracle_mla_attention.argtypes = [vp, vp, i32, vp, i32, vp, vp, i32, i32, vp, i32, i32,
                                            vp, vp, i32, vp, i32, i32, f32, i32]
+        l.oracle_gated_attention.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32,
+                                             f32, i32]
         l.oracle_hardware_threads.restype = i32
         for f in ("oracle_kv_write", "oracle_quant_rows", "oracle_quant_legacy",
                   "oracle_dequant_legacy", "oracle_mla_pack_c8", "oracle_mla_norm_rope_write",
-                  "oracle_paged_decode",
+                  "oracle_paged_decode", "oracle_gated_attention",
                   "oracle_varlen_prefill", "oracle_mla_decode", "oracle_mla_attention"):
             getattr(l, f).restype = None
         _lib = l
@@ -204,4 +206,22 @@ def mla_attention(q, cache, block_tables, kv_lens, heads, block_size, scale, c8=
     lib().oracle_mla_attention(_p(q), _p(cache), int(c8), _p(tables), tables.shape[1], _p(cu),
                                _p(kv), kv.size, rows, _p(idx), topk, int(window), _p(sk), _p(sv),
                                ns, _p(out), heads, block_size, float(scale), threads)
+    return out
+
+
+def gated_attention(q, keys, values, table, mask, gate, hq=8, hkv=2, d=256, scale=0.0625,
+                    threads=0):
+    """fp32 [batch, hq, d]: softmax(q.K[table]*scale + mask) V[table], times gate.
+    q/gate bf16 bits [batch, hq, d]; keys/values bf16 bits [slots, hkv*d];
+    table int64, mask fp32 [batch, context]."""
+    q = _c(q, np.uint16)
+    keys = _c(keys, np.uint16)
+    values = _c(values, np.uint16)
+    table = _c(table, np.int64)
+    mask = _c(mask, np.float32)
+    gate = _c(gate, np.uint16)
+    batch, context = table.shape
+    out = np.zeros((batch, hq, d), np.float32)
+    lib().oracle_gated_attention(_p(q), _p(keys), _p(values), _p(table), _p(mask), _p(gate),
+                                 _p(out), batch, context, hq, hkv, d, float(scale), threads)
     return out

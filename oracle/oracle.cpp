@@ -28,6 +28,10 @@
 //                          mode that keeps the Rust oracle's roundings. Pinned: closed
 //                          forms (q = 0 mean, constant-per-head V, two-token softmax),
 //                          sequence_attention_probe.cpp:26-27,100 known answer.
+//   oracle_gated_attention the Qwen session operation, inferfabric_acl.cpp:1343-1430.
+//                          Pinned: equality with oracle_paged_decode when the mask opens
+//                          a prefix (gate 1), mask-shift invariance, gate linearity,
+//                          a two-position closed form with mask and gate.
 //   oracle_varlen_prefill  causal rule of openpangu_attention_metadata.h:20-22.
 //                          Pinned: q = 0 causal prefix means, decode-row equivalence.
 //   oracle_mla_decode      packed_cache_probe.cpp:47-66 / sliding_window_probe.cpp:144-163
@@ -299,6 +303,55 @@ void oracle_paged_decode(const uint16_t *q, const void *k_cache, const void *v_c
         o[e] = acc;
       }
     }
+  });
+}
+
+// Qwen-shape gated attention over per-position physical rows
+// (inferfabric_acl_paged_attention_prepare, native/src/inferfabric_acl.cpp:1343-1430:
+// scatter of the step's K/V rows, gather by `table`, scores * scale + additive
+// fp32 mask, fp32 softmax, PV, product with the gate). Caches [slots, hkv*d]
+// bf16; q/gate/out [batch, hq, d]; table int64 and mask fp32 [batch, context].
+// The caches must already hold the step's rows (apply oracle_kv_write first).
+// fp32 throughout (no bf16 rounding between the steps). A request whose mask is
+// -inf everywhere gets zeros (the reference's softmax would give NaN).
+void oracle_gated_attention(const uint16_t *q, const uint16_t *keys, const uint16_t *values,
+                            const int64_t *table, const float *mask, const uint16_t *gate,
+                            float *out, int32_t batch, int32_t context, int32_t hq, int32_t hkv,
+                            int32_t d, float scale, int32_t threads) {
+  const int group = hq / hkv;
+  parallel_for(int64_t(batch) * hq, default_threads(threads), [&](int64_t unit) {
+    const int b = int(unit / hq), h = int(unit % hq), kh = h / group;
+    const uint16_t *qh = q + (int64_t(b) * hq + h) * d;
+    std::vector<float> s(context);
+    float mx = -INFINITY;
+    for (int j = 0; j < context; ++j) {
+      const float m = mask[int64_t(b) * context + j];
+      if (m == -INFINITY) {
+        s[j] = -INFINITY;
+        continue;
+      }
+      const int64_t row = table[int64_t(b) * context + j];
+      float acc = 0.0f;
+      for (int e = 0; e < d; ++e) acc += bf(qh[e]) * bf(keys[(row * hkv + kh) * d + e]);
+      s[j] = acc * scale + m;
+      mx = std::max(mx, s[j]);
+    }
+    float *o = out + (int64_t(b) * hq + h) * d;
+    std::fill(o, o + d, 0.0f);
+    if (mx == -INFINITY) return;
+    float sum = 0.0f;
+    for (int j = 0; j < context; ++j) {
+      s[j] = s[j] == -INFINITY ? 0.0f : std::exp(s[j] - mx);
+      sum += s[j];
+    }
+    for (int j = 0; j < context; ++j) {
+      if (s[j] == 0.0f) continue;
+      const int64_t row = table[int64_t(b) * context + j];
+      const float p = s[j] / sum;
+      for (int e = 0; e < d; ++e) o[e] += p * bf(values[(row * hkv + kh) * d + e]);
+    }
+    const uint16_t *gh = gate + (int64_t(b) * hq + h) * d;
+    for (int e = 0; e < d; ++e) o[e] *= bf(gh[e]);
   });
 }
 

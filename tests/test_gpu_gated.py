@@ -1,0 +1,95 @@
+"""GPU parity for the Qwen-shape gated attention (ifattn_gated_paged_attention_bf16,
+the operation of inferfabric_acl_paged_attention_prepare,
+native/src/inferfabric_acl.cpp:1343-1430) against oracle_gated_attention:
+appended rows bit-exact, outputs within 1e-2 abs + 1e-2 rel and relative L2."""
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_close, assert_rel_l2, bf16_host, bits_host, to_dev
+from ironpangu_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 8, 2, 256
+
+
+def _run(seed, batch, context, slots, holes=0.0, finite_mask=False):
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, context + 1, batch)
+    lens[0] = context
+    # every position of every request gets its own physical row (random order);
+    # the step's new row is the request's last live position
+    rows = rng.permutation(slots)[: batch * context].reshape(batch, context).astype(np.int64)
+    pos = np.arange(context)
+    live = pos[None, :] < lens[:, None]
+    if holes:
+        live &= ~((rng.random((batch, context)) < holes) & (pos[None, :] < lens[:, None] - 1))
+    mask = np.where(live, 0.0, -np.inf).astype(np.float32)
+    if finite_mask:  # finite additive biases on live positions
+        mask = np.where(live, rng.uniform(-4, 1, (batch, context)), -np.inf).astype(np.float32)
+    append = rows[np.arange(batch), lens - 1].copy()
+    keys = W.bf16_randn(rng, (slots, HKV * D))
+    values = W.bf16_randn(rng, (slots, HKV * D))
+    q = W.bf16_randn(rng, (batch, HQ, D))
+    k = W.bf16_randn(rng, (batch, HKV * D))
+    v = W.bf16_randn(rng, (batch, HKV * D))
+    gate = W.bf16_bits(1.0 / (1.0 + np.exp(-rng.standard_normal((batch, HQ, D)).astype(np.float32))))
+    kd, vd = to_dev(keys), to_dev(values)
+    out = ops.gated_paged_attention(to_dev(q), to_dev(k), to_dev(v), to_dev(gate), kd, vd,
+                                    to_dev(append), to_dev(rows), to_dev(mask))
+    torch.cuda.synchronize()
+    oracle.kv_write(k, keys, append)
+    oracle.kv_write(v, values, append)
+    assert np.array_equal(bits_host(kd), keys), "appended K rows not bit-exact"
+    assert np.array_equal(bits_host(vd), values), "appended V rows not bit-exact"
+    exp = oracle.gated_attention(q, keys, values, rows, mask, gate, threads=16)
+    got = bf16_host(out)
+    assert_rel_l2(got, exp, what="gated attention")
+    assert_close(got, exp, what="gated attention")
+
+
+@pytest.mark.parametrize("batch,context,holes,finite", [(3, 700, 0.0, False),     # one partition
+                                                        (7, 3000, 0.0, False),    # three partitions
+                                                        (5, 2500, 0.3, True),     # holes + biases
+                                                        (64, 129, 0.5, False)])   # batch 64
+def test_gated_attention(batch, context, holes, finite):
+    _run(batch * 1000 + context, batch, context, batch * context + 17, holes, finite)
+
+
+def test_gated_attention_long_context():
+    # 4 requests over 65536 positions (64 partitions, merged), 2^18 + 3 slots
+    _run(42, 4, 65536, (1 << 18) + 3)
+
+
+def test_gated_attention_all_masked_request_is_zero():
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(5)
+    batch, context, slots = 2, 1500, 4000
+    keys = to_dev(W.bf16_randn(rng, (slots, 512)))
+    values = to_dev(W.bf16_randn(rng, (slots, 512)))
+    q = to_dev(W.bf16_randn(rng, (batch, 8, 256)))
+    kv = to_dev(W.bf16_randn(rng, (batch, 512)))
+    gate = to_dev(W.bf16_bits(np.ones((batch, 8, 256), np.float32)))
+    rows = to_dev(rng.integers(0, slots, (batch, context)).astype(np.int64))
+    mask = np.zeros((batch, context), np.float32)
+    mask[1] = -np.inf
+    out = ops.gated_paged_attention(q, kv, kv, gate, keys, values,
+                                    to_dev(np.array([0, 1], np.int64)), rows, to_dev(mask))
+    torch.cuda.synchronize()
+    o = bf16_host(out)
+    assert np.all(o[1] == 0) and np.isfinite(o).all() and np.abs(o[0]).sum() > 0
+
+
+def test_gated_attention_rejects_limits():
+    import torch
+    from ironpangu_amd._native import IfattnError
+    from ironpangu_amd import ops
+    z = lambda *s, dt=torch.bfloat16: torch.zeros(*s, dtype=dt, device="cuda")
+    with pytest.raises(IfattnError):  # batch 65 > 64
+        ops.gated_paged_attention(z(65, 8, 256), z(65, 512), z(65, 512), z(65, 8, 256), z(8, 512),
+                                  z(8, 512), z(65, dt=torch.int64), z(65, 4, dt=torch.int64),
+                                  z(65, 4, dt=torch.float32))
