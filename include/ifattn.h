@@ -39,6 +39,10 @@ extern "C" {
 #define IFATTN_DTYPE_I32 4
 #define IFATTN_DTYPE_I64 5
 
+/* Version of this direct ifattn_* C ABI (functions, argument lists, status
+ * codes). It is raised only by an incompatible change; added entry points keep
+ * it. It is unrelated to the IFKernelV1 plug-in table's abi_version (1 or 2,
+ * chosen per call by requested_version; see inferfabric_kernel_v1.h). */
 #define IFATTN_ABI_VERSION 1
 
 int32_t ifattn_abi_version(void);

@@ -6,14 +6,26 @@
  * can dlopen these libraries unchanged. Interface declarations have to match
  * field for field; the text here is this project's own.
  *
- * Additive extension, reported as abi_version 2 (the same struct):
- *   dtype  4 = I32, 5 = I64   (block tables, slot mappings, cu_seqlens)
- *   access 3 = read + write   (caches updated in place by the write operators)
- * Every operator here needs at least one of these, so
- * inferfabric_kernel_v1(1) returns NULL and inferfabric_kernel_v1(2) returns the
- * table. The contract string fixes the semantics, including the softmax scale
- * (1/sqrt(head_dim) for GQA, 1/sqrt(192) for MLA) since the ABI carries no
- * scalars. target is "gfx950". stream is a hipStream_t passed as void*.
+ * Two versions of every operator, chosen by requested_version:
+ *
+ *   abi_version 1 -- the reference loader's version (it calls
+ *     inferfabric_kernel_v1(1) and requires abi_version == 1). Contract names
+ *     end in ".v1". Only the reference's dtypes (I8, BF16, F32) and accesses
+ *     (read, write) appear: every integer port (block tables, lengths,
+ *     cu_seqlens, index lists: int32; slot mappings: int64) is an I8 tensor
+ *     holding the little-endian integers, its last extent 4x (int32) or 8x
+ *     (int64) the integer count. Caches that a write operator updates in place
+ *     are outputs with write access: the operator writes the rows the slot
+ *     mapping names and leaves every other row as it was.
+ *   abi_version 2 -- the same struct with dtype 4 = I32, 5 = I64 and access
+ *     3 = read + write. Contract names end in ".v2".
+ *
+ * The gated Qwen-shape attention reads the caches it appends to, which version
+ * 1 cannot express (outputs must not alias inputs); it exists as ".v2" only.
+ * The contract string fixes the semantics, including the softmax scale
+ * (1/sqrt(head_dim) for GQA, 1/sqrt(192) for MLA, 1/16 for the gated
+ * attention) since the ABI carries no scalars. target is "gfx950". stream is
+ * a hipStream_t passed as void*.
  *
  * prepare validates every descriptor and allocates only host state; enqueue
  * launches the kernels asynchronously on `stream`, allocates nothing, never
@@ -99,13 +111,22 @@ typedef const IFKernelV1 *(*IFKernelEntryV1)(uint32_t requested_version);
  *   libifk_mla_sparse_attention_c8 "inferfabric.mla_sparse_attention.c8.v2"
  *       q, cache I8 [blocks, block_size, 656], indices I32 [rows, topk], block_tables,
  *       cu_seqlens_q, kv_lens, sink_keys, sink_values ; out bf16 [rows, heads, 512]
+ *   libifk_paged_attention_qwen_gated_bf16 "inferfabric.paged_attention.qwen_gated.bf16.v2"
+ *       q bf16 [batch <= 64, 8, 256], k, v bf16 [batch, 512], gate bf16 [batch, 8, 256],
+ *       append I64 [batch], table I64 [batch, context], mask F32 [batch, context] ;
+ *       keys, values bf16 [slots, 512] (access 3), out bf16 [batch, 8, 256]
+ *       (inferfabric_acl_paged_attention_prepare, native/src/inferfabric_acl.cpp:1343-1430)
+ * Every contract above except the gated attention also answers version 1
+ * under the same name with ".v1" (integer ports as I8 byte views).
  * Attention contracts use scale 1/sqrt(192) for MLA and 1/sqrt(head_dim) for GQA.
  * max_context is entries * block_size of the block-table descriptor.
  */
 
-/* Lookup by contract name inside libifattn_hip.so (the per-operator libraries
- * forward to it). NULL for unknown contracts or unsupported versions. */
+/* Lookup by contract name ("...v1" with version 1, "...v2" with version 2)
+ * inside libifattn_hip.so. NULL for unknown contracts or unsupported versions. */
 const IFKernelV1 *ifattn_kernel_v1_contract(const char *contract, uint32_t requested_version);
+/* Lookup by operator index (the per-operator libraries forward here). */
+const IFKernelV1 *ifattn_kernel_v1_operator(int32_t index, uint32_t requested_version);
 
 #ifdef __cplusplus
 }

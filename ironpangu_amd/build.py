@@ -51,6 +51,7 @@ PLUGINS = {
     "mla_window_attention_w512_bf16": 10,
     "mla_window_attention_w2048_bf16": 11,
     "mla_sparse_attention_c8": 12,
+    "paged_attention_qwen_gated_bf16": 13,
 }
 
 

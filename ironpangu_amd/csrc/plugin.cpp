@@ -1,4 +1,7 @@
-// IFKernelV1-layout operator plug-ins (abi_version 2) over the ifattn C ABI.
+// IFKernelV1-layout operator plug-ins over the ifattn C ABI, in two versions:
+// abi_version 1 (the reference loader's: I8/BF16/F32 only, integer ports as I8
+// byte views, in-place caches declared write-only) and abi_version 2 (I32/I64
+// dtypes and read-write access).
 // prepare: descriptor validation in the manner of the reference loader
 // (native/src/compiled_kernel.cpp:20-41,71-83) plus per-contract shape checks,
 // host state only. enqueue: one call into the launchers, no allocation, no
@@ -28,6 +31,7 @@ enum Op : int {
   kMlaWindow512,
   kMlaWindow2048,
   kMlaSparseC8,
+  kGatedBf16,
   kOpCount
 };
 
@@ -40,12 +44,52 @@ const char *const kContract[kOpCount] = {
     "inferfabric.mla_window_attention.w512.bf16.v2",
     "inferfabric.mla_window_attention.w2048.bf16.v2",
     "inferfabric.mla_sparse_attention.c8.v2",
+    "inferfabric.paged_attention.qwen_gated.bf16.v2",
+};
+// The same operators under abi_version 1 (the reference loader's version):
+// contract names end in ".v1" and integer ports travel as I8 byte views.
+const char *const kContractV1[kOpCount] = {
+    "inferfabric.kv_cache_write.bf16.v1",   "inferfabric.kv_cache_write.c8.v1",
+    "inferfabric.paged_decode.gqa.bf16.v1", "inferfabric.paged_decode.gqa.c8.v1",
+    "inferfabric.varlen_prefill.bf16.v1",   "inferfabric.mla_decode.bf16.v1",
+    "inferfabric.mla_decode.c8.v1",         "inferfabric.mla_cache_write.c8.v1",
+    "inferfabric.mla_norm_rope_cache.bf16.v1", "inferfabric.mla_norm_rope_cache.c8.v1",
+    "inferfabric.mla_window_attention.w512.bf16.v1",
+    "inferfabric.mla_window_attention.w2048.bf16.v1",
+    "inferfabric.mla_sparse_attention.c8.v1",
+    nullptr,  // reads and writes its caches in one call: no version-1 form
 };
 constexpr const char *kTarget = "gfx950";
 
+// Version-1 port map of each operator: input ports that carry integers (an I8
+// byte view whose last extent is 4x the int32 extent, or 8x for the int64 slot
+// mappings) and output ports that the operator updates in place (declared
+// write-only in version 1: the operator writes the mapped rows and reads
+// nothing else of them).
+struct PortMap {
+  uint8_t int32_inputs, int64_inputs;  // bit i = input port i
+  uint8_t in_place_outputs;            // bit i = output port i
+};
+constexpr PortMap kPorts[kOpCount] = {
+    {0x00, 0x04, 0x03},  // kv write bf16: slots ; k, v caches
+    {0x00, 0x04, 0x0f},  // kv write c8: slots ; caches and scales
+    {0x18, 0x00, 0x00},  // decode bf16: tables, lengths
+    {0x60, 0x00, 0x00},  // decode c8
+    {0x38, 0x00, 0x00},  // prefill: tables, cu_seqlens, kv_lens
+    {0x0c, 0x00, 0x00},  // mla decode bf16
+    {0x0c, 0x00, 0x00},  // mla decode c8
+    {0x00, 0x02, 0x01},  // mla c8 row write
+    {0x00, 0x10, 0x01},  // norm/rope writer bf16
+    {0x00, 0x10, 0x01},  // norm/rope writer c8
+    {0x1c, 0x00, 0x00},  // window 512
+    {0x1c, 0x00, 0x00},  // window 2048
+    {0x3c, 0x00, 0x00},  // sparse: indices, tables, cu_seqlens, kv_lens
+    {0x00, 0x00, 0x00},
+};
+
 struct State {
   int op;
-  IFKernelTensorV1 inputs[8], outputs[4];
+  IFKernelTensorV1 inputs[8], outputs[4];  // as version 2 sees them
   uint64_t workspace;
   int32_t slot_dtype;
   int64_t rows, row_bytes, num_slots, num_blocks;
@@ -318,12 +362,80 @@ void prepare_op(State &s, const IFKernelTensorV1 *in, uint32_t nin, const IFKern
                                                         s.topk, s.n_sinks, s.block_size);
       return;
     }
+    case kGatedBf16: {
+      require(nin == 7 && nout == 3, "gated attention: 7 inputs, 3 outputs");
+      check_tensor(in[0], BF, R, 3);
+      require(in[0].shape[1] == 8 && in[0].shape[2] == 256, "q must be [batch, 8, 256]");
+      s.n = int32_t(in[0].shape[0]);
+      require(s.n <= 64, "batch must be 1..64");
+      check_tensor(in[1], BF, R, 2);
+      check_tensor(in[2], BF, R, 2);
+      require(in[1].shape[0] == s.n && in[1].shape[1] == 512 && same_shape(in[1], in[2]),
+              "k, v rows must be [batch, 512]");
+      check_tensor(in[3], BF, R, 3);
+      require(same_shape(in[3], in[0]), "gate must match q");
+      check_tensor(in[4], IF_KERNEL_DTYPE_I64, R, 1);
+      require(in[4].shape[0] == s.n, "append must be [batch]");
+      check_tensor(in[5], IF_KERNEL_DTYPE_I64, R, 2);
+      check_tensor(in[6], F32, R, 2);
+      require(in[5].shape[0] == s.n && same_shape(in[5], in[6]),
+              "table (I64) and mask (F32) must be [batch, context]");
+      s.max_ctx = int32_t(in[5].shape[1] <= 262144 ? in[5].shape[1] : 0);
+      require(s.max_ctx > 0, "context must be 1..262144");
+      check_tensor(out[0], BF, RW, 2);
+      check_tensor(out[1], BF, RW, 2);
+      require(out[0].shape[1] == 512 && same_shape(out[0], out[1]) && out[0].shape[0] <= 1048576,
+              "keys, values must be [slots <= 2^20, 512]");
+      s.num_slots = out[0].shape[0];
+      check_tensor(out[2], BF, W, 3);
+      require(same_shape(out[2], in[0]), "out must match q");
+      s.workspace = ifattn_gated_paged_attention_workspace_size(s.n, s.max_ctx);
+      return;
+    }
     default:
       require(false, "unknown operator");
   }
 }
 
-template <int OP>
+// Version-1 descriptors -> the version-2 view prepare_op checks: integer byte
+// views become I32/I64 tensors, in-place caches become read-write.
+void widen_v1(int op, const IFKernelTensorV1 *in, uint32_t nin, const IFKernelTensorV1 *out,
+              uint32_t nout, IFKernelTensorV1 *in2, IFKernelTensorV1 *out2) {
+  const PortMap &m = kPorts[op];
+  for (uint32_t i = 0; i < nin; ++i) {
+    in2[i] = in[i];
+    const bool i32 = m.int32_inputs >> i & 1, i64 = m.int64_inputs >> i & 1;
+    require(in[i].dtype != IF_KERNEL_DTYPE_I32 && in[i].dtype != IF_KERNEL_DTYPE_I64 &&
+                in[i].access != IF_KERNEL_ACCESS_READ_WRITE,
+            "version 1 carries no I32/I64 dtypes and no read-write access");
+    if (!i32 && !i64) continue;
+    require(in[i].dtype == IF_KERNEL_DTYPE_I8 && in[i].rank >= 1 && in[i].rank <= 8,
+            "version 1 integer port: I8 byte view");
+    const int64_t w = i64 ? 8 : 4;
+    const uint32_t last = in[i].rank - 1;
+    require(in[i].shape[last] > 0 && in[i].shape[last] % w == 0,
+            "version 1 integer port: last extent a multiple of the integer size");
+    in2[i].dtype = i64 ? IF_KERNEL_DTYPE_I64 : IF_KERNEL_DTYPE_I32;
+    in2[i].shape[last] = in[i].shape[last] / w;
+    require(in[i].strides[last] == 1, "tensor must be contiguous");
+    int64_t stride = 1;
+    for (uint32_t d = in[i].rank; d-- > 0;) {
+      require(d == last || in[i].strides[d] == in[i].strides[d + 1] * in[i].shape[d + 1],
+              "tensor must be contiguous");
+      in2[i].strides[d] = stride;
+      stride *= in2[i].shape[d];
+    }
+  }
+  for (uint32_t i = 0; i < nout; ++i) {
+    out2[i] = out[i];
+    require(out[i].dtype != IF_KERNEL_DTYPE_I32 && out[i].dtype != IF_KERNEL_DTYPE_I64 &&
+                out[i].access == IF_KERNEL_ACCESS_WRITE,
+            "version 1 outputs: write access, no I32/I64 dtypes");
+    if (m.in_place_outputs >> i & 1) out2[i].access = IF_KERNEL_ACCESS_READ_WRITE;
+  }
+}
+
+template <int OP, int VERSION>
 int32_t prepare(const IFKernelTensorV1 *inputs, uint32_t input_count,
                 const IFKernelTensorV1 *outputs, uint32_t output_count, IFKernelPreparedV1 *out) {
   if (!out) return ifattn::fail(IFATTN_EINVAL, "prepare: null output");
@@ -334,6 +446,11 @@ int32_t prepare(const IFKernelTensorV1 *inputs, uint32_t input_count,
   if (!s) return ifattn::fail(IFATTN_EINVAL, "prepare: host allocation");
   s->op = OP;
   try {
+    if (VERSION == 1) {
+      widen_v1(OP, inputs, input_count, outputs, output_count, s->inputs, s->outputs);
+      inputs = s->inputs;
+      outputs = s->outputs;
+    }
     prepare_op(*s, inputs, input_count, outputs, output_count);
     for (uint32_t i = 0; i < output_count; ++i) {
       for (uint32_t j = 0; j < input_count; ++j)
@@ -344,8 +461,10 @@ int32_t prepare(const IFKernelTensorV1 *inputs, uint32_t input_count,
     delete s;
     return ifattn::fail(IFATTN_EINVAL, r.what);
   }
-  std::memcpy(s->inputs, inputs, sizeof(IFKernelTensorV1) * input_count);
-  std::memcpy(s->outputs, outputs, sizeof(IFKernelTensorV1) * output_count);
+  if (VERSION != 1) {
+    std::memcpy(s->inputs, inputs, sizeof(IFKernelTensorV1) * input_count);
+    std::memcpy(s->outputs, outputs, sizeof(IFKernelTensorV1) * output_count);
+  }
   out->state = s;
   out->workspace_bytes = s->workspace;
   out->workspace_alignment = 256;
@@ -414,6 +533,12 @@ int32_t enqueue(void *state, void *workspace, uint64_t bytes, void *stream) {
           static_cast<const int32_t *>(in[4].data), static_cast<const int32_t *>(in[5].data), s->n,
           s->total_q, in[6].data, in[7].data, s->n_sinks, out[0].data, s->q_heads, s->block_size,
           s->num_blocks, s->max_ctx, s->scale, workspace, bytes, stream);
+    case kGatedBf16:
+      return ifattn_gated_paged_attention_bf16(
+          in[0].data, in[1].data, in[2].data, in[3].data, out[0].data, out[1].data,
+          static_cast<const int64_t *>(in[4].data), static_cast<const int64_t *>(in[5].data),
+          static_cast<const float *>(in[6].data), out[2].data, s->n, s->num_slots, s->max_ctx,
+          workspace, bytes, stream);
     default:
       return ifattn::fail(IFATTN_EINVAL, "enqueue: unknown operator");
   }
@@ -421,22 +546,37 @@ int32_t enqueue(void *state, void *workspace, uint64_t bytes, void *stream) {
 
 void release(void *state) { delete static_cast<State *>(state); }
 
-template <int OP>
+template <int OP, int VERSION>
 IFKernelV1 table() {
-  return IFKernelV1{sizeof(IFKernelV1), 2, kContract[OP], kTarget, &prepare<OP>, &enqueue, &release};
+  return IFKernelV1{sizeof(IFKernelV1), uint32_t(VERSION),
+                    VERSION == 1 ? kContractV1[OP] : kContract[OP], kTarget, &prepare<OP, VERSION>,
+                    &enqueue, &release};
 }
 
-const IFKernelV1 kTables[kOpCount] = {table<0>(),  table<1>(),  table<2>(), table<3>(),
-                                      table<4>(),  table<5>(),  table<6>(), table<7>(),
-                                      table<8>(),  table<9>(),  table<10>(), table<11>(),
-                                      table<12>()};
+template <int... OPS>
+struct Tables {
+  const IFKernelV1 v1[kOpCount] = {table<OPS, 1>()...};
+  const IFKernelV1 v2[kOpCount] = {table<OPS, 2>()...};
+};
+const Tables<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13> kTables;
+static_assert(kOpCount == 14, "one table entry per operator");
 
 }  // namespace
 
 extern "C" const IFKernelV1 *ifattn_kernel_v1_contract(const char *contract,
                                                        uint32_t requested_version) {
-  if (!contract || requested_version != 2) return nullptr;
-  for (int i = 0; i < kOpCount; ++i)
-    if (std::strcmp(contract, kContract[i]) == 0) return &kTables[i];
+  if (!contract || (requested_version != 1 && requested_version != 2)) return nullptr;
+  for (int i = 0; i < kOpCount; ++i) {
+    const char *name = requested_version == 1 ? kContractV1[i] : kContract[i];
+    if (name && std::strcmp(contract, name) == 0)
+      return requested_version == 1 ? &kTables.v1[i] : &kTables.v2[i];
+  }
+  return nullptr;
+}
+
+extern "C" const IFKernelV1 *ifattn_kernel_v1_operator(int32_t index, uint32_t requested_version) {
+  if (index < 0 || index >= kOpCount) return nullptr;
+  if (requested_version == 2) return &kTables.v2[index];
+  if (requested_version == 1 && kContractV1[index]) return &kTables.v1[index];
   return nullptr;
 }

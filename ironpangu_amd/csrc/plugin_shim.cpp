@@ -7,20 +7,10 @@
 #error "IFK_CONTRACT_INDEX must select the operator contract"
 #endif
 
-namespace {
-const char *const kContracts[] = {
-    "inferfabric.kv_cache_write.bf16.v2",   "inferfabric.kv_cache_write.c8.v2",
-    "inferfabric.paged_decode.gqa.bf16.v2", "inferfabric.paged_decode.gqa.c8.v2",
-    "inferfabric.varlen_prefill.bf16.v2",   "inferfabric.mla_decode.bf16.v2",
-    "inferfabric.mla_decode.c8.v2",         "inferfabric.mla_cache_write.c8.v2",
-    "inferfabric.mla_norm_rope_cache.bf16.v2", "inferfabric.mla_norm_rope_cache.c8.v2",
-    "inferfabric.mla_window_attention.w512.bf16.v2",
-    "inferfabric.mla_window_attention.w2048.bf16.v2",
-    "inferfabric.mla_sparse_attention.c8.v2",
-};
-}
+extern "C" const IFKernelV1 *ifattn_kernel_v1_operator(int32_t index, uint32_t requested_version);
 
+// Version 1 (the reference loader's request) or 2; NULL for any other version.
 extern "C" __attribute__((visibility("default"))) const IFKernelV1 *inferfabric_kernel_v1(
     uint32_t requested_version) {
-  return ifattn_kernel_v1_contract(kContracts[IFK_CONTRACT_INDEX], requested_version);
+  return ifattn_kernel_v1_operator(IFK_CONTRACT_INDEX, requested_version);
 }

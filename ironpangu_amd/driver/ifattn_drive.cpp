@@ -207,7 +207,8 @@ int main(int argc, char **argv) {
     if (!h) die(std::string("dlopen ") + file + ": " + dlerror());
     auto entry = reinterpret_cast<IFKernelEntryV1>(dlsym(h, "inferfabric_kernel_v1"));
     if (!entry) die(std::string("no inferfabric_kernel_v1 in ") + file);
-    if (entry(1) != nullptr) die("a version-1 handshake must be refused");
+    const IFKernelV1 *k1 = entry(1);  // the reference loader's request
+    if (!k1 || k1->abi_version != 1) die("version-1 handshake");
     const IFKernelV1 *k = entry(2);
     if (!k || k->abi_version != 2 || std::strcmp(k->target, "gfx950") != 0) die("plug-in handshake");
     return k;

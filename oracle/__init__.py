@@ -18,6 +18,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 _lib = None
 _ref = None
+_loader = None
 
 i32, i64, u32, u64, f32, vp = C.c_int32, C.c_int64, C.c_uint32, C.c_uint64, C.c_float, C.c_void_p
 
@@ -67,6 +68,25 @@ def ref():
             return None
         _ref = C.CDLL(str(path))
     return _ref
+
+
+def ref_loader():
+    """The reference's plug-in loader (native/src/compiled_kernel.cpp) compiled in
+    place behind a C shim, or None where absent."""
+    global _loader
+    if _loader is None:
+        path = HERE / "_ref" / "libref_loader.so"
+        if not path.exists():
+            return None
+        l = C.CDLL(str(path))
+        l.ref_loader_error.restype = C.c_char_p
+        l.ref_loader_open.argtypes = [C.c_char_p, C.c_char_p, C.c_char_p, C.POINTER(vp)]
+        l.ref_loader_close.argtypes = [vp]
+        l.ref_loader_prepare.argtypes = [vp, vp, u32, vp, u32, C.POINTER(vp), C.POINTER(u64)]
+        l.ref_loader_enqueue.argtypes = [vp, vp, u64, vp]
+        l.ref_loader_release.argtypes = [vp]
+        _loader = l
+    return _loader
 
 
 def _p(a):

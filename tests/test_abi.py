@@ -105,11 +105,17 @@ def load_plugin(name):
 @pytest.mark.parametrize("name", sorted(PLUGINS))
 def test_plugin_handshake(name):
     so, entry = load_plugin(name)
-    assert not entry(1), "v1 must be refused: the operator needs I32/I64 or in-place tensors"
     k = entry(2).contents
     assert k.struct_bytes == C.sizeof(KernelV1) == 48  # 2 x u32, 2 strings, 3 function pointers
     assert k.abi_version == 2 and k.target == b"gfx950"
     assert k.contract.decode().startswith("inferfabric.") and k.contract.decode().endswith(".v2")
+    assert not entry(0) and not entry(3)
+    if name == "paged_attention_qwen_gated_bf16":
+        assert not entry(1), "reads the caches it appends to: no version-1 form"
+        return
+    k1 = entry(1).contents
+    assert k1.abi_version == 1 and k1.target == b"gfx950"
+    assert k1.contract.decode() == k.contract.decode()[:-3] + ".v1"
 
 
 def _prepare(k, ins, outs):
@@ -246,3 +252,79 @@ def test_work_item_encoding_bounds():
     st = lib.ifattn_varlen_prefill_bf16(a, a, a, a, 2048, a, a, a, 1, 32769, 32769, 262144, 16, 1,
                                         256, 128, 2048, 0.1, a, 1 << 40, None)
     assert st == -1 and b"4096 query tiles" in lib.ifattn_last_error()
+
+
+# ---- the reference's own loader (native/src/compiled_kernel.cpp, compiled in place)
+
+def _ref_loader():
+    import oracle
+    l = oracle.ref_loader()
+    if l is None:
+        pytest.skip("reference loader not built (reference tree absent at build time)")
+    return l
+
+
+def ref_open(name, contract):
+    l = _ref_loader()
+    _native.lib()
+    h = C.c_void_p()
+    st = l.ref_loader_open(str(ROOT / "ironpangu_amd" / f"libifk_{name}.so").encode(),
+                           contract.encode(), b"gfx950", C.byref(h))
+    return st, h, l
+
+
+def ref_prepare(l, h, ins, outs):
+    a = (Tensor * len(ins))(*ins)
+    b = (Tensor * len(outs))(*outs)
+    p, ws = C.c_void_p(), C.c_uint64()
+    st = l.ref_loader_prepare(h, C.cast(a, C.c_void_p), len(ins), C.cast(b, C.c_void_p), len(outs),
+                              C.byref(p), C.byref(ws))
+    return st, p, ws.value
+
+
+def byte_view(shape, width):
+    """Version-1 integer port: I8 tensor whose last extent is width x the count."""
+    return tensor(list(shape[:-1]) + [shape[-1] * width], 1, 1)
+
+
+@pytest.mark.parametrize("name", sorted(set(PLUGINS) - {"paged_attention_qwen_gated_bf16"}))
+def test_reference_loader_accepts_every_v1_plugin(name):
+    so, entry = load_plugin(name)
+    contract = entry(1).contents.contract.decode()
+    st, h, l = ref_open(name, contract)
+    assert st == 0, l.ref_loader_error()
+    l.ref_loader_close(h)
+    # the v2 name is not what version 1 answers
+    st, h, l = ref_open(name, contract[:-3] + ".v2")
+    assert st != 0 and b"contract" in l.ref_loader_error()
+
+
+def test_reference_loader_prepares_v1_decode_and_write():
+    st, h, l = ref_open("paged_decode_gqa_bf16", "inferfabric.paged_decode.gqa.bf16.v1")
+    assert st == 0
+    n, hq, hkv, d, nb, bs, entries = 4, 16, 2, 128, 64, 128, 8
+    ins = [tensor([n, hq, d], 2, 1), tensor([nb, bs, hkv, d], 2, 1), tensor([nb, bs, hkv, d], 2, 1),
+           byte_view([n, entries], 4), byte_view([n], 4)]
+    outs = [tensor([n, hq, d], 2, 2)]
+    st, p, ws = ref_prepare(l, h, ins, outs)
+    assert st == 0, l.ref_loader_error()
+    assert ws == _native.lib().ifattn_paged_decode_workspace_size(n, hq, d, entries * bs)
+    l.ref_loader_release(p)
+    # an I32 dtype is outside version 1: the reference loader itself refuses it
+    bad = list(ins)
+    bad[3] = tensor([n, entries], 4, 1)
+    assert ref_prepare(l, h, bad, outs)[0] != 0 and b"dtype" in l.ref_loader_error()
+    # a byte view whose length is not whole int32s: the plug-in refuses it
+    bad = list(ins)
+    bad[4] = tensor([n * 4 + 1], 1, 1)
+    assert ref_prepare(l, h, bad, outs)[0] != 0
+    l.ref_loader_close(h)
+    # in-place cache write: caches are write-only outputs in version 1
+    st, h, l = ref_open("kv_cache_write_c8", "inferfabric.kv_cache_write.c8.v1")
+    ins = [tensor([8, 2, 128], 2, 1), tensor([8, 2, 128], 2, 1), byte_view([8], 8)]
+    outs = [tensor([4, 32, 2, 128], 1, 2), tensor([4, 32, 2, 128], 1, 2),
+            tensor([4, 32, 2], 3, 2), tensor([4, 32, 2], 3, 2)]
+    st, p, ws = ref_prepare(l, h, ins, outs)
+    assert st == 0 and ws == 0, l.ref_loader_error()
+    l.ref_loader_release(p)
+    l.ref_loader_close(h)

@@ -138,3 +138,86 @@ def test_plugin_norm_rope_write_and_attention_contracts():
                            sink_values=sv)
     torch.cuda.synchronize()
     assert torch.equal(o3, o4)
+
+
+def _ref_run(name, contract, ins, outs):
+    """prepare -> enqueue -> release through the reference's own loader
+    (native/src/compiled_kernel.cpp, compiled in place), version 1 descriptors:
+    integer tensors as I8 byte views, in-place caches as write outputs."""
+    import torch
+    from test_abi import ref_open, ref_prepare
+    st, h, l = ref_open(name, contract)
+    assert st == 0, l.ref_loader_error()
+
+    def v1(t, access):
+        if t.dtype in (torch.int32, torch.int64):
+            t = t.view(torch.int8)  # byte view: last extent x4 / x8
+        return desc(t, access)
+
+    st, p, ws = ref_prepare(l, h, [v1(t, a) for t, a in ins], [v1(t, a) for t, a in outs])
+    assert st == 0, l.ref_loader_error()
+    w = torch.empty(max(ws, 256), dtype=torch.uint8, device="cuda")
+    st = l.ref_loader_enqueue(p, w.data_ptr(), w.numel(), torch.cuda.current_stream().cuda_stream)
+    assert st == 0, l.ref_loader_error()
+    torch.cuda.synchronize()
+    l.ref_loader_release(p)
+    l.ref_loader_close(h)
+
+
+def test_reference_loader_v1_write_decode_prefill_match_direct():
+    import torch
+    from ironpangu_amd import ops
+    case = W.config_case("cpu_ref", seed=8)
+    h = case.host
+    nb, bs, hkv, hd = case.pool_blocks, case.block_size, case.kv_heads, case.head_dim
+    kc1 = to_dev(h["k_pool"]).view(nb, bs, hkv, hd)
+    vc1 = to_dev(h["v_pool"]).view(nb, bs, hkv, hd)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    kn, vn, q = to_dev(h["k_new"]), to_dev(h["v_new"]), to_dev(h["q"])
+    slots = to_dev(case.slot_mapping.astype(np.int64))
+    tables, lens = to_dev(case.block_tables), to_dev(case.seq_lens)
+    _ref_run("kv_cache_write_bf16", "inferfabric.kv_cache_write.bf16.v1",
+             [(kn, 1), (vn, 1), (slots, 1)], [(kc1, 2), (vc1, 2)])
+    ops.kv_cache_write(kn, vn, kc2, vc2, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    out1 = torch.empty_like(q)
+    _ref_run("paged_decode_gqa_bf16", "inferfabric.paged_decode.gqa.bf16.v1",
+             [(q, 1), (kc1, 1), (vc1, 1), (tables, 1), (lens, 1)], [(out1, 2)])
+    out2 = ops.paged_decode(q, kc2, vc2, tables, lens, tables.shape[1] * bs, 1.0 / np.sqrt(hd))
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2)
+    # packed varlen prefill: one 5-row chunk and one decode row over the same caches
+    cu = torch.tensor([0, 5, 6], dtype=torch.int32, device="cuda")
+    kv = torch.tensor([int(case.seq_lens[0]), int(case.seq_lens[1])], dtype=torch.int32, device="cuda")
+    qp = q[:6].contiguous()
+    o1 = torch.empty_like(qp)
+    _ref_run("varlen_prefill_bf16", "inferfabric.varlen_prefill.bf16.v1",
+             [(qp, 1), (kc1, 1), (vc1, 1), (tables[:2].contiguous(), 1), (cu, 1), (kv, 1)], [(o1, 2)])
+    o2 = ops.varlen_prefill(qp, kc2, vc2, tables[:2].contiguous(), cu, kv, 6, tables.shape[1] * bs)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+def test_plugin_gated_attention_matches_direct():
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(31)
+    batch, context, nslots = 5, 1500, 8192
+    q = to_dev(W.bf16_randn(rng, (batch, 8, 256)))
+    k, v = to_dev(W.bf16_randn(rng, (batch, 512))), to_dev(W.bf16_randn(rng, (batch, 512)))
+    gate = to_dev(W.bf16_randn(rng, (batch, 8, 256)))
+    keys1 = to_dev(W.bf16_randn(rng, (nslots, 512)))
+    vals1 = to_dev(W.bf16_randn(rng, (nslots, 512)))
+    keys2, vals2 = keys1.clone(), vals1.clone()
+    append = torch.from_numpy(rng.permutation(nslots)[:batch].astype(np.int64)).cuda()
+    table = torch.from_numpy(rng.integers(0, nslots, (batch, context)).astype(np.int64)).cuda()
+    mask = torch.from_numpy(np.where(rng.random((batch, context)) < 0.2, -np.inf, 0.0)
+                            .astype(np.float32)).cuda()
+    o1 = torch.empty_like(q)
+    run("paged_attention_qwen_gated_bf16",
+        [(q, 1), (k, 1), (v, 1), (gate, 1), (append, 1), (table, 1), (mask, 1)],
+        [(keys1, 3), (vals1, 3), (o1, 2)])
+    o2 = ops.gated_paged_attention(q, k, v, gate, keys2, vals2, append, table, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(keys1, keys2) and torch.equal(vals1, vals2)
