@@ -160,6 +160,23 @@ int32_t ifattn_gated_paged_attention_bf16(const void *q, const void *k, const vo
                                           int64_t slots, int64_t context, void *workspace,
                                           uint64_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ifattn_paged_decode_step_bf16 without a workspace. The
+ * call's scratch (work queue, work list, split-K partials) lives in a static
+ * device array of IFATTN_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends; calls needing more (ifattn_paged_decode_workspace_size above it) fail
+ * with IFATTN_EINVAL. The entry point allocates nothing. All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU (concurrent streams,
+ * threads) race and must be serialized by the caller. */
+#define IFATTN_NOALLOC_SCRATCH_BYTES (32ull << 20)
+int32_t ifattn_paged_decode_step_bf16_noalloc(
+    const void *q, const void *k_rows, const void *v_rows, void *k_cache, void *v_cache,
+    const void *slot_mapping, int32_t slot_dtype, int64_t rows, const int32_t *block_tables,
+    int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs, int32_t q_heads,
+    int32_t kv_heads, int32_t head_dim, int32_t block_size, int64_t num_blocks,
+    int32_t max_context, float scale, void *stream);
+
 /* Same over an int8 cache with fp32 scales per (token, kv head), dequantized in
  * registers (replaces cache_dequantize + bf16 attention, token_executor.h:812-822). */
 int32_t ifattn_paged_decode_c8(const void *q, const void *k_cache, const void *v_cache,

@@ -41,6 +41,8 @@ SIGNATURES = {
                                        i32, f32, vp, u64, vp]),
     "ifattn_paged_decode_step_bf16": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, vp, i32, vp, vp, i32,
                                             i32, i32, i32, i32, i64, i32, f32, vp, u64, vp]),
+    "ifattn_paged_decode_step_bf16_noalloc": (i32, [vp, vp, vp, vp, vp, vp, i32, i64, vp, i32, vp, vp,
+                                                    i32, i32, i32, i32, i32, i64, i32, f32, vp]),
     "ifattn_paged_decode_c8": (i32, [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32,
                                      i64, i32, f32, vp, u64, vp]),
     "ifattn_gated_paged_attention_workspace_size": (u64, [i64, i64]),

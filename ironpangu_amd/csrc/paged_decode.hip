@@ -38,6 +38,7 @@
 // so QK^T runs on the integer codes and the K scale multiplies the score; the
 // V scale is folded into the probability before the PV MFMA.
 #include <cstdlib>
+#include <mutex>
 
 #include "common.h"
 #include "ifattn_internal.h"
@@ -610,4 +611,59 @@ extern "C" int32_t ifattn_paged_decode_step_bf16(
   return decode_common(false, q, k_cache, v_cache, nullptr, nullptr, block_tables, table_stride,
                        seq_lens, out, num_seqs, q_heads, kv_heads, head_dim, block_size, num_blocks,
                        max_context, scale, workspace, workspace_bytes, stream, wr);
+}
+
+// ---------------------------------------------------------------- no-allocation step
+//
+// Device scratch for ifattn_paged_decode_step_bf16_noalloc: the split-K work
+// queue, work list and partials of one call live here instead of in a caller
+// workspace. Every GPU the library runs on holds its own copy until the process
+// ends. Nothing in it has to start at zero (the prologue kernel writes the queue
+// words and the work list before the decode kernel reads them, and partials are
+// written before the merge reads them).
+static __device__ __align__(256) uint8_t scratch[IFATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch[kMaxDevices] = {};
+
+// Device address of this GPU's `scratch` (the host-side symbol is only a
+// stand-in), looked up once per device with that device current.
+int32_t scratch_address(void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(IFATTN_ELAUNCH, "decode step (no allocation): no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(IFATTN_ELAUNCH, "decode step (no allocation): scratch lookup",
+                  hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return IFATTN_OK;
+}
+}  // namespace
+
+extern "C" int32_t ifattn_paged_decode_step_bf16_noalloc(
+    const void *q, const void *k_rows, const void *v_rows, void *k_cache, void *v_cache,
+    const void *slot_mapping, int32_t slot_dtype, int64_t rows, const int32_t *block_tables,
+    int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs, int32_t q_heads,
+    int32_t kv_heads, int32_t head_dim, int32_t block_size, int64_t num_blocks,
+    int32_t max_context, float scale, void *stream) {
+  const uint64_t need = ifattn_paged_decode_workspace_size(num_seqs, q_heads, head_dim, max_context);
+  if (need > IFATTN_NOALLOC_SCRATCH_BYTES)
+    return fail(IFATTN_EINVAL,
+                "decode step (no allocation): the call needs more than the 32 MiB static scratch "
+                "(fewer sequences or a shorter max_context)");
+  void *ws = nullptr;
+  if (const int32_t st = scratch_address(&ws)) return st;
+  return ifattn_paged_decode_step_bf16(q, k_rows, v_rows, k_cache, v_cache, slot_mapping,
+                                       slot_dtype, rows, block_tables, table_stride, seq_lens, out,
+                                       num_seqs, q_heads, kv_heads, head_dim, block_size,
+                                       num_blocks, max_context, scale, ws,
+                                       IFATTN_NOALLOC_SCRATCH_BYTES, stream);
 }

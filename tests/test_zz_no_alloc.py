@@ -1,0 +1,68 @@
+"""GPU: the allocation-free decode step (ifattn_paged_decode_step_bf16_noalloc,
+a static device scratch in place of the workspace) against the workspace entry
+point ifattn_paged_decode_step_bf16, bit for bit: outputs and caches, on two
+calls in a row with the second smaller, plus the size rejection."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import to_dev
+from ironpangu_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(noalloc, case, h, kc, vc, out):
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd._native import check, lib
+    q, kn, vn = to_dev(h["q"]), to_dev(h["k_new"]), to_dev(h["v_new"])
+    slots = to_dev(case.slot_mapping.astype(np.int64))
+    tables, lens = to_dev(case.block_tables), to_dev(case.seq_lens)
+    nb, bs, hkv, hd = kc.shape
+    args = [q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+            slots.data_ptr(), 5, case.num_seqs, tables.data_ptr(), tables.shape[1], lens.data_ptr(),
+            out.data_ptr(), case.num_seqs, case.q_heads, hkv, hd, bs, nb, case.max_context,
+            case.scale]
+    s = torch.cuda.current_stream().cuda_stream
+    if noalloc:
+        check(lib().ifattn_paged_decode_step_bf16_noalloc(*args, s), "noalloc step")
+    else:
+        ws = ops.decode_workspace(case.num_seqs, case.q_heads, hd, case.max_context)
+        check(lib().ifattn_paged_decode_step_bf16(*args, ws.data_ptr(), ws.numel(), s), "step")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("order", ["large_then_small"])
+def test_noalloc_step_matches_workspace_step(order):
+    import torch
+    # call 1: 64 sequences up to 20000 tokens (split-K partials in the scratch);
+    # call 2: 5 shorter sequences, so stale scratch contents must not leak in
+    for seed, n, hi in ((3, 64, 20000), (4, 5, 3000)):
+        print(f"noalloc case seed={seed} seqs={n} hi={hi}", flush=True)
+        case = W.decode_host_case(seed, num_seqs=n, lo=1, hi=hi, dist="loguniform", q_heads=16,
+                                  kv_heads=2, head_dim=128, block_size=128,
+                                  pool_blocks=n * ((hi + 127) // 128) + 4)
+        h = case.host
+        shape = (case.pool_blocks, 128, 2, 128)
+        k1, v1 = to_dev(h["k_pool"]).view(shape), to_dev(h["v_pool"]).view(shape)
+        k2, v2 = k1.clone(), v1.clone()
+        o1 = torch.empty((n, 16, 128), dtype=torch.bfloat16, device="cuda")
+        o2 = torch.empty_like(o1)
+        _step(False, case, h, k1, v1, o1)
+        _step(True, case, h, k2, v2, o2)
+        assert torch.equal(o1, o2), "outputs differ"
+        assert torch.equal(k1, k2) and torch.equal(v1, v2), "caches differ"
+
+
+def test_noalloc_step_rejects_calls_beyond_the_scratch():
+    from ironpangu_amd._native import lib
+    l = lib()
+    # 4096 sequences over 128k tokens need far more than 32 MiB of partials
+    need = l.ifattn_paged_decode_workspace_size(4096, 16, 128, 131072)
+    assert need > (32 << 20)
+    a = 0x10000
+    st = l.ifattn_paged_decode_step_bf16_noalloc(a, a, a, a, a, a, 5, 4096, a, 1024, a, a, 4096,
+                                                 16, 2, 128, 128, 1 << 20, 131072, 0.1, None)
+    assert st == -1 and b"32 MiB" in l.ifattn_last_error()
