@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=64)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (counter calibration)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only measure the HBM read ceiling (64 KiB blocks over an 8.6 GB footprint)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip configs 3-5 (reported under 'secondary')")
     return ap.parse_args()
@@ -110,7 +112,8 @@ def cpu_baseline(seed, sample_seqs):
     k = W.bf16_randn(rng, (nslot, hkv, hd))
     v = W.bf16_randn(rng, (nslot, hkv, hd))
     q = W.bf16_randn(rng, (len(lens), hq, hd))
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host_cores = os.cpu_count() or 1
+    threads = max(1, min(16, host_cores))  # the box's CPU share for one GPU
     oracle.paged_decode(q, k, v, table, np.minimum(lens, 64), hq, hkv, hd, bs, full.scale,
                         threads=threads)  # warm
     t0 = time.perf_counter()
@@ -122,7 +125,10 @@ def cpu_baseline(seed, sample_seqs):
             break
     dt = (time.perf_counter() - t0) / reps
     b = W.decode_bytes(lens, hq, hkv, hd, bs, with_write=False)["attention"]
-    return {"value": round(b / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(b / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "host_cores": host_cores,
+            "cores_note": "threads used (capped at the 16-core CPU share of one GPU); "
+                          "host_cores is what the host reports", "kind": "port",
             "tokens_per_s": round(len(lens) / dt, 1), "seconds_per_pass": round(dt, 4),
             "sample": f"oracle_paged_decode (fp32 C++ restatement) over the first {len(lens)} of "
                       f"the 256 config-2 sequences ({int(lens.sum())} context tokens), "
@@ -556,6 +562,48 @@ def bench_norm_rope_write(seed, steps, warmup):
                          "note": "launch-bound at this size (8.5 MB per call)"}}
 
 
+def read_ceiling(steps, sweep=False):
+    """HBM read ceiling for the decode's access pattern: every 64 KiB block of an
+    8.6 GB footprint (config 2's K + V pools) read once per launch, in order or
+    in a random order, with the default and the nontemporal cache policy. The
+    best of a few launch shapes (workgroups per CU, blocks in flight) is kept."""
+    import ctypes as C
+    import torch
+    lib = C.CDLL(str(ROOT / "ironpangu_amd" / "libifattn_probe.so"))
+    lib.ifattn_probe_read_blocks.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                             C.c_int32, C.c_void_p, C.c_int32, C.c_void_p]
+    nblocks = 2 * 65536
+    buf = torch.ones(nblocks * 65536, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    orders = {"sequential": torch.arange(nblocks, dtype=torch.int32, device="cuda"),
+              "random_64KiB": torch.randperm(nblocks, generator=g, device="cuda").to(torch.int32)}
+    res, shapes = {}, {}
+    for name, order in orders.items():
+        for nt in (0, 1):
+            best = None
+            for wgs in (2, 4, 8):
+                for unroll in (1, 2):
+                    def run():
+                        st = lib.ifattn_probe_read_blocks(buf.data_ptr(), order.data_ptr(), nblocks,
+                                                          nt, unroll, sink.data_ptr(), cus * wgs,
+                                                          torch.cuda.current_stream().cuda_stream)
+                        assert st == 0
+                    gbps = nblocks * 65536 / timed(run, steps, 2) / 1e6
+                    if sweep:
+                        shapes[f"{name}_{'nt' if nt else 'default'}_wg{wgs}_u{unroll}"] = round(gbps, 1)
+                    best = max(best or 0.0, gbps)
+            res[f"{name}_{'nontemporal' if nt else 'default'}_GBps"] = round(best, 1)
+    out = {"read_ceiling": res, "bytes_per_launch": nblocks * 65536,
+           "note": "best over 2/4/8 four-wave workgroups per CU and 1/2 blocks in flight per "
+                   "workgroup; 16-byte loads over whole 64 KiB blocks"}
+    if sweep:
+        out["shapes"] = shapes
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -566,6 +614,10 @@ def main():
     import torch
     from ironpangu_amd import ops
     from ironpangu_amd import workloads as W
+
+    if args.read_ceiling:
+        print(json.dumps(read_ceiling(max(args.steps, 5), sweep=True)))
+        return
 
     if args.calibrate_copy:
         # Known traffic for scaling rocprof FETCH_SIZE / WRITE_SIZE: each copy

@@ -190,6 +190,36 @@ def test_prefill_causal_prefix_means_and_decode_row():
     np.testing.assert_allclose(out[cu[1]], dec[0], rtol=1e-6)
 
 
+def test_prefill_nonzero_q_closed_form_per_row():
+    """A 3-row chunk after 1 cached token (kv_len 4): row t sees keys
+    0 .. t + 1 (kv_len - count + t + 1 of them, openpangu_attention_metadata.h:22).
+    q row t and K are multiples of the first unit vector, so score(t, j) =
+    scale * c_t * a_j, and V of key j is the constant v_j: every output is a
+    small closed-form softmax. A row offset of one either way changes the
+    number of visible keys and fails."""
+    bs, d, scale = 32, 32, 0.25
+    a = np.array([1.0, -2.0, 3.0, 0.5], np.float32)     # K[j] = a_j e0
+    vals = np.array([2.0, -1.0, 4.0, 8.0], np.float32)  # V[j] = v_j everywhere
+    c = np.array([1.5, -0.75, 2.0], np.float32)         # q row t = c_t e0
+    k = np.zeros((bs, 1, d), np.uint16)
+    v = np.zeros((bs, 1, d), np.uint16)
+    for j in range(4):
+        k[j, 0, 0] = bf(a[j])
+        v[j, 0, :] = bf(vals[j])
+    q = np.zeros((3, 2, d), np.uint16)  # 2 q heads on 1 kv head
+    q[:, 0, 0] = bf(c)
+    q[:, 1, 0] = bf(-c)
+    table = np.zeros((1, 1), np.int32)
+    out = oracle.varlen_prefill(q, k, v, table, np.array([0, 3], np.int32),
+                                np.array([4], np.int32), 2, 1, d, bs, scale)
+    for t in range(3):
+        for h, sign in ((0, 1.0), (1, -1.0)):
+            n = t + 2
+            w = np.exp(scale * sign * c[t] * a[:n].astype(np.float64))
+            exp = float((w * vals[:n]).sum() / w.sum())
+            np.testing.assert_allclose(out[t, h], exp, rtol=2e-6, atol=1e-6)
+
+
 def test_mla_q_zero_mean_and_rope_only_scores():
     rng = np.random.default_rng(6)
     bs = 64
