@@ -58,10 +58,12 @@ constexpr int decode_tile(int d) { return d > 128 ? 16 : 32; }
 #endif
 // V loads stream with the nontemporal cache policy: each V load instruction
 // covers whole 128-B lines (16 lanes x 16 B of one row), which no other load
-// touches again (config-2 decode 5.58 -> 5.95 TB/s, C8 5.2 -> 5.5). K loads
-// keep the default policy: one K instruction covers half of each line of 16
-// rows and the next one the other half, which the default policy serves from
-// L2 (nontemporal K loads measured 16% slower).
+// touches again (config-2 decode 5.58 -> 5.95 TB/s, C8 5.2 -> 5.5). With
+// half-line K loads (one instruction reading half of each line of 16 rows, the
+// next the other half) the nontemporal policy measured 16% slower, because the
+// second half is then fetched again; bf16 K therefore uses the whole-line
+// scheme below and streams nontemporally too (kKPolicy), while C8 K keeps
+// half-line loads with the default policy.
 constexpr int kVPolicy = 2;
 // K loads cover whole lines too: instruction (h, L) of a 16-token row block
 // reads line L (128 B) of the kv head's slice of rows 8h .. 8h+7, lane (c, g)
