@@ -125,27 +125,55 @@ struct LaneOffsets {
 };
 
 // The partition's block ids are fetched once per item, one per lane
-// (`lane_blocks`); a tile reads its id with v_readlane instead of a dependent
-// scalar load in front of every tile's loads.
-template <int D, bool C8>
+// (`lane_blocks`; a second register holds ids 64..127 with 16-token pages); a
+// tile reads its id with v_readlane instead of a dependent scalar load in front
+// of every tile's loads.
+struct LaneBlocks {
+  int lo, hi;
+};
+template <bool SP>
+__device__ __forceinline__ int block_at(const LaneBlocks &lb, int i) {  // i wave-uniform
+  if constexpr (SP) return i < 64 ? __builtin_amdgcn_readlane(lb.lo, i) : __builtin_amdgcn_readlane(lb.hi, i - 64);
+  return __builtin_amdgcn_readlane(lb.lo, i);
+}
+
+// SP (16-token pages): a 32-token tile spans two pages, so its rows 0..15 and
+// 16..31 come through one buffer descriptor each; the lane offsets of the
+// second half are then relative to the second page (see decode_item).
+template <int D, bool C8, bool SP>
 __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams &p,
-                                          int lane_blocks, int t_begin, int kvh, int t0,
-                                          int t_end, const LaneOffsets &o) {
+                                          const LaneBlocks &lane_blocks, int t_begin, int kvh,
+                                          int t0, int t_end, const LaneOffsets &o) {
   constexpr int EB = C8 ? 1 : 2;  // element bytes
   constexpr int TT = TileRegs<D, C8>::TT;
+  constexpr bool SPLIT = SP && TT == 32;
   const int bs = p.block_size;
-  const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 - (t_begin & ~(bs - 1))) / bs);
+  const int idx = (t0 - (t_begin & ~(bs - 1))) / bs;
+  const int blk = block_at<SP>(lane_blocks, idx);
   const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
   const int n_live = t_end - t0 < TT ? t_end - t0 : TT;
   const uint32_t row_bytes = uint32_t(p.kv_heads) * D * EB;
   // Rows past the live tokens read as zero (buffer range check), which masks
   // V of a partial tile without any per-lane selects.
-  const uint32_t extent = uint32_t(n_live - 1) * row_bytes + D * EB;
+  const int n0 = SPLIT && n_live > 16 ? 16 : n_live;
+  const uint32_t extent = uint32_t(n0 - 1) * row_bytes + D * EB;
   const int64_t first = (tok0 * p.kv_heads + kvh) * D * EB;
-  const auto rk = make_rsrc(p.k_cache + first, extent);
-  const auto rv = make_rsrc(p.v_cache + first, extent);
+  const auto rk0 = make_rsrc(p.k_cache + first, extent);
+  const auto rv0 = make_rsrc(p.v_cache + first, extent);
+  // Second page of a split tile (an empty range when no row of it is live).
+  auto rk1 = rk0, rv1 = rv0;
+  int64_t tok1 = tok0;
+  uint32_t extent1 = 0;
+  if constexpr (SPLIT) {
+    tok1 = int64_t(block_at<SP>(lane_blocks, idx + 1)) * bs;
+    extent1 = n_live > 16 ? uint32_t(n_live - 17) * row_bytes + D * EB : 0u;
+    const int64_t first1 = (tok1 * p.kv_heads + kvh) * D * EB;
+    rk1 = make_rsrc(p.k_cache + first1, extent1);
+    rv1 = make_rsrc(p.v_cache + first1, extent1);
+  }
 #pragma unroll
   for (int mt = 0; mt < TileRegs<D, C8>::MT; ++mt) {
+    const auto &rk = SPLIT && mt == 1 ? rk1 : rk0;
     if constexpr (!C8) {
 #pragma unroll
       for (int s = 0; s < D / 32; ++s) {
@@ -166,6 +194,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
   constexpr int DW = VSlice<D, C8>::DW;
 #pragma unroll
   for (int j = 0; j < TileRegs<D, C8>::TPL; ++j) {
+    const auto &rv = SPLIT && j >= 4 ? rv1 : rv0;
     if constexpr (DW == 1) {
       t.v[j][0] = buf_load_x1(rv, o.v[j]);
     } else if constexpr (DW == 2) {
@@ -185,13 +214,20 @@ __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams
   }
   if constexpr (C8) {
     const int64_t s0 = tok0 * p.kv_heads + kvh;
-    const uint32_t sext = (uint32_t(n_live - 1) * p.kv_heads + 1) * 4;
-    const auto rks = make_rsrc(p.k_scale + s0, sext);
-    const auto rvs = make_rsrc(p.v_scale + s0, sext);
+    const uint32_t sext = (uint32_t(n0 - 1) * p.kv_heads + 1) * 4;
+    const auto rks0 = make_rsrc(p.k_scale + s0, sext);
+    const auto rvs0 = make_rsrc(p.v_scale + s0, sext);
+    auto rks1 = rks0, rvs1 = rvs0;
+    if constexpr (SPLIT) {
+      const int64_t s1 = tok1 * p.kv_heads + kvh;
+      const uint32_t sext1 = n_live > 16 ? (uint32_t(n_live - 17) * p.kv_heads + 1) * 4 : 0u;
+      rks1 = make_rsrc(p.k_scale + s1, sext1);
+      rvs1 = make_rsrc(p.v_scale + s1, sext1);
+    }
 #pragma unroll
     for (int j = 0; j < TileRegs<D, C8>::TPL; ++j) {
-      t.ks[j] = buf_load_f32(rks, o.sc[j]);
-      t.vs[j] = buf_load_f32(rvs, o.sc[j]);
+      t.ks[j] = buf_load_f32(SPLIT && j >= 4 ? rks1 : rks0, o.sc[j]);
+      t.vs[j] = buf_load_f32(SPLIT && j >= 4 ? rvs1 : rvs0, o.sc[j]);
     }
   }
 }
@@ -217,7 +253,7 @@ __device__ __forceinline__ int i8_at(uint32_t w, int b) {
 // are rescaled; probabilities then stay below 2^8, exact enough for bf16 P.
 constexpr float kRescaleSlack = 8.0f;
 
-template <int D, bool C8>
+template <int D, bool C8, bool SP>
 __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int part, int kvh,
                                             int lane) {
   const int len = clamp_len(p, seq);
@@ -252,27 +288,33 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   {
     constexpr int EB = C8 ? 1 : 2;
     const uint32_t row_bytes = uint32_t(p.kv_heads) * D * EB;
+    // Split tiles (16-token pages) address rows 16..31 from their own page.
+    constexpr int kHalf = SP && decode_tile(D) == 32 ? 16 : 0;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
+      const int r0 = 16 * mt - (mt ? kHalf : 0);
       if (k_lines<D, C8>())
-        o.k[mt] = uint32_t(16 * mt + (c & 7)) * row_bytes + 16 * (g + 4 * (c >> 3));
+        o.k[mt] = uint32_t(r0 + (c & 7)) * row_bytes + 16 * (g + 4 * (c >> 3));
       else
-        o.k[mt] = uint32_t(16 * mt + c) * row_bytes + (D / 4) * g * EB;
+        o.k[mt] = uint32_t(r0 + c) * row_bytes + (D / 4) * g * EB;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      o.v[j] = uint32_t(tile_token(g, j)) * row_bytes + c * VSlice<D, C8>::BYTES;
-      o.sc[j] = uint32_t(tile_token(g, j)) * p.kv_heads * 4;
+      const int row = tile_token(g, j) - (j >= 4 ? kHalf : 0);
+      o.v[j] = uint32_t(row) * row_bytes + c * VSlice<D, C8>::BYTES;
+      o.sc[j] = uint32_t(row) * p.kv_heads * 4;
     }
   }
   const int t_begin = part * PT;
   const int t_end = t_begin + PT < len ? t_begin + PT : len;
-  int lane_blocks;
+  LaneBlocks lane_blocks{0, 0};
   {
     const int first = t_begin / p.block_size;
-    const int nblk = (t_end - 1) / p.block_size - first + 1;  // <= 64 (host-checked)
-    int b = lane < nblk ? p.block_tables[int64_t(seq) * p.table_stride + first + lane] : 0;
-    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+    const int nblk = (t_end - 1) / p.block_size - first + 1;  // <= 64, or 128 with SP (host-checked)
+    const int32_t *row = p.block_tables + int64_t(seq) * p.table_stride + first;
+    auto clamp = [&](int b) { return b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b); };
+    lane_blocks.lo = clamp(lane < nblk ? row[lane] : 0);
+    if constexpr (SP) lane_blocks.hi = clamp(lane + 64 < nblk ? row[lane + 64] : 0);
   }
 
   constexpr int NV = D / 16;  // PV MFMAs per tile (each yields 16 dims x 16 heads)
@@ -384,12 +426,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (TT - 1)); };
 #pragma unroll
   for (int i = 0; i < kStages - 1; ++i)
-    load_tile<D, C8>(tr[i], p, lane_blocks, t_begin, kvh, clamp_tile(t_begin + i * TT), t_end, o);
+    load_tile<D, C8, SP>(tr[i], p, lane_blocks, t_begin, kvh, clamp_tile(t_begin + i * TT), t_end, o);
   int t0 = t_begin;
   while (true) {
 #pragma unroll
     for (int i = 0; i < kStages; ++i) {
-      load_tile<D, C8>(tr[(i + kStages - 1) % kStages], p, lane_blocks, t_begin, kvh,
+      load_tile<D, C8, SP>(tr[(i + kStages - 1) % kStages], p, lane_blocks, t_begin, kvh,
                        clamp_tile(t0 + (kStages - 1) * TT), t_end, o);
       // Keep the prefetch issued ahead of this tile's math (the scheduler would
       // otherwise sink it below the QK^T MFMAs and shrink the loads in flight).
@@ -443,7 +485,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 // waves of a workgroup take the kv heads of one item, so the halves of every
 // cache row are fetched by sibling waves at the same time (whole rows stay
 // DRAM-page friendly; measured ~40% more bandwidth than independent waves).
-template <int D, bool C8>
+template <int D, bool C8, bool SP>
 __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kernel(
     DecodeParams p, int waves_per_wg) {
   __shared__ int item_slot;
@@ -462,7 +504,7 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
     const uint32_t e = uniform(p.items[it / groups]);
     const int seq = int(e >> 12);
     const int kvh = uniform((it % groups) * waves_per_wg + wave);  // wave-uniform for SGPR descriptors
-    if (kvh < p.kv_heads) decode_item<D, C8>(p, seq, int(e & 0xfffu), kvh, lane);
+    if (kvh < p.kv_heads) decode_item<D, C8, SP>(p, seq, int(e & 0xfffu), kvh, lane);
   }
 }
 
@@ -471,7 +513,11 @@ template <int D, bool C8>
 void launch_decode(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
   launch_prologue(p, wr, s);  // p.static_items = 0: the queue hands out every item
   const int waves = p.kv_heads < max_decode_waves(D) ? p.kv_heads : max_decode_waves(D);
-  paged_decode_kernel<D, C8><<<device_cus() * wgs_per_cu(), 64 * waves, 0, s>>>(p, waves);
+  const int grid = device_cus() * wgs_per_cu();
+  if (p.block_size == 16)  // the reference's bf16 page (paged_state_contract.h:25)
+    paged_decode_kernel<D, C8, true><<<grid, 64 * waves, 0, s>>>(p, waves);
+  else
+    paged_decode_kernel<D, C8, false><<<grid, 64 * waves, 0, s>>>(p, waves);
   launch_merge<D>(p, s);
 }
 
@@ -501,8 +547,8 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
     return fail(IFATTN_EINVAL, "paged decode: need q_heads = group * kv_heads with group <= 16");
   if (head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(IFATTN_EINVAL, "paged decode: head_dim must be 64, 128 or 256");
-  if (block_size < 32 || (block_size & (block_size - 1)))
-    return fail(IFATTN_EINVAL, "paged decode: block_size must be a power of two >= 32");
+  if (block_size < 16 || (block_size & (block_size - 1)))
+    return fail(IFATTN_EINVAL, "paged decode: block_size must be a power of two >= 16");
   if (max_context <= 0 || num_blocks <= 0 || table_stride <= 0 ||
       int64_t(table_stride) * block_size < max_context)
     return fail(IFATTN_EINVAL, "paged decode: table_stride * block_size must cover max_context");
@@ -532,8 +578,8 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   p.max_parts = max_parts_for(max_context, c8);
   p.scale_log2 = scale * kLog2e;
   if (p.max_parts > 4096) return fail(IFATTN_EINVAL, "paged decode: max_context above 1M tokens");
-  if (p.part_tokens > 64 * block_size)
-    return fail(IFATTN_EINVAL, "paged decode: partition spans more than 64 blocks");
+  if (p.part_tokens > (block_size == 16 ? 128 : 64) * block_size)
+    return fail(IFATTN_EINVAL, "paged decode: partition spans more than 64 blocks (128 of 16 tokens)");
   const uint64_t need = ifattn_paged_decode_workspace_size(num_seqs, q_heads, head_dim, max_context);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(IFATTN_EWORKSPACE, "paged decode: workspace missing, short or misaligned");

@@ -126,11 +126,49 @@ def test_decode_rejects_bad_contracts():
     from ironpangu_amd import ops
     from ironpangu_amd._native import IfattnError
     q = torch.zeros(2, 16, 128, dtype=torch.bfloat16, device="cuda")
-    kc = torch.zeros(4, 16, 2, 128, dtype=torch.bfloat16, device="cuda")  # block 16 unsupported
+    kc = torch.zeros(4, 8, 2, 128, dtype=torch.bfloat16, device="cuda")  # block 8 unsupported
     bt = torch.zeros(2, 8, dtype=torch.int32, device="cuda")
     sl = torch.ones(2, dtype=torch.int32, device="cuda")
     with pytest.raises(IfattnError):
         ops.paged_decode(q, kc, kc, bt, sl, 64)
+
+
+@pytest.mark.parametrize("hd,c8", [(128, False), (64, False), (256, False), (128, True),
+                                   (256, True)])
+def test_decode_16_token_pages(hd, c8):
+    """The reference's bf16 page of 16 tokens (native/include/paged_state_contract.h:25):
+    32-token tiles span two pages and a 2048-token partition spans 128 pages.
+    Lengths cross page, tile and partition edges; partitions run past 64 pages."""
+    import torch
+    from ironpangu_amd import ops
+    lens = [1, 15, 16, 17, 31, 33, 1023, 1025, 2047, 2049, 5000]
+    bs, pool = 16, len(lens) * ((5000 + 15) // 16) + 7  # covers the drawn lengths too
+    case = W.decode_host_case(77 + hd, num_seqs=len(lens), lo=1, hi=5000, dist="uniform",
+                              q_heads=8, kv_heads=2, head_dim=hd, block_size=bs, pool_blocks=pool,
+                              c8=c8)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(hd), case.seq_lens, bs, pool,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(len(lens)), bs)
+    if not c8:
+        *_, out, exp = _step(case)
+        assert_close(bf16_host(out), exp)
+        return
+    h = case.host
+    kc = torch.zeros((pool, bs, 2, hd), dtype=torch.int8, device="cuda")
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((pool, bs, 2), dtype=torch.float32, device="cuda")
+    vs = torch.zeros_like(ks)
+    ops.kv_cache_write_c8(to_dev(h["k_pool"]), to_dev(h["v_pool"]), kc, vc, ks, vs,
+                          torch.arange(pool * bs, dtype=torch.int64, device="cuda"))
+    out = ops.paged_decode(to_dev(h["q"]), kc, vc, to_dev(case.block_tables),
+                           to_dev(case.seq_lens), case.max_context, case.scale, k_scale=ks,
+                           v_scale=vs)
+    torch.cuda.synchronize()
+    exp = oracle.paged_decode(h["q"], kc.cpu().numpy(), vc.cpu().numpy(), case.block_tables,
+                              case.seq_lens, 8, 2, hd, bs, case.scale, k_scale=ks.cpu().numpy(),
+                              v_scale=vs.cpu().numpy())
+    assert_close(bf16_host(out), exp)
 
 
 def test_graph_replay_matches_eager():
@@ -197,17 +235,17 @@ def test_decode_step_matches_write_then_decode():
     assert_close(bf16_host(out1), exp)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(12))
 def test_decode_random_shapes(seed):
     """Seeded random shapes across the K/V load paths (whole-line bf16 K loads
     with lane rotation at head_dim 64/128/256, 16- and 32-token tiles, group
-    sizes 1..16, block sizes 32..128) with ragged lengths that cross tile,
+    sizes 1..16, block sizes 16..128) with ragged lengths that cross tile,
     block and split-K partition edges."""
     rng = np.random.default_rng(1000 + seed)
     hd = int(rng.choice([64, 128, 256]))
     hkv = int(rng.choice([1, 2, 4, 8]))
     group = int(rng.choice([g for g in (1, 2, 4, 8, 16) if g * hkv <= 64]))
-    bs = int(rng.choice([32, 64, 128]))  # a partition spans at most 64 blocks
+    bs = int(rng.choice([16, 32, 64, 128]))
     n = int(rng.integers(1, 12))
     hi = int(rng.choice([40, 700, 2500, 5000]))
     lens = rng.integers(1, hi + 1, n)
