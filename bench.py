@@ -503,6 +503,58 @@ def bench_mla_rows(seed, steps, warmup, sparse):
     return res
 
 
+def bench_gated(seed, steps, warmup):
+    """The reference session's Qwen-shape paged attention
+    (inferfabric_acl_paged_attention_prepare: 8 q / 2 kv heads, head_dim 256,
+    per-position int64 rows, fp32 additive mask, output gate) at its batch bound
+    of 64 requests over a 32768-position table: live lengths log-uniform
+    [128, 32768] (mask -inf beyond), rows drawn at random from a 2^20-row pool."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    rng = np.random.default_rng(seed + 21)
+    batch, context, slots = 64, 32768, 1 << 20
+    lens = W.lengths(rng, batch, 128, context, "loguniform")
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 22)
+    keys = torch.empty((slots, 512), dtype=torch.bfloat16, device=dev)
+    vals = torch.empty_like(keys)
+    fill_randn(keys, g)
+    fill_randn(vals, g)
+    table = torch.randint(0, slots, (batch, context), generator=g, device=dev, dtype=torch.int64)
+    pos = torch.arange(context, device=dev)[None, :]
+    mask = torch.where(pos < torch.from_numpy(lens).to(dev)[:, None], 0.0, float("-inf")).to(torch.float32)
+    q = torch.randn((batch, 8, 256), generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn((batch, 512), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((batch, 512), generator=g, device=dev).to(torch.bfloat16)
+    gate = torch.sigmoid(torch.randn((batch, 8, 256), generator=g, device=dev)).to(torch.bfloat16)
+    append = table[torch.arange(batch, device=dev), torch.from_numpy(lens - 1).to(dev)].contiguous()
+    out = torch.empty_like(q)
+    nws = ops.lib().ifattn_gated_paged_attention_workspace_size(batch, context)
+    ws = torch.empty(max(int(nws), 16), dtype=torch.uint8, device=dev)
+
+    def step():
+        ops.gated_paged_attention(q, k, v, gate, keys, vals, append, table, mask, out=out, workspace=ws)
+
+    ms = timed(step, steps, warmup)
+    live = int(lens.sum())
+    # K and V rows of every live position, the table and mask of every position,
+    # q / gate / out, and the appended rows read and written.
+    nbytes = live * 2048 + batch * context * 12 + batch * 8 * 256 * 2 * 3 + batch * 1024 * 2
+    res = {"workload": "Qwen-shape gated paged attention (session ABI), 64 requests, 32768-position "
+                       "table, live lengths log-uniform [128, 32768]",
+           "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
+           "live_positions": live,
+           "roofline": {"bound": "hbm", "kernel": "gated paged attention operator (append, attention, merge)",
+                        "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes}}
+    del keys, vals
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_slot_reuse(seed, steps, warmup):
     """Slot reuse on a 2 GiB page field (20992-byte pages, the packed C8 MLA
     page): state copy of 1 GiB of pages from one resident to another (read +
@@ -722,6 +774,7 @@ def main():
                             "mla_decode_c8": bench_mla_c8(args.seed, args.steps, args.warmup),
                             "gqa_decode_hd256": bench_decode_hd256(args.seed, args.steps, args.warmup),
                             "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup),
+                            "gated_attention_qwen": bench_gated(args.seed, args.steps, args.warmup),
                             "mla_window_attention": bench_mla_rows(args.seed, args.steps, args.warmup, False),
                             "mla_sparse_attention": bench_mla_rows(args.seed, args.steps, args.warmup, True),
                             "slot_reuse": bench_slot_reuse(args.seed, args.steps, args.warmup),

@@ -13,7 +13,7 @@
 // product. Accumulation is fp32 (scores, softmax, PV); the reference rounds
 // scores and probabilities to bf16 between its ACLNN calls.
 //
-// Kernel: one wave per (request, kv head, 1024-position partition). The wave
+// Kernel: one wave per (request, kv head, 256-position partition). The wave
 // reads 64 (mask, index) pairs at a time, one per lane, and compacts the
 // positions that can contribute (mask not -inf, index in range) into an LDS
 // list by ballot; masked positions cost 12 bytes of metadata and no cache
@@ -34,7 +34,7 @@ constexpr int kGroup = 4;         // q heads per kv head
 constexpr int kKvHeads = 2;
 constexpr int kHeads = kGroup * kKvHeads;
 constexpr int kRowBytes = kKvHeads * kD * 2;  // 1024 B per cache row
-constexpr int kPart = 1024;       // context positions per partition
+constexpr int kPart = 256;        // context positions per partition
 constexpr float kScale = 0.0625f; // 1/sqrt(256), inferfabric_acl.cpp:1400
 
 struct GatedParams {
@@ -77,16 +77,21 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   const int t_begin = part * kPart;
   const int t_end = t_begin + kPart < p.context ? t_begin + kPart : p.context;
   const int64_t meta = int64_t(b) * p.context;
-  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+  // (mask, row) of the lane's position in a 64-position chunk; the next chunk's
+  // pair is loaded while this chunk's rows are processed.
+  auto fetch = [&](int t0, float &mk, int64_t &row) {
     const int t = t0 + lane;
-    bool live = false;
-    int64_t row = 0;
-    float mk = -INFINITY;
-    if (t < t_end) {
-      mk = p.mask[meta + t];
-      row = p.table[meta + t];
-      live = mk != -INFINITY && row >= 0 && row < p.slots;
-    }
+    mk = t < t_end ? p.mask[meta + t] : -INFINITY;
+    row = t < t_end ? p.table[meta + t] : 0;
+  };
+  float mk_next;
+  int64_t row_next;
+  fetch(t_begin, mk_next, row_next);
+  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
+    const float mk = mk_next;
+    const int64_t row = row_next;
+    if (t0 + 64 < t_end) fetch(t0 + 64, mk_next, row_next);
+    const bool live = mk != -INFINITY && row >= 0 && row < p.slots;
     const uint64_t ballot = __ballot(live);
     const int n_live = __popcll(ballot);
     if (n_live == 0) continue;
@@ -101,10 +106,12 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
     for (int k0 = 0; k0 < n_live; k0 += 16) {
       // K: lane (c, g) loads row k0 + c, dims 32s + 8g .. +7 for every k-step.
       const bool kl = k0 + c < n_live;
-      const uint32_t krow = kl ? s_row[k0 + c] : 0u;
+      // Padded rows read past the buffer (zeros): no stale value (NaN or inf)
+      // can reach the scores or the accumulator.
+      const uint32_t krow = kl ? s_row[k0 + c] * uint32_t(kRowBytes) : 0xFFFFFC00u;
       u32x4 kv[kD / 32];
 #pragma unroll
-      for (int s = 0; s < kD / 32; ++s) kv[s] = buf_load_x4(rk, krow * kRowBytes + 64 * s + 16 * g);
+      for (int s = 0; s < kD / 32; ++s) kv[s] = buf_load_x4(rk, krow + 64 * s + 16 * g);
       // V: lane (c, g) loads rows k0 + 4g + j, dims 16c .. 16c + 15 (32 bytes).
       uint32_t vw[4][8];
       float xm[4];
@@ -112,16 +119,14 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
       for (int j = 0; j < 4; ++j) {
         const int e = k0 + 4 * g + j;
         const bool vl = e < n_live;
-        const uint32_t vrow = vl ? s_row[e] : 0u;
+        const uint32_t vrow = vl ? s_row[e] * uint32_t(kRowBytes) : 0xFFFFFC00u;
         xm[j] = vl ? s_mask[e] : -INFINITY;
-        const u32x4 a = buf_load_x4(rv, vrow * kRowBytes + 32 * c);
-        const u32x4 z = buf_load_x4(rv, vrow * kRowBytes + 32 * c + 16);
-        // A padded row's probability is 0; zero its V too so no stale value
-        // (NaN or inf) can reach the accumulator.
+        const u32x4 a = buf_load_x4(rv, vrow + 32 * c);
+        const u32x4 z = buf_load_x4(rv, vrow + 32 * c + 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          vw[j][i] = vl ? a[i] : 0u;
-          vw[j][4 + i] = vl ? z[i] : 0u;
+          vw[j][i] = a[i];
+          vw[j][4 + i] = z[i];
         }
       }
       f32x4 sacc = f32x4{0, 0, 0, 0};
