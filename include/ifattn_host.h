@@ -23,6 +23,8 @@ void ifattn_pages_destroy(ifattn_pages *pages);
 int32_t ifattn_pages_select(ifattn_pages *pages, uint32_t slot);
 /* ResidentPages::bind for the selected resident (page_binding.h:87-106). */
 int32_t ifattn_pages_bind(ifattn_pages *pages, const int32_t *ids, uint64_t count);
+/* The selected resident (ResidentPages::select's argument; 0 initially). */
+int32_t ifattn_pages_selected(const ifattn_pages *pages, uint32_t *slot);
 /* ResidentPages::release (page_binding.h:107-111). */
 int32_t ifattn_pages_release(ifattn_pages *pages, uint32_t slot);
 /* Owned pages of a resident; *count receives the number, ids may be NULL to query it. */

@@ -28,6 +28,16 @@ class SequenceSlice(C.Structure):
     _fields_ = [("resident", u32), ("position", u32), ("tokens", u32), ("sample", i32)]
 
 
+class StateGeometry(C.Structure):
+    _fields_ = [("format", u32), ("page_tokens", u32), ("row_bytes", u32), ("num_blocks", u32),
+                ("table_entries", u32), ("heads", u32), ("cache_bytes", u64)]
+
+
+class StateBuffers(C.Structure):
+    _fields_ = [(n, vp) for n in ("cache", "table", "scales", "query", "out", "indices", "kv_len",
+                                  "sink_keys", "sink_values")]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "ifattn_abi_version": (i32, []),
@@ -72,6 +82,17 @@ SIGNATURES = {
     "ifattn_pages_select": (i32, [vp, u32]),
     "ifattn_pages_bind": (i32, [vp, pi32, u64]),
     "ifattn_pages_release": (i32, [vp, u32]),
+    "ifattn_pages_selected": (i32, [vp, pu32]),
+    "ifattn_attention_state_create": (i32, [u32, u32, i32, u32, i32, u32, u32, C.POINTER(vp)]),
+    "ifattn_attention_state_destroy": (None, [vp]),
+    "ifattn_attention_state_geometry_of": (i32, [vp, C.POINTER(StateGeometry)]),
+    "ifattn_attention_state_pages": (i32, [vp, C.POINTER(vp)]),
+    "ifattn_attention_state_append": (i32, [vp, u32, pu64]),
+    "ifattn_attention_state_blocks": (i32, [vp, pi32, u32, pu32]),
+    "ifattn_attention_state_buffers_of": (i32, [vp, C.POINTER(StateBuffers)]),
+    "ifattn_attention_state_upload_table": (i32, [vp, vp]),
+    "ifattn_attention_state_set_length": (i32, [vp, i32, vp]),
+    "ifattn_attention_state_attend": (i32, [vp, i32, i32, vp]),
     "ifattn_pages_owned": (i32, [vp, u32, pi32, u64, pu64]),
     "ifattn_pages_append": (i32, [vp, u32, u32, pu64]),
     "ifattn_pages_slot_mapping": (i32, [vp, pi32, pi32, u64, pi64]),

@@ -135,6 +135,12 @@ extern "C" int32_t ifattn_pages_select(ifattn_pages *pages, uint32_t slot) {
   return IFATTN_OK;
 }
 
+extern "C" int32_t ifattn_pages_selected(const ifattn_pages *pages, uint32_t *slot) {
+  if (!pages || !slot) return reject("pages: null pool or output");
+  *slot = pages->selected;
+  return IFATTN_OK;
+}
+
 extern "C" int32_t ifattn_pages_bind(ifattn_pages *p, const int32_t *ids, uint64_t count) {
   if (!p || (!ids && count)) return reject("pages: null pool or page list");
   const uint32_t r = p->selected, per = p->per_resident;

@@ -13,7 +13,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._native import SequenceSlice, lib
+from ._native import SequenceSlice, StateBuffers, StateGeometry, lib
 
 
 class MetadataError(RuntimeError):
@@ -219,3 +219,71 @@ class SequenceBatch:
         return SequenceBatch(starts[: n + 1].tolist(), res[:n].tolist(), pos[:r].tolist(),
                              rr[:r].tolist(), qe[:n].tolist(), pr[:n].tolist(), kv[:n].tolist(),
                              lens[:r].tolist(), sr[:s].tolist(), sres[:s].tolist())
+
+
+class _BorrowedPages(ResidentPages):
+    """ResidentPages view of a page binding owned by an AttentionState."""
+
+    def __init__(self, handle, page_tokens, logical_tokens, slots, owner):
+        self._h = handle
+        self.page_tokens, self.logical_tokens, self.slots = page_tokens, logical_tokens, slots
+        self._owner = owner  # keeps the state (and the binding) alive
+
+    def __del__(self):
+        pass
+
+
+class AttentionState:
+    """One MLA attention layer's state (native/src/openpangu_decoder_state.h:16-48):
+    cache, page binding, block table, query/output/index/length buffers and 128
+    sink rows, over include/ifattn_state.h. Device buffers are allocated on the
+    current device at the first call that needs them."""
+
+    FORMATS = {0: "bf16", 1: "packed_c8", 2: "row_quant"}
+
+    def __init__(self, bits=16, capacity=512, packed=False, residents=1, shared=False, context=0,
+                 heads=6):
+        self._h = C.c_void_p()
+        _check(lib().ifattn_attention_state_create(bits, capacity, int(packed), residents,
+                                                   int(shared), context, heads, C.byref(self._h)))
+        g = StateGeometry()
+        _check(lib().ifattn_attention_state_geometry_of(self._h, C.byref(g)))
+        self.geometry = {f: getattr(g, f) for f, _ in StateGeometry._fields_}
+        self.format = self.FORMATS[g.format]
+        self.capacity, self.context, self.residents = capacity, context, residents
+        ph = C.c_void_p()
+        _check(lib().ifattn_attention_state_pages(self._h, C.byref(ph)))
+        self.page_binding = _BorrowedPages(ph, g.page_tokens, capacity, residents, self)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().ifattn_attention_state_destroy(h)
+            self._h = None
+
+    def append(self, position: int) -> int:
+        out = C.c_uint64()
+        _check(lib().ifattn_attention_state_append(self._h, position, C.byref(out)))
+        return out.value
+
+    def blocks(self) -> np.ndarray:
+        n = C.c_uint32()
+        _check(lib().ifattn_attention_state_blocks(self._h, None, 0, C.byref(n)))
+        out = np.zeros(max(n.value, 1), np.int32)
+        _check(lib().ifattn_attention_state_blocks(self._h, out.ctypes.data_as(C.POINTER(C.c_int32)),
+                                                   out.size, C.byref(n)))
+        return out[: n.value]
+
+    def buffers(self) -> dict:
+        b = StateBuffers()
+        _check(lib().ifattn_attention_state_buffers_of(self._h, C.byref(b)))
+        return {f: getattr(b, f) for f, _ in StateBuffers._fields_}
+
+    def upload_table(self, stream=0) -> None:
+        _check(lib().ifattn_attention_state_upload_table(self._h, stream))
+
+    def set_length(self, kv_len: int, stream=0) -> None:
+        _check(lib().ifattn_attention_state_set_length(self._h, kv_len, stream))
+
+    def attend(self, window: int = 0, sinks: bool = False, stream=0) -> None:
+        _check(lib().ifattn_attention_state_attend(self._h, window, int(sinks), stream))
