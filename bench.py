@@ -271,6 +271,48 @@ def bench_decode_hd256(seed, steps, warmup):
     return res
 
 
+def bench_decode_page16(seed, steps, warmup):
+    """Config 2's sequences and heads over the reference's 16-token bf16 pages
+    (native/include/paged_state_contract.h:25): 256 seqs, log-uniform
+    [128, 32768], random block tables over a pool of 16-token pages."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    lens = W.decode_meta(seed, **W.CONFIGS["decode"]).seq_lens
+    need = int(((lens.astype(np.int64) + 15) // 16).sum())
+    kw = dict(W.CONFIGS["decode"])
+    kw.update(block_size=16, pool_blocks=need + 64)
+    case = W.decode_meta(seed, **kw)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 9)
+    shape = (case.pool_blocks, 16, 2, 128)
+    kc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    fill_randn(kc, g)
+    fill_randn(vc, g)
+    q = torch.randn((256, 16, 128), generator=g, device=dev).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens_d = torch.from_numpy(case.seq_lens).to(dev)
+    ws = ops.decode_workspace(256, 16, 128, case.max_context)
+    out = torch.empty_like(q)
+
+    def attn():
+        ops.paged_decode(q, kc, vc, tables, lens_d, case.max_context, case.scale, out=out, workspace=ws)
+
+    ms = timed(attn, steps, warmup)
+    b = W.decode_bytes(case.seq_lens, 16, 2, 128, 16)["attention"]
+    res = {"workload": "GQA paged decode on 16-token pages, config-2 sequences (256, log-uniform [128,32768])",
+           "value": round(b / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
+           "roofline": {"bound": "hbm", "kernel": "paged_decode bf16 operator (16-token pages)",
+                        "achieved": round(b / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(b / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": b}}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_mla_c8(seed, steps, warmup):
     """Config 5's rows and lengths over packed C8 latent rows (656 B per key)."""
     import torch
@@ -773,6 +815,7 @@ def main():
                             "mla_decode": bench_mla(args.seed, args.steps, args.warmup),
                             "mla_decode_c8": bench_mla_c8(args.seed, args.steps, args.warmup),
                             "gqa_decode_hd256": bench_decode_hd256(args.seed, args.steps, args.warmup),
+                            "gqa_decode_page16": bench_decode_page16(args.seed, args.steps, args.warmup),
                             "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup),
                             "gated_attention_qwen": bench_gated(args.seed, args.steps, args.warmup),
                             "mla_window_attention": bench_mla_rows(args.seed, args.steps, args.warmup, False),

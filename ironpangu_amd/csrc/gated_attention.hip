@@ -201,27 +201,53 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   }
 }
 
-// One wave per (request, head): combine the partitions' (m, l, O), normalise,
-// apply the gate. Lane l owns dims 4l .. 4l + 3.
-__global__ __launch_bounds__(64) void gated_merge_kernel(GatedParams p) {
-  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+// One workgroup of four waves per (request, head): combine the partitions'
+// (m, l, O), normalise, apply the gate. Wave w takes partitions w, w + 4, ...
+// (lane l owns dims 4l .. 4l + 3), eight partials in flight at a time, and
+// partitions without a live position (m = -inf) are skipped by their (m, l)
+// alone; the four waves' sums meet in LDS.
+__global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
+  __shared__ float s_max[4], s_l[4];
+  __shared__ f32x4 s_o[4][64];
+  const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t base = int64_t(b) * p.parts * kHeads + h;
+  auto ml_at = [&](int k) { return *reinterpret_cast<const float2 *>(p.part_ml + (base + int64_t(k) * kHeads) * 2); };
   float mmax = -INFINITY;
-  for (int k = lane; k < p.parts; k += 64) mmax = fmaxf(mmax, p.part_ml[(base + int64_t(k) * kHeads) * 2]);
+  for (int k = int(threadIdx.x); k < p.parts; k += 256) mmax = fmaxf(mmax, ml_at(k).x);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
+  if (lane == 0) s_max[w] = mmax;
+  __syncthreads();
+  mmax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
   f32x4 acc = f32x4{0, 0, 0, 0};
   float lsum = 0.0f;
   if (mmax != -INFINITY) {
-    for (int k = 0; k < p.parts; ++k) {
-      const int64_t r = base + int64_t(k) * kHeads;
-      const float m = p.part_ml[r * 2];
-      if (m == -INFINITY) continue;
-      const float w = fast_exp2(m - mmax);
-      lsum += w * p.part_ml[r * 2 + 1];
-      acc += w * *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane);
+    constexpr int U = 8;
+    for (int k0 = w; k0 < p.parts; k0 += 4 * U) {
+      float2 ml[U];
+      f32x4 o[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = k0 + 4 * u;
+        ml[u] = k < p.parts ? ml_at(k) : make_float2(-INFINITY, 0.0f);
+        o[u] = ml[u].x != -INFINITY
+                   ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(k) * kHeads) * kD + 4 * lane)
+                   : f32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float wt = ml[u].x == -INFINITY ? 0.0f : fast_exp2(ml[u].x - mmax);
+        lsum += wt * ml[u].y;
+        acc += wt * o[u];
+      }
     }
   }
+  s_o[w][lane] = acc;
+  if (lane == 0) s_l[w] = lsum;
+  __syncthreads();
+  if (w != 0) return;
+  acc = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
+  lsum = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
   const int64_t o = (int64_t(b) * kHeads + h) * kD + 4 * lane;
   const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o);
@@ -300,6 +326,6 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
       static_cast<const uint8_t *>(k), static_cast<const uint8_t *>(v),
       static_cast<uint8_t *>(keys), static_cast<uint8_t *>(values), append, int(batch), slots);
   gated_decode_kernel<<<dim3(p.parts, kKvHeads, unsigned(batch)), 64, 0, s>>>(p);
-  if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 64, 0, s>>>(p);
+  if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 256, 0, s>>>(p);
   return launch_status("gated paged attention");
 }
