@@ -690,9 +690,35 @@ def read_ceiling(steps, sweep=False):
                         shapes[f"{name}_{'nt' if nt else 'default'}_wg{wgs}_u{unroll}"] = round(gbps, 1)
                     best = max(best or 0.0, gbps)
             res[f"{name}_{'nontemporal' if nt else 'default'}_GBps"] = round(best, 1)
+    # Row gathers at random row offsets: the per-position K/V half rows of the
+    # gated attention (512 of 1024 B), packed C8 MLA rows (656 B) and bf16 MLA
+    # rows (1152 B); about 750 MB per launch from a pool of the buffer's size.
+    lib.ifattn_probe_gather_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
+                                             C.c_int64, C.c_int32, C.c_void_p, C.c_int32,
+                                             C.c_void_p]
+    for row_bytes, stride in ((512, 1024), (656, 656), (1152, 1152)):
+        pool = buf.numel() // stride
+        nrows = (750 << 20) // row_bytes
+        order = torch.randint(0, pool, (nrows,), generator=g, device="cuda", dtype=torch.int32)
+        for nt in (0, 1):
+            best = None
+            for wgs in (4, 8, 16):
+                def run():
+                    st = lib.ifattn_probe_gather_rows(buf.data_ptr(), order.data_ptr(), nrows,
+                                                      row_bytes, stride, nt, sink.data_ptr(),
+                                                      cus * wgs, torch.cuda.current_stream().cuda_stream)
+                    assert st == 0
+                gbps = nrows * row_bytes / timed(run, steps, 2) / 1e6
+                if sweep:
+                    shapes[f"rows{row_bytes}_{'nt' if nt else 'default'}_wg{wgs}"] = round(gbps, 1)
+                best = max(best or 0.0, gbps)
+            res[f"random_rows_{row_bytes}B_{'nontemporal' if nt else 'default'}_GBps"] = round(best, 1)
+        del order
     out = {"read_ceiling": res, "bytes_per_launch": nblocks * 65536,
-           "note": "best over 2/4/8 four-wave workgroups per CU and 1/2 blocks in flight per "
-                   "workgroup; 16-byte loads over whole 64 KiB blocks"}
+           "note": "blocks: best over 2/4/8 four-wave workgroups per CU and 1/2 blocks in flight "
+                   "per workgroup, 16-byte loads over whole 64 KiB blocks; rows: about 750 MB of "
+                   "rows at random offsets (stride 1024, 656, 1152 B), 8 loads in flight per "
+                   "thread, best over 4/8/16 workgroups per CU"}
     if sweep:
         out["shapes"] = shapes
     return out
