@@ -36,6 +36,8 @@ constexpr int kHeads = kGroup * kKvHeads;
 constexpr int kRowBytes = kKvHeads * kD * 2;  // 1024 B per cache row
 constexpr int kPart = 256;        // context positions per partition
 constexpr float kScale = 0.0625f; // 1/sqrt(256), inferfabric_acl.cpp:1400
+// Cache-policy bits of the K/V row loads (2: nontemporal; rows are read once).
+constexpr int kPolicy = 2;
 
 struct GatedParams {
   const uint16_t *q, *gate;
@@ -49,21 +51,21 @@ struct GatedParams {
   int context, parts;
 };
 
+// Lane c of a 16-lane row gets the value of lane (c + 8) % 16 (DPP row_ror:8).
+__device__ __forceinline__ u32x4 row_ror8(u32x4 v) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_update_dpp(0u, v[i], 0x128, 0xF, 0xF, false);
+  return r;
+}
+
 __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
-  __shared__ uint32_t s_row[64];
-  __shared__ float s_mask[64];
+  __shared__ uint32_t s_row[kPart];
+  __shared__ float s_mask[kPart];
   const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
   const bool head_live = c < kGroup;
   const int head = kvh * kGroup + c;
-  // q as the B operand of QK^T: k-step s, lane group g holds dims 32s + 8g .. +7.
-  u32x4 qv[kD / 32];
-  {
-    const uint16_t *qr = p.q + (int64_t(b) * kHeads + (head_live ? head : 0)) * kD;
-#pragma unroll
-    for (int s = 0; s < kD / 32; ++s)
-      qv[s] = head_live ? load_u32x4(qr + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
-  }
   // Whole caches as buffers: rows are < 2^20, so byte offsets fit 32 bits.
   const auto rk = make_rsrc(p.keys + kvh * kD * 2, uint32_t(p.slots) * kRowBytes);
   const auto rv = make_rsrc(p.values + kvh * kD * 2, uint32_t(p.slots) * kRowBytes);
@@ -77,127 +79,166 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   const int t_begin = part * kPart;
   const int t_end = t_begin + kPart < p.context ? t_begin + kPart : p.context;
   const int64_t meta = int64_t(b) * p.context;
-  // (mask, row) of the lane's position in a 64-position chunk; the next chunk's
-  // pair is loaded while this chunk's rows are processed.
-  auto fetch = [&](int t0, float &mk, int64_t &row) {
-    const int t = t0 + lane;
-    mk = t < t_end ? p.mask[meta + t] : -INFINITY;
-    row = t < t_end ? p.table[meta + t] : 0;
-  };
-  float mk_next;
-  int64_t row_next;
-  fetch(t_begin, mk_next, row_next);
-  for (int t0 = t_begin; t0 < t_end; t0 += 64) {
-    const float mk = mk_next;
-    const int64_t row = row_next;
-    if (t0 + 64 < t_end) fetch(t0 + 64, mk_next, row_next);
-    const bool live = mk != -INFINITY && row >= 0 && row < p.slots;
+  // The partition's live positions (mask not -inf, row in range), in order, as
+  // an LDS list: every lane's four (mask, row) pairs are loaded before the first
+  // ballot.
+  float mk[kPart / 64];
+  int64_t rw[kPart / 64];
+#pragma unroll
+  for (int j = 0; j < kPart / 64; ++j) {
+    const int t = t_begin + 64 * j + lane;
+    mk[j] = t < t_end ? p.mask[meta + t] : -INFINITY;
+    rw[j] = t < t_end ? p.table[meta + t] : 0;
+  }
+  int n_live = 0;
+#pragma unroll
+  for (int j = 0; j < kPart / 64; ++j) {
+    const bool live = mk[j] != -INFINITY && rw[j] >= 0 && rw[j] < p.slots;
     const uint64_t ballot = __ballot(live);
-    const int n_live = __popcll(ballot);
-    if (n_live == 0) continue;
     if (live) {
-      const int at = __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
-                                               __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u));
-      s_row[at] = uint32_t(row);
-      s_mask[at] = mk * kLog2e;
+      const int at = n_live + __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u));
+      s_row[at] = uint32_t(rw[j]);
+      s_mask[at] = mk[j] * kLog2e;
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    for (int k0 = 0; k0 < n_live; k0 += 16) {
-      // K: lane (c, g) loads row k0 + c, dims 32s + 8g .. +7 for every k-step.
-      const bool kl = k0 + c < n_live;
-      // Padded rows read past the buffer (zeros): no stale value (NaN or inf)
-      // can reach the scores or the accumulator.
-      const uint32_t krow = kl ? s_row[k0 + c] * uint32_t(kRowBytes) : 0xFFFFFC00u;
-      u32x4 kv[kD / 32];
+    n_live += __popcll(ballot);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+  // q as the B operand of QK^T: k-step s, lane group g holds dims 32s + 8g .. +7.
+  u32x4 qv[kD / 32];
+  {
+    const uint16_t *qr = p.q + (int64_t(b) * kHeads + (head_live ? head : 0)) * kD;
 #pragma unroll
-      for (int s = 0; s < kD / 32; ++s) kv[s] = buf_load_x4(rk, krow + 64 * s + 16 * g);
-      // V: lane (c, g) loads rows k0 + 4g + j, dims 16c .. 16c + 15 (32 bytes).
-      uint32_t vw[4][8];
-      float xm[4];
+    for (int s = 0; s < kD / 32; ++s)
+      qv[s] = head_live && n_live > 0 ? load_u32x4(qr + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+  // Tile loads, every instruction reading whole 128-B lines (the vector L1
+  // tracks misses per line, and half-line loads spend twice the entries per
+  // byte). K: instruction (L, h) reads line L of rows k0 + 8h .. + 7, lane
+  // (c, g) taking 16-B chunk g + 4(c >> 3) of row k0 + (c & 7) + 8h; k-step s's
+  // operand (row k0 + c, dims 32s + 8g .. +7) is then the lane's own chunk or
+  // lane c ^ 8's (DPP row_ror:8). V: lane (c, g) reads rows k0 + 4g + j, dims
+  // 8c .. 8c + 7 and 128 + 8c .. 128 + 8c + 7 (16 lanes cover 256 B of a row).
+  // Padded rows read past the buffer (zeros), so no stale value (NaN or inf)
+  // can reach the scores or the accumulator, and a tile past the list issues
+  // no memory traffic.
+  auto row_off = [&](int e) { return e < n_live ? s_row[e] * uint32_t(kRowBytes) : 0xFFFFFC00u; };
+  u32x4 kv[kD / 32];
+  u32x4 vw[4][2];
+  auto load_k = [&](int k0) {
+    const uint32_t chunk = 16 * (g + 4 * (c >> 3));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = k0 + 4 * g + j;
-        const bool vl = e < n_live;
-        const uint32_t vrow = vl ? s_row[e] * uint32_t(kRowBytes) : 0xFFFFFC00u;
-        xm[j] = vl ? s_mask[e] : -INFINITY;
-        const u32x4 a = buf_load_x4(rv, vrow + 32 * c);
-        const u32x4 z = buf_load_x4(rv, vrow + 32 * c + 16);
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t krow = row_off(k0 + (c & 7) + 8 * h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vw[j][i] = a[i];
-          vw[j][4 + i] = z[i];
-        }
-      }
-      f32x4 sacc = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int s = 0; s < kD / 32; ++s) sacc = mfma16x16x32(kv[s], qv[s], sacc);
-      // Lane (c, g) holds the scores of rows k0 + 4g + r for head c.
-      float x[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = sacc[r] * sl2 + xm[r];
-      float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      tmax = max_xor16(tmax);
-      tmax = max_xor32(tmax);
-      if (tmax > m_run) {
-        const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax);
-        m_run = tmax;
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[i] *= alpha;
-      }
-      float pr[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pr[r] = m_run == -INFINITY ? 0.0f : fast_exp2(x[r] - m_run);
-      l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-      const u32x2 pb = u32x2{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])};
-      // PV: MFMA d gives O^T rows m = c <-> dim 16c + d for the lane's head.
-#pragma unroll
-      for (int d = 0; d < 16; ++d) {
-        const int w = d >> 1;
-        const u32x2 a = (d & 1) ? u32x2{pack_hi16(vw[0][w], vw[1][w]), pack_hi16(vw[2][w], vw[3][w])}
-                                : u32x2{pack_lo16(vw[0][w], vw[1][w]), pack_lo16(vw[2][w], vw[3][w])};
-        oacc[d] = mfma16x16x16(a, pb, oacc[d]);
-      }
+      for (int L = 0; L < kD / 64; ++L) kv[2 * L + h] = buf_load_x4<kPolicy>(rk, krow + 128 * L + chunk);
     }
-    __builtin_amdgcn_wave_barrier();  // the list is rewritten by the next chunk
+  };
+  auto load_v = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t vrow = row_off(k0 + 4 * g + j);
+      vw[j][0] = buf_load_x4<kPolicy>(rv, vrow + 16 * c);
+      vw[j][1] = buf_load_x4<kPolicy>(rv, vrow + 256 + 16 * c);
+    }
+  };
+  // Rolling prefetch: the next tile's K is issued as soon as QK^T has consumed
+  // this tile's K, and its V once PV has consumed this tile's V, so a tile's
+  // worth of rows stays in flight without a second set of registers.
+  if (n_live > 0) {
+    load_k(0);
+    load_v(0);
+  }
+  for (int k0 = 0; k0 < n_live; k0 += 16) {
+    f32x4 sacc = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < kD / 32; ++s) {
+      const u32x4 A = kv[s & ~1], B = kv[s | 1];
+      const bool lo = c < 8;
+      u32x4 op;
+      if ((s & 1) == 0) {
+        const u32x4 r = row_ror8(B);
+        op = u32x4{lo ? A[0] : r[0], lo ? A[1] : r[1], lo ? A[2] : r[2], lo ? A[3] : r[3]};
+      } else {
+        const u32x4 r = row_ror8(A);
+        op = u32x4{lo ? r[0] : B[0], lo ? r[1] : B[1], lo ? r[2] : B[2], lo ? r[3] : B[3]};
+      }
+      sacc = mfma16x16x32(op, qv[s], sacc);
+    }
+    load_k(k0 + 16);
+    // Lane (c, g) holds the scores of rows k0 + 4g + r for head c.
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int e = k0 + 4 * g + r;
+      x[r] = sacc[r] * sl2 + (e < n_live ? s_mask[e] : -INFINITY);
+    }
+    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    tmax = max_xor16(tmax);
+    tmax = max_xor32(tmax);
+    if (tmax > m_run) {
+      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax);
+      m_run = tmax;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[i] *= alpha;
+    }
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = m_run == -INFINITY ? 0.0f : fast_exp2(x[r] - m_run);
+    l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    const u32x2 pb = u32x2{pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])};
+    // PV: MFMA d gives O^T row m <-> dim 8m + d (d < 8) or 128 + 8m + d - 8.
+#pragma unroll
+    for (int d = 0; d < 16; ++d) {
+      const int w = (d >> 1) & 3, h = d >> 3;
+      const u32x2 a = (d & 1) ? u32x2{pack_hi16(vw[0][h][w], vw[1][h][w]), pack_hi16(vw[2][h][w], vw[3][h][w])}
+                              : u32x2{pack_lo16(vw[0][h][w], vw[1][h][w]), pack_lo16(vw[2][h][w], vw[3][h][w])};
+      oacc[d] = mfma16x16x16(a, pb, oacc[d]);
+    }
+    load_v(k0 + 16);
   }
   float l_tot = sum_xor16(l_run);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  // Lane (c, g) holds dims (4g + r) * 16 + d = 64g .. 64g + 63 of head c.
+  // Lane (c, g) holds two 32-dim runs of head c: dims 128u + 32g + e (e < 32)
+  // in oacc[8u + (e & 7)][e >> 3].
+  auto elem = [&](int u, int e) { return oacc[8 * u + (e & 7)][e >> 3]; };
   if (p.parts == 1) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    const int64_t o = (int64_t(b) * kHeads + head) * kD + 64 * g;
-    const uint16_t *gp = p.gate + o;
-    uint16_t *op = p.out + o;
+    const int64_t o = (int64_t(b) * kHeads + head) * kD + 32 * g;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {  // 8 dims per 16-byte store
-      const u32x4 gw = load_u32x4(gp + 8 * k);
-      u32x4 w;
+    for (int u = 0; u < 2; ++u) {
+      const uint16_t *gp = p.gate + o + 128 * u;
+      uint16_t *op = p.out + o + 128 * u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e0 = 8 * k + 2 * i, e1 = e0 + 1;
-        const float v0 = oacc[e0 & 15][e0 >> 4] * inv * bf16_bits_to_f32(gw[i] & 0xffffu);
-        const float v1 = oacc[e1 & 15][e1 >> 4] * inv * bf16_bits_to_f32(gw[i] >> 16);
-        w[i] = pack_bf16x2(v0, v1);
+      for (int k = 0; k < 4; ++k) {  // 8 dims per 16-byte store
+        const u32x4 gw = load_u32x4(gp + 8 * k);
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e0 = 8 * k + 2 * i;
+          w[i] = pack_bf16x2(elem(u, e0) * inv * bf16_bits_to_f32(gw[i] & 0xffffu),
+                             elem(u, e0 + 1) * inv * bf16_bits_to_f32(gw[i] >> 16));
+        }
+        store_u32x4(op + 8 * k, w);
       }
-      store_u32x4(op + 8 * k, w);
     }
   } else {
     const int64_t prow = (int64_t(b) * p.parts + part) * kHeads + head;
-    float *po = p.part_o + prow * kD + 64 * g;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      f32x4 v;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int e = 4 * k + i;
-        v[i] = oacc[e & 15][e >> 4];
-      }
-      *reinterpret_cast<f32x4 *>(po + 4 * k) = v;
-    }
     if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
+    // A partition without live positions leaves m = -inf, and the merge then
+    // never reads its O.
+    if (n_live == 0) return;
+    float *po = p.part_o + prow * kD + 32 * g;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<f32x4 *>(po + 128 * u + 4 * k) =
+            f32x4{elem(u, 4 * k), elem(u, 4 * k + 1), elem(u, 4 * k + 2), elem(u, 4 * k + 3)};
   }
 }
 
