@@ -42,6 +42,8 @@ constexpr int kPolicy = 2;
 // the nontemporal policy would fetch twice: default policy (measured 194
 // against 227 us per operator).
 constexpr int kKPolicy = 0;
+// Growth of a head's running max (log2 units) tolerated before rescaling.
+constexpr float kRescaleSlack = 8.0f;
 
 struct GatedParams {
   const uint16_t *q, *gate;
@@ -171,9 +173,13 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
     float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     tmax = max_xor16(tmax);
     tmax = max_xor32(tmax);
-    if (tmax > m_run) {
-      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - tmax);
-      m_run = tmax;
+    // Lazy rescale: the accumulators (held in AGPRs) are rescaled only when a
+    // head's max grows by more than 2^8, so probabilities stay below 2^8
+    // (exact enough for bf16 P) and most tiles skip the 64 multiplies.
+    if (__any(tmax > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - m_new);
+      m_run = m_new;
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < 16; ++i) oacc[i] *= alpha;
