@@ -25,6 +25,7 @@
 // launch combines and gates.
 #include "common.h"
 #include "ifattn_internal.h"
+#include "split_k.h"
 
 namespace ifattn {
 namespace {
@@ -44,6 +45,8 @@ constexpr int kPolicy = 2;
 constexpr int kKPolicy = 0;
 // Growth of a head's running max (log2 units) tolerated before rescaling.
 constexpr float kRescaleSlack = 8.0f;
+// Persistent decode waves per CU (two per SIMD: the kernel's register use).
+constexpr int kWavesPerCu = 8;
 
 struct GatedParams {
   const uint16_t *q, *gate;
@@ -53,8 +56,10 @@ struct GatedParams {
   uint16_t *out;
   float *part_o;   // [batch, parts, heads, D]
   float *part_ml;  // [batch, parts, heads, 2]
+  int32_t *live_parts;  // [batch, parts]: each request's partitions with a live position
+  int32_t *live_count;  // [batch]; both null for a one-partition context
   int64_t slots;
-  int context, parts;
+  int context, parts, batch;
 };
 
 // Lane c of a 16-lane row gets the value of lane (c + 8) % 16 (DPP row_ror:8).
@@ -65,10 +70,10 @@ __device__ __forceinline__ u32x4 row_ror8(u32x4 v) {
   return r;
 }
 
-__global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
-  __shared__ uint32_t s_row[kPart];
-  __shared__ float s_mask[kPart];
-  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+// One (request b, kv head kvh, partition part) item; s_row / s_mask hold the
+// wave's list of live positions.
+__device__ __forceinline__ void gated_item(const GatedParams &p, int part, int kvh, int b,
+                                           uint32_t *s_row, float *s_mask) {
   const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
   const bool head_live = c < kGroup;
   const int head = kvh * kGroup + c;
@@ -241,19 +246,105 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   }
 }
 
-// One workgroup of four waves per (request, head): combine the partitions'
-// (m, l, O), normalise, apply the gate. Wave w takes partitions w, w + 4, ...
-// (lane l owns dims 4l .. 4l + 3), eight partials in flight at a time, and
-// partitions without a live position (m = -inf) are skipped by their (m, l)
-// alone; the four waves' sums meet in LDS.
+// Live partitions of each request: workgroup b scans mask row b (1024 threads,
+// up to 32 positions each in flight) and lists, in order, the partitions with
+// at least one position whose mask is not -inf.
+constexpr int kMaxParts = 262144 / kPart;
+__global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
+  __shared__ uint32_t s_flag[kMaxParts];
+  __shared__ int s_wave[16];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < p.parts; i += 1024) s_flag[i] = 0u;
+  __syncthreads();
+  const float *m = p.mask + int64_t(b) * p.context;
+  constexpr int U = 32;
+  for (int t0 = 0; t0 < p.context; t0 += U * 1024) {
+    float x[U];
+#pragma unroll
+    for (int e = 0; e < U; ++e) {
+      const int t = t0 + e * 1024 + tid;
+      x[e] = t < p.context ? m[t] : -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < U; ++e)
+      if (x[e] != -INFINITY) s_flag[(t0 + e * 1024 + tid) / kPart] = 1u;
+  }
+  __syncthreads();
+  // Compaction in partition order: wave w owns partitions 64w + 1024r + lane.
+  int base = 0;
+  for (int r0 = 0; r0 < p.parts; r0 += 1024) {
+    const int i = r0 + tid;
+    const bool live = i < p.parts && s_flag[i] != 0u;
+    const uint64_t ballot = __ballot(live);
+    if (lane == 0) s_wave[w] = __popcll(ballot);
+    __syncthreads();
+    int before = base;
+    for (int u = 0; u < w; ++u) before += s_wave[u];
+    if (live)
+      p.live_parts[int64_t(b) * p.parts + before +
+                   __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u))] = i;
+    for (int u = 0; u < 16; ++u) base += s_wave[u];
+    __syncthreads();
+  }
+  if (tid == 0) p.live_count[b] = base;
+}
+
+// Persistent waves (kWavesPerCu per CU) over the live items: item k is kv head
+// k % 2 of the (k / 2)-th live partition in (request, partition) order, and
+// wave w takes items w, w + grid, ... Items are whole partitions and nearly
+// equal, so the static split is balanced, and the two kv heads of a partition
+// (the halves of the same 1024-B rows) are read by neighbouring waves at about
+// the same time. With one workgroup per (request, kv head, partition), most of
+// them without a live position on ragged batches, the dispatcher kept a third
+// of the wave slots busy and live items started up to 150 us late.
+// A one-partition context (no plan) runs one wave per (request, kv head).
+__global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
+  __shared__ uint32_t s_row[kPart];
+  __shared__ float s_mask[kPart];
+  if (!p.live_parts) {
+    gated_item(p, 0, int(blockIdx.x) % kKvHeads, int(blockIdx.x) / kKvHeads, s_row, s_mask);
+    return;
+  }
+  const int lane = threadIdx.x;
+  // Inclusive prefix of the live counts over requests (lane b = request b).
+  const int cnt = lane < p.batch ? p.live_count[lane] : 0;
+  int incl = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  const int total = kKvHeads * __builtin_amdgcn_readlane(incl, 63);
+  for (int k = blockIdx.x; k < total; k += gridDim.x) {
+    const int idx = k / kKvHeads;  // live partition index over all requests
+    const int b = __popcll(__ballot(incl <= idx));
+    const int j = idx - (__builtin_amdgcn_readlane(incl, b) - __builtin_amdgcn_readlane(cnt, b));
+    const int part = p.live_parts[int64_t(b) * p.parts + j];
+    gated_item(p, part, k % kKvHeads, b, s_row, s_mask);
+    // The next item rewrites the list this one read.
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  }
+}
+
+// One workgroup of four waves per (request, head): combine the live
+// partitions' (m, l, O), normalise, apply the gate. Wave w takes list entries
+// w, w + 4, ... (lane l owns dims 4l .. 4l + 3), eight partials in flight at a
+// time; a partition whose rows were all out of range (m = -inf) is skipped by
+// its (m, l) alone; the four waves' sums meet in LDS.
 __global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
   __shared__ float s_max[4], s_l[4];
   __shared__ f32x4 s_o[4][64];
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = p.live_count[b];
+  const int32_t *parts = p.live_parts + int64_t(b) * p.parts;
   const int64_t base = int64_t(b) * p.parts * kHeads + h;
-  auto ml_at = [&](int k) { return *reinterpret_cast<const float2 *>(p.part_ml + (base + int64_t(k) * kHeads) * 2); };
+  auto ml_at = [&](int part) {
+    return *reinterpret_cast<const float2 *>(p.part_ml + (base + int64_t(part) * kHeads) * 2);
+  };
   float mmax = -INFINITY;
-  for (int k = int(threadIdx.x); k < p.parts; k += 256) mmax = fmaxf(mmax, ml_at(k).x);
+  for (int k = int(threadIdx.x); k < n; k += 256) mmax = fmaxf(mmax, ml_at(parts[k]).x);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
   if (lane == 0) s_max[w] = mmax;
@@ -263,15 +354,16 @@ __global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
   float lsum = 0.0f;
   if (mmax != -INFINITY) {
     constexpr int U = 8;
-    for (int k0 = w; k0 < p.parts; k0 += 4 * U) {
+    for (int k0 = w; k0 < n; k0 += 4 * U) {
       float2 ml[U];
       f32x4 o[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int k = k0 + 4 * u;
-        ml[u] = k < p.parts ? ml_at(k) : make_float2(-INFINITY, 0.0f);
+        const int part = k < n ? parts[k] : 0;
+        ml[u] = k < n ? ml_at(part) : make_float2(-INFINITY, 0.0f);
         o[u] = ml[u].x != -INFINITY
-                   ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(k) * kHeads) * kD + 4 * lane)
+                   ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(part) * kHeads) * kD + 4 * lane)
                    : f32x4{0, 0, 0, 0};
       }
 #pragma unroll
@@ -326,7 +418,9 @@ extern "C" uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, i
   if (batch <= 0 || context <= 0) return 0;
   const uint64_t parts = uint64_t(parts_for(context));
   if (parts == 1) return 16;
-  return uint64_t(batch) * parts * kHeads * (kD + 2) * sizeof(float);
+  // Partials (O, then (m, l)), the live partition lists and their counts.
+  return uint64_t(batch) * parts * (kHeads * (kD + 2) * sizeof(float) + sizeof(int32_t)) +
+         align16(uint64_t(batch) * sizeof(int32_t));
 }
 
 extern "C" int32_t ifattn_gated_paged_attention_bf16(
@@ -359,13 +453,19 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
       return fail(IFATTN_EWORKSPACE, "gated paged attention: workspace missing, short or misaligned");
     p.part_o = static_cast<float *>(workspace);
     p.part_ml = p.part_o + uint64_t(batch) * p.parts * kHeads * kD;
+    p.live_parts = reinterpret_cast<int32_t *>(p.part_ml + uint64_t(batch) * p.parts * kHeads * 2);
+    p.live_count = p.live_parts + uint64_t(batch) * p.parts;
   }
+  p.batch = int(batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int vecs = int(batch) * (kRowBytes / 16) * 2;
   gated_append_kernel<<<(vecs + 255) / 256, 256, 0, s>>>(
       static_cast<const uint8_t *>(k), static_cast<const uint8_t *>(v),
       static_cast<uint8_t *>(keys), static_cast<uint8_t *>(values), append, int(batch), slots);
-  gated_decode_kernel<<<dim3(p.parts, kKvHeads, unsigned(batch)), 64, 0, s>>>(p);
+  const int items = p.parts * kKvHeads * int(batch);
+  const int waves = device_cus() * kWavesPerCu;
+  if (p.live_parts) gated_plan_kernel<<<unsigned(batch), 1024, 0, s>>>(p);
+  gated_decode_kernel<<<p.live_parts ? (items < waves ? items : waves) : items, 64, 0, s>>>(p);
   if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 256, 0, s>>>(p);
   return launch_status("gated paged attention");
 }
