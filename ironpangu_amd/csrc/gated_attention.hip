@@ -35,7 +35,8 @@ constexpr int kGroup = 4;         // q heads per kv head
 constexpr int kKvHeads = 2;
 constexpr int kHeads = kGroup * kKvHeads;
 constexpr int kRowBytes = kKvHeads * kD * 2;  // 1024 B per cache row
-constexpr int kPart = 256;        // context positions per partition
+constexpr int kPart = 256;        // largest partition (context positions)
+constexpr int kMinPart = 64;      // smallest partition
 constexpr float kScale = 0.0625f; // 1/sqrt(256), inferfabric_acl.cpp:1400
 // Cache-policy bits of the V row loads (2: nontemporal; rows are read once).
 constexpr int kPolicy = 2;
@@ -60,6 +61,7 @@ struct GatedParams {
   int32_t *live_count;  // [batch]; both null for a one-partition context
   int64_t slots;
   int context, parts, batch;
+  int part, part_shift;  // partition length (64, 128 or 256) and its log2
 };
 
 // Lane c of a 16-lane row gets the value of lane (c + 8) % 16 (DPP row_ror:8).
@@ -87,12 +89,12 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int k
   for (int i = 0; i < 16; ++i) oacc[i] = f32x4{0, 0, 0, 0};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const int t_begin = part * kPart;
-  const int t_end = t_begin + kPart < p.context ? t_begin + kPart : p.context;
+  const int t_begin = part * p.part;
+  const int t_end = t_begin + p.part < p.context ? t_begin + p.part : p.context;
   const int64_t meta = int64_t(b) * p.context;
   // The partition's live positions (mask not -inf, row in range), in order, as
-  // an LDS list: every lane's four (mask, row) pairs are loaded before the first
-  // ballot.
+  // an LDS list: every lane's (mask, row) pairs (four at the largest partition)
+  // are loaded before the first ballot.
   float mk[kPart / 64];
   int64_t rw[kPart / 64];
 #pragma unroll
@@ -233,9 +235,8 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int k
   } else {
     const int64_t prow = (int64_t(b) * p.parts + part) * kHeads + head;
     if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
-    // A partition without live positions leaves m = -inf, and the merge then
-    // never reads its O.
-    if (n_live == 0) return;
+    // Written even without a live row (zeros, m = -inf): the merge loads every
+    // listed partition's O alongside its (m, l).
     float *po = p.part_o + prow * kD + 32 * g;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -249,7 +250,7 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int k
 // Live partitions of each request: workgroup b scans mask row b (1024 threads,
 // up to 32 positions each in flight) and lists, in order, the partitions with
 // at least one position whose mask is not -inf.
-constexpr int kMaxParts = 262144 / kPart;
+constexpr int kMaxParts = 262144 / kMinPart;
 __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
   __shared__ uint32_t s_flag[kMaxParts];
   __shared__ int s_wave[16];
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
     }
 #pragma unroll
     for (int e = 0; e < U; ++e)
-      if (x[e] != -INFINITY) s_flag[(t0 + e * 1024 + tid) / kPart] = 1u;
+      if (x[e] != -INFINITY) s_flag[(t0 + e * 1024 + tid) >> p.part_shift] = 1u;
   }
   __syncthreads();
   // Compaction in partition order: wave w owns partitions 64w + 1024r + lane.
@@ -328,14 +329,16 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   }
 }
 
-// One workgroup of four waves per (request, head): combine the live
+// One workgroup of kMergeWaves waves per (request, head): combine the live
 // partitions' (m, l, O), normalise, apply the gate. Wave w takes list entries
-// w, w + 4, ... (lane l owns dims 4l .. 4l + 3), eight partials in flight at a
-// time; a partition whose rows were all out of range (m = -inf) is skipped by
-// its (m, l) alone; the four waves' sums meet in LDS.
-__global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
-  __shared__ float s_max[4], s_l[4];
-  __shared__ f32x4 s_o[4][64];
+// w, w + kMergeWaves, ... (lane l owns dims 4l .. 4l + 3), eight partials in
+// flight at a time (O is loaded with its (m, l), not after it; a partition
+// whose rows were all out of range has m = -inf, weight 0 and zero O); the
+// waves' sums meet in LDS.
+constexpr int kMergeWaves = 16;
+__global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedParams p) {
+  __shared__ float s_max[kMergeWaves], s_l[kMergeWaves];
+  __shared__ f32x4 s_o[kMergeWaves][64];
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int n = p.live_count[b];
   const int32_t *parts = p.live_parts + int64_t(b) * p.parts;
@@ -344,27 +347,28 @@ __global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
     return *reinterpret_cast<const float2 *>(p.part_ml + (base + int64_t(part) * kHeads) * 2);
   };
   float mmax = -INFINITY;
-  for (int k = int(threadIdx.x); k < n; k += 256) mmax = fmaxf(mmax, ml_at(parts[k]).x);
+  for (int k = int(threadIdx.x); k < n; k += 64 * kMergeWaves) mmax = fmaxf(mmax, ml_at(parts[k]).x);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
   if (lane == 0) s_max[w] = mmax;
   __syncthreads();
-  mmax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  mmax = s_max[0];
+#pragma unroll
+  for (int u = 1; u < kMergeWaves; ++u) mmax = fmaxf(mmax, s_max[u]);
   f32x4 acc = f32x4{0, 0, 0, 0};
   float lsum = 0.0f;
   if (mmax != -INFINITY) {
     constexpr int U = 8;
-    for (int k0 = w; k0 < n; k0 += 4 * U) {
+    for (int k0 = w; k0 < n; k0 += kMergeWaves * U) {
       float2 ml[U];
       f32x4 o[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int k = k0 + 4 * u;
+        const int k = k0 + kMergeWaves * u;
         const int part = k < n ? parts[k] : 0;
         ml[u] = k < n ? ml_at(part) : make_float2(-INFINITY, 0.0f);
-        o[u] = ml[u].x != -INFINITY
-                   ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(part) * kHeads) * kD + 4 * lane)
-                   : f32x4{0, 0, 0, 0};
+        o[u] = k < n ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(part) * kHeads) * kD + 4 * lane)
+                     : f32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -378,8 +382,13 @@ __global__ __launch_bounds__(256) void gated_merge_kernel(GatedParams p) {
   if (lane == 0) s_l[w] = lsum;
   __syncthreads();
   if (w != 0) return;
-  acc = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
-  lsum = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  acc = s_o[0][lane];
+  lsum = s_l[0];
+#pragma unroll
+  for (int u = 1; u < kMergeWaves; ++u) {
+    acc += s_o[u][lane];
+    lsum += s_l[u];
+  }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
   const int64_t o = (int64_t(b) * kHeads + h) * kD + 4 * lane;
   const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o);
@@ -407,7 +416,21 @@ __global__ __launch_bounds__(256) void gated_append_kernel(const uint8_t *k, con
               load_u32x4((val ? v : k) + (int64_t(r) * kVecs + c) * 16));
 }
 
-int parts_for(int64_t context) { return int((context + kPart - 1) / kPart); }
+// Partition length: 256 positions when the batch's partitions give at least
+// two items per wave slot of a full MI355X (256 CUs x kWavesPerCu), else 128,
+// else 64, so that small batches over long contexts still spread over the chip
+// (a wave's items run one after another, one tile latency at a time). A
+// function of (batch, context) only, so the workspace size follows it.
+int part_len(int64_t batch, int64_t context) {
+  constexpr int64_t kTarget = 2 * 256 * kWavesPerCu;
+  for (int len = kPart; len > kMinPart; len /= 2)
+    if (batch * ((context + len - 1) / len) * kKvHeads >= kTarget) return len;
+  return kMinPart;
+}
+int parts_for(int64_t batch, int64_t context) {
+  const int len = part_len(batch, context);
+  return int((context + len - 1) / len);
+}
 
 }  // namespace
 }  // namespace ifattn
@@ -416,7 +439,7 @@ using namespace ifattn;
 
 extern "C" uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, int64_t context) {
   if (batch <= 0 || context <= 0) return 0;
-  const uint64_t parts = uint64_t(parts_for(context));
+  const uint64_t parts = uint64_t(parts_for(batch, context));
   if (parts == 1) return 16;
   // Partials (O, then (m, l)), the live partition lists and their counts.
   return uint64_t(batch) * parts * (kHeads * (kD + 2) * sizeof(float) + sizeof(int32_t)) +
@@ -447,7 +470,9 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
   p.out = static_cast<uint16_t *>(out);
   p.slots = slots;
   p.context = int(context);
-  p.parts = parts_for(context);
+  p.parts = parts_for(batch, context);
+  p.part = part_len(batch, context);
+  p.part_shift = __builtin_ctz(unsigned(p.part));
   if (p.parts > 1) {
     if (!workspace || workspace_bytes < need || !aligned16(workspace))
       return fail(IFATTN_EWORKSPACE, "gated paged attention: workspace missing, short or misaligned");
@@ -466,6 +491,6 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
   const int waves = device_cus() * kWavesPerCu;
   if (p.live_parts) gated_plan_kernel<<<unsigned(batch), 1024, 0, s>>>(p);
   gated_decode_kernel<<<p.live_parts ? (items < waves ? items : waves) : items, 64, 0, s>>>(p);
-  if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 256, 0, s>>>(p);
+  if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 64 * kMergeWaves, 0, s>>>(p);
   return launch_status("gated paged attention");
 }
