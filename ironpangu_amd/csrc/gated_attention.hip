@@ -13,16 +13,21 @@
 // product. Accumulation is fp32 (scores, softmax, PV); the reference rounds
 // scores and probabilities to bf16 between its ACLNN calls.
 //
-// Kernel: one wave per (request, kv head, 256-position partition). The wave
-// reads 64 (mask, index) pairs at a time, one per lane, and compacts the
-// positions that can contribute (mask not -inf, index in range) into an LDS
-// list by ballot; masked positions cost 12 bytes of metadata and no cache
-// traffic. Live rows are processed 16 at a time: QK^T as MFMA 16x16x32 bf16
-// (A = the 16 rows' K slices straight from HBM, B = the group's four q heads),
-// the score tile feeding PV directly as the B operand of MFMA 16x16x16 (A = V
-// rows, 32 bytes of dims per lane and row), online softmax in the exp2 domain.
-// Requests over several partitions write (m, l, O) partials that a merge
-// launch combines and gates.
+// Launches (one stream): append the step's rows; plan (one workgroup per
+// request lists the partitions of 64/128/256 positions holding a position whose
+// mask is not -inf); decode (persistent waves, eight per CU, take the live
+// (partition, kv head) items round-robin); merge (per request and head, the
+// live partitions' (m, l, O), normalised and gated). A one-partition context
+// skips plan and merge.
+//
+// Decode item: the wave loads the partition's (mask, index) pairs and compacts
+// the positions that can contribute (mask not -inf, index in range) into an
+// LDS list by ballot. Live rows are processed 16 at a time, the next tile's
+// rows loaded while this tile is computed: QK^T as MFMA 16x16x32 bf16 (A = the
+// 16 rows' K straight from HBM, moved into the operand layout with ds_bpermute;
+// B = the group's four q heads), the score tile feeding PV directly as the B
+// operand of MFMA 16x16x16 (A = V rows), online softmax in the exp2 domain with
+// lazy rescale.
 #include "common.h"
 #include "ifattn_internal.h"
 #include "split_k.h"
@@ -257,18 +262,22 @@ __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   for (int i = tid; i < p.parts; i += 1024) s_flag[i] = 0u;
   __syncthreads();
-  const float *m = p.mask + int64_t(b) * p.context;
+  // Unconditional buffer loads (zeros past the row; the position test comes
+  // after the load), so all U loads of a thread are in flight together.
+  const auto rm = make_rsrc(p.mask + int64_t(b) * p.context, uint32_t(p.context) * 4u);
   constexpr int U = 32;
   for (int t0 = 0; t0 < p.context; t0 += U * 1024) {
     float x[U];
 #pragma unroll
+    for (int e = 0; e < U; ++e) x[e] = buf_load_f32(rm, uint32_t(t0 + e * 1024 + tid) * 4u);
+    // A wave's 64 positions lie in one partition (partitions are 64-aligned
+    // multiples of 64): one flag store per wave, not one per lane (same-address
+    // LDS stores from many lanes serialise).
+#pragma unroll
     for (int e = 0; e < U; ++e) {
       const int t = t0 + e * 1024 + tid;
-      x[e] = t < p.context ? m[t] : -INFINITY;
+      if (__ballot(t < p.context && x[e] != -INFINITY) != 0 && lane == 0) s_flag[t >> p.part_shift] = 1u;
     }
-#pragma unroll
-    for (int e = 0; e < U; ++e)
-      if (x[e] != -INFINITY) s_flag[(t0 + e * 1024 + tid) >> p.part_shift] = 1u;
   }
   __syncthreads();
   // Compaction in partition order: wave w owns partitions 64w + 1024r + lane.
@@ -330,64 +339,72 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
 }
 
 // One workgroup of kMergeWaves waves per (request, head): combine the live
-// partitions' (m, l, O), normalise, apply the gate. Wave w takes list entries
-// w, w + kMergeWaves, ... (lane l owns dims 4l .. 4l + 3), eight partials in
-// flight at a time (O is loaded with its (m, l), not after it; a partition
-// whose rows were all out of range has m = -inf, weight 0 and zero O); the
-// waves' sums meet in LDS.
+// partitions' (m, l, O) in one online pass, normalise, apply the gate. Wave w
+// takes list entries w, w + kMergeWaves, ...: their partition ids are loaded
+// 64 at a time, one per lane, and read back with v_readlane, so each round of
+// eight partials ((m, l) with O, lane l owning dims 4l .. 4l + 3) costs one
+// memory round trip. A partition whose rows were all out of range has m = -inf,
+// weight 0 and zero O. The waves' (m, l, O) meet in LDS.
 constexpr int kMergeWaves = 16;
 __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedParams p) {
-  __shared__ float s_max[kMergeWaves], s_l[kMergeWaves];
+  __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
   __shared__ f32x4 s_o[kMergeWaves][64];
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int n = p.live_count[b];
   const int32_t *parts = p.live_parts + int64_t(b) * p.parts;
   const int64_t base = int64_t(b) * p.parts * kHeads + h;
-  auto ml_at = [&](int part) {
-    return *reinterpret_cast<const float2 *>(p.part_ml + (base + int64_t(part) * kHeads) * 2);
-  };
-  float mmax = -INFINITY;
-  for (int k = int(threadIdx.x); k < n; k += 64 * kMergeWaves) mmax = fmaxf(mmax, ml_at(parts[k]).x);
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) mmax = wave_max_xor(mmax, m);
-  if (lane == 0) s_max[w] = mmax;
-  __syncthreads();
-  mmax = s_max[0];
-#pragma unroll
-  for (int u = 1; u < kMergeWaves; ++u) mmax = fmaxf(mmax, s_max[u]);
+  float m_run = -INFINITY, l_run = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
-  float lsum = 0.0f;
-  if (mmax != -INFINITY) {
-    constexpr int U = 8;
-    for (int k0 = w; k0 < n; k0 += kMergeWaves * U) {
+  constexpr int U = 8;
+  for (int k0 = w; k0 < n; k0 += kMergeWaves * 64) {
+    const int kk = k0 + kMergeWaves * lane;
+    const int my_part = kk < n ? parts[kk] : 0;
+    const int cnt = (n - k0 + kMergeWaves - 1) / kMergeWaves < 64 ? (n - k0 + kMergeWaves - 1) / kMergeWaves : 64;
+    for (int u0 = 0; u0 < cnt; u0 += U) {
       float2 ml[U];
       f32x4 o[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int k = k0 + kMergeWaves * u;
-        const int part = k < n ? parts[k] : 0;
-        ml[u] = k < n ? ml_at(part) : make_float2(-INFINITY, 0.0f);
-        o[u] = k < n ? *reinterpret_cast<const f32x4 *>(p.part_o + (base + int64_t(part) * kHeads) * kD + 4 * lane)
-                     : f32x4{0, 0, 0, 0};
+        const int i = u0 + u;
+        const int64_t r = base + int64_t(__builtin_amdgcn_readlane(my_part, i < 64 ? i : 63)) * kHeads;
+        ml[u] = i < cnt ? *reinterpret_cast<const float2 *>(p.part_ml + r * 2) : make_float2(-INFINITY, 0.0f);
+        o[u] = i < cnt ? *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane) : f32x4{0, 0, 0, 0};
       }
+      float mx = m_run;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, ml[u].x);
+      if (mx == -INFINITY) continue;
+      const float sc = m_run == -INFINITY ? 0.0f : fast_exp2(m_run - mx);
+      m_run = mx;
+      l_run *= sc;
+      acc *= sc;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float wt = ml[u].x == -INFINITY ? 0.0f : fast_exp2(ml[u].x - mmax);
-        lsum += wt * ml[u].y;
+        const float wt = ml[u].x == -INFINITY ? 0.0f : fast_exp2(ml[u].x - mx);
+        l_run += wt * ml[u].y;
         acc += wt * o[u];
       }
     }
   }
   s_o[w][lane] = acc;
-  if (lane == 0) s_l[w] = lsum;
+  if (lane == 0) {
+    s_m[w] = m_run;
+    s_l[w] = l_run;
+  }
   __syncthreads();
   if (w != 0) return;
-  acc = s_o[0][lane];
-  lsum = s_l[0];
+  float mmax = s_m[0];
 #pragma unroll
-  for (int u = 1; u < kMergeWaves; ++u) {
-    acc += s_o[u][lane];
-    lsum += s_l[u];
+  for (int u = 1; u < kMergeWaves; ++u) mmax = fmaxf(mmax, s_m[u]);
+  acc = f32x4{0, 0, 0, 0};
+  float lsum = 0.0f;
+  if (mmax != -INFINITY) {
+#pragma unroll
+    for (int u = 0; u < kMergeWaves; ++u) {
+      const float wt = s_m[u] == -INFINITY ? 0.0f : fast_exp2(s_m[u] - mmax);
+      acc += wt * s_o[u][lane];
+      lsum += wt * s_l[u];
+    }
   }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
   const int64_t o = (int64_t(b) * kHeads + h) * kD + 4 * lane;
