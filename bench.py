@@ -819,6 +819,9 @@ def main():
                    "head_dim": case.head_dim, "block_size": case.block_size,
                    "pool_blocks": case.pool_blocks, "parallelism": "none (1 GPU)"},
         "tokens_per_s": round(case.num_seqs / (ms_step * 1e-3), 1),
+        # Per-step distribution: each step bracketed by its own event pair.
+        "step_ms_median": round(float(np.median(attn_ms)), 5),
+        "step_ms_p95": round(float(np.percentile(attn_ms, 95)), 5),
         "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_step": nbytes["total"],
         "roofline": {"bound": "hbm", "kernel": "paged_decode_step operator (prologue: plan + row writes; decode; split-K merge)",
