@@ -15,8 +15,6 @@ HQ, HKV, D = 8, 2, 256
 
 
 def _run(seed, batch, context, slots, holes=0.0, finite_mask=False):
-    import torch
-    from ironpangu_amd import ops
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, context + 1, batch)
     lens[0] = context
@@ -31,6 +29,14 @@ def _run(seed, batch, context, slots, holes=0.0, finite_mask=False):
     if finite_mask:  # finite additive biases on live positions
         mask = np.where(live, rng.uniform(-4, 1, (batch, context)), -np.inf).astype(np.float32)
     append = rows[np.arange(batch), lens - 1].copy()
+    _check(rng, rows, mask, append, slots)
+
+
+def _check(rng, rows, mask, append, slots):
+    """Run the operator on random caches/q/k/v/gate and compare with the oracle."""
+    import torch
+    from ironpangu_amd import ops
+    batch = rows.shape[0]
     keys = W.bf16_randn(rng, (slots, HKV * D))
     values = W.bf16_randn(rng, (slots, HKV * D))
     q = W.bf16_randn(rng, (batch, HQ, D))
@@ -51,16 +57,52 @@ def _run(seed, batch, context, slots, holes=0.0, finite_mask=False):
     assert_close(got, exp, what="gated attention")
 
 
-@pytest.mark.parametrize("batch,context,holes,finite", [(3, 700, 0.0, False),     # one partition
-                                                        (7, 3000, 0.0, False),    # three partitions
+# Partition lengths follow (batch, context): 64 positions for these small
+# calls (one partition for context <= 64), 256 for the ragged batch below.
+@pytest.mark.parametrize("batch,context,holes,finite", [(3, 50, 0.0, False),      # one partition
+                                                        (3, 700, 0.0, False),     # 11 partitions
+                                                        (7, 3000, 0.0, False),
                                                         (5, 2500, 0.3, True),     # holes + biases
                                                         (64, 129, 0.5, False)])   # batch 64
 def test_gated_attention(batch, context, holes, finite):
     _run(batch * 1000 + context, batch, context, batch * context + 17, holes, finite)
 
 
+def test_gated_attention_ragged_batch_256_position_partitions():
+    # 16 requests over a 32768-position table, live lengths log-uniform
+    # [128, 32768] (the benchmark's shape at a quarter of its batch): 256-position
+    # partitions, most of them without a live position. Rows drawn from a
+    # 65536-row pool (repeats allowed); the appended rows are distinct rows
+    # outside it.
+    rng = np.random.default_rng(77)
+    batch, context, pool = 16, 32768, 65536
+    lens = W.lengths(rng, batch, 128, context, "loguniform")
+    lens[0] = context
+    rows = rng.integers(0, pool, (batch, context)).astype(np.int64)
+    append = pool + np.arange(batch, dtype=np.int64)
+    rows[np.arange(batch), lens - 1] = append
+    mask = np.where(np.arange(context)[None, :] < lens[:, None], 0.0, -np.inf).astype(np.float32)
+    _check(rng, rows, mask, append, pool + batch)
+
+
+def test_gated_attention_live_positions_after_dead_partitions():
+    # live windows that start deep in the table: whole leading partitions have
+    # no live position, and one request's only live positions are its last 3
+    rng = np.random.default_rng(78)
+    batch, context = 4, 9000
+    slots = batch * context + 5
+    rows = rng.permutation(slots)[: batch * context].reshape(batch, context).astype(np.int64)
+    pos = np.arange(context)
+    starts = np.array([5000, 64, 8997, 1234])
+    ends = np.array([9000, 300, 9000, 7000])
+    live = (pos[None, :] >= starts[:, None]) & (pos[None, :] < ends[:, None])
+    mask = np.where(live, 0.0, -np.inf).astype(np.float32)
+    append = rows[np.arange(batch), ends - 1].copy()
+    _check(rng, rows, mask, append, slots)
+
+
 def test_gated_attention_long_context():
-    # 4 requests over 65536 positions (64 partitions, merged), 2^18 + 3 slots
+    # 4 requests over 65536 positions (512 partitions of 128, merged), 2^18 + 3 slots
     _run(42, 4, 65536, (1 << 18) + 3)
 
 
