@@ -57,6 +57,8 @@ def parse():
                     help="only measure the HBM read ceiling (64 KiB blocks over an 8.6 GB footprint)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip configs 3-5 (reported under 'secondary')")
+    ap.add_argument("--only", choices=sorted(SECONDARY),
+                    help="run one secondary workload alone and print its JSON (profiling)")
     return ap.parse_args()
 
 
@@ -588,7 +590,7 @@ def bench_gated(seed, steps, warmup):
                        "table, live lengths log-uniform [128, 32768]",
            "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
            "live_positions": live,
-           "roofline": {"bound": "hbm", "kernel": "gated paged attention operator (append, attention, merge)",
+           "roofline": {"bound": "hbm", "kernel": "gated paged attention operator (plan + row append, decode, merge)",
                         "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
                         "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
                         "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes}}
@@ -724,6 +726,22 @@ def read_ceiling(steps, sweep=False):
     return out
 
 
+# Secondary workloads, in report order.
+SECONDARY = {
+    "c8_decode": bench_c8,
+    "mla_decode": bench_mla,
+    "mla_decode_c8": bench_mla_c8,
+    "gqa_decode_hd256": bench_decode_hd256,
+    "gqa_decode_page16": bench_decode_page16,
+    "mixed_prefill_decode": bench_mixed,
+    "gated_attention_qwen": bench_gated,
+    "mla_window_attention": lambda seed, steps, warmup: bench_mla_rows(seed, steps, warmup, False),
+    "mla_sparse_attention": lambda seed, steps, warmup: bench_mla_rows(seed, steps, warmup, True),
+    "slot_reuse": bench_slot_reuse,
+    "norm_rope_write": bench_norm_rope_write,
+}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -734,6 +752,10 @@ def main():
     import torch
     from ironpangu_amd import ops
     from ironpangu_amd import workloads as W
+
+    if args.only:
+        print(json.dumps({args.only: SECONDARY[args.only](args.seed, args.steps, args.warmup)}))
+        return
 
     if args.read_ceiling:
         print(json.dumps(read_ceiling(max(args.steps, 5), sweep=True)))
@@ -840,17 +862,8 @@ def main():
     if not args.no_secondary:
         del t
         torch.cuda.empty_cache()
-        res["secondary"] = {"c8_decode": bench_c8(args.seed, args.steps, args.warmup),
-                            "mla_decode": bench_mla(args.seed, args.steps, args.warmup),
-                            "mla_decode_c8": bench_mla_c8(args.seed, args.steps, args.warmup),
-                            "gqa_decode_hd256": bench_decode_hd256(args.seed, args.steps, args.warmup),
-                            "gqa_decode_page16": bench_decode_page16(args.seed, args.steps, args.warmup),
-                            "mixed_prefill_decode": bench_mixed(args.seed, args.steps, args.warmup),
-                            "gated_attention_qwen": bench_gated(args.seed, args.steps, args.warmup),
-                            "mla_window_attention": bench_mla_rows(args.seed, args.steps, args.warmup, False),
-                            "mla_sparse_attention": bench_mla_rows(args.seed, args.steps, args.warmup, True),
-                            "slot_reuse": bench_slot_reuse(args.seed, args.steps, args.warmup),
-                            "norm_rope_write": bench_norm_rope_write(args.seed, args.steps, args.warmup)}
+        res["secondary"] = {name: fn(args.seed, args.steps, args.warmup)
+                            for name, fn in SECONDARY.items()}
     print(json.dumps(res), flush=True)
 
 

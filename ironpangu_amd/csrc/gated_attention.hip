@@ -13,12 +13,12 @@
 // product. Accumulation is fp32 (scores, softmax, PV); the reference rounds
 // scores and probabilities to bf16 between its ACLNN calls.
 //
-// Launches (one stream): append the step's rows; plan (one workgroup per
-// request lists the partitions of 64/128/256 positions holding a position whose
-// mask is not -inf); decode (persistent waves, eight per CU, take the live
+// Launches (one stream): plan (one workgroup per request appends the step's
+// rows and lists the partitions of 64/128/256 positions holding a position
+// whose mask is not -inf); decode (persistent waves, eight per CU, take the live
 // (partition, kv head) items round-robin); merge (per request and head, the
 // live partitions' (m, l, O), normalised and gated). A one-partition context
-// skips plan and merge.
+// runs an append launch in place of the plan, and no merge.
 //
 // Decode item: the wave loads the partition's (mask, index) pairs and compacts
 // the positions that can contribute (mask not -inf, index in range) into an
@@ -64,6 +64,10 @@ struct GatedParams {
   float *part_ml;  // [batch, parts, heads, 2]
   int32_t *live_parts;  // [batch, parts]: each request's partitions with a live position
   int32_t *live_count;  // [batch]; both null for a one-partition context
+  // The step's rows (appended by the plan kernel when there is one).
+  const uint8_t *k_new, *v_new;
+  const int64_t *append;
+  uint8_t *keys_out, *values_out;
   int64_t slots;
   int context, parts, batch;
   int part, part_shift;  // partition length (64, 128 or 256) and its log2
@@ -260,6 +264,16 @@ __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
   __shared__ uint32_t s_flag[kMaxParts];
   __shared__ int s_wave[16];
   const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // Append request b's step row (K by threads 0-63, V by 64-127, 16 B each)
+  // before the decode launch reads the caches.
+  if (tid < 2 * (kRowBytes / 16)) {
+    const int64_t slot = p.append[b];
+    const bool val = tid >= kRowBytes / 16;
+    const int c = val ? tid - kRowBytes / 16 : tid;
+    if (slot >= 0 && slot < p.slots)
+      store_u32x4((val ? p.values_out : p.keys_out) + (slot * (kRowBytes / 16) + c) * 16,
+                  load_u32x4((val ? p.v_new : p.k_new) + (int64_t(b) * (kRowBytes / 16) + c) * 16));
+  }
   for (int i = tid; i < p.parts; i += 1024) s_flag[i] = 0u;
   __syncthreads();
   // Unconditional buffer loads (zeros past the row; the position test comes
@@ -500,13 +514,20 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
   }
   p.batch = int(batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int vecs = int(batch) * (kRowBytes / 16) * 2;
-  gated_append_kernel<<<(vecs + 255) / 256, 256, 0, s>>>(
-      static_cast<const uint8_t *>(k), static_cast<const uint8_t *>(v),
-      static_cast<uint8_t *>(keys), static_cast<uint8_t *>(values), append, int(batch), slots);
+  p.k_new = static_cast<const uint8_t *>(k);
+  p.v_new = static_cast<const uint8_t *>(v);
+  p.append = append;
+  p.keys_out = static_cast<uint8_t *>(keys);
+  p.values_out = static_cast<uint8_t *>(values);
   const int items = p.parts * kKvHeads * int(batch);
   const int waves = device_cus() * kWavesPerCu;
-  if (p.live_parts) gated_plan_kernel<<<unsigned(batch), 1024, 0, s>>>(p);
+  if (p.live_parts) {
+    gated_plan_kernel<<<unsigned(batch), 1024, 0, s>>>(p);  // appends the step's rows too
+  } else {
+    const int vecs = int(batch) * (kRowBytes / 16) * 2;
+    gated_append_kernel<<<(vecs + 255) / 256, 256, 0, s>>>(p.k_new, p.v_new, p.keys_out,
+                                                            p.values_out, append, int(batch), slots);
+  }
   gated_decode_kernel<<<p.live_parts ? (items < waves ? items : waves) : items, 64, 0, s>>>(p);
   if (p.parts > 1) gated_merge_kernel<<<dim3(unsigned(batch), kHeads), 64 * kMergeWaves, 0, s>>>(p);
   return launch_status("gated paged attention");
