@@ -9,12 +9,13 @@
 // (grouping kh = h / (q_heads/kv_heads) at :226). slot(b,j) = table[b][j/bs]*bs + j%bs
 // (native/src/page_binding.h:56-59).
 //
-// Work decomposition: a prologue kernel lists (sequence, partition) items
-// longest first; a persistent grid (two workgroups per CU) pulls them from a
-// device queue:
-//  * a workgroup owns a `part_tokens` slice of one sequence; each of its waves
-//    owns one kv head, so the two waves of a 2-kv-head model stream the two
-//    halves of the same 512-byte cache rows at the same time;
+// Work decomposition: a prologue kernel cuts the call's tokens (plus a start
+// cost per sequence) into equal contiguous shares, one per worker; a
+// persistent grid (two workgroups per CU) walks them:
+//  * a workgroup owns the tile range of one share within one sequence at a
+//    time; each of its waves owns one kv head, so the two waves of a
+//    2-kv-head model stream the two halves of the same 512-byte cache rows at
+//    the same time;
 //  * a wave walks 32-token tiles (16-token tiles at head_dim 256). QK^T is one
 //    MFMA 16x16x32 bf16 per (16 tokens, 32 dims): A = K rows straight from HBM
 //    (16 B per lane; bf16 loads cover whole 128-B lines and one DPP lane
@@ -29,9 +30,9 @@
 //    with v_perm, so V is never staged or transposed through LDS;
 //  * online softmax in the exp2 domain with lazy rescaling; max/sum across
 //    the four lane groups by permlane swaps;
-//  * sequences longer than one partition write (m, l, unnormalised O) partials
-//    and a second kernel merges them (split-K); single-partition sequences
-//    write bf16 output directly.
+//  * sequences spread over several shares write (m, l, unnormalised O)
+//    partials and a second kernel merges them (split-K); a sequence inside one
+//    share writes bf16 output directly.
 //  * a register ring of decode_stages() tiles keeps the next tiles' loads in
 //    flight while the current tile is reduced.
 // C8: K/V int8 with an fp32 scale per (token, kv head). int8 -> bf16 is exact,
@@ -142,13 +143,13 @@ __device__ __forceinline__ int block_at(const LaneBlocks &lb, int i) {  // i wav
 // second half are then relative to the second page (see decode_item).
 template <int D, bool C8, bool SP>
 __device__ __forceinline__ void load_tile(TileRegs<D, C8> &t, const DecodeParams &p,
-                                          const LaneBlocks &lane_blocks, int t_begin, int kvh,
+                                          const LaneBlocks &lane_blocks, int win0, int kvh,
                                           int t0, int t_end, const LaneOffsets &o) {
   constexpr int EB = C8 ? 1 : 2;  // element bytes
   constexpr int TT = TileRegs<D, C8>::TT;
   constexpr bool SPLIT = SP && TT == 32;
   const int bs = p.block_size;
-  const int idx = (t0 - (t_begin & ~(bs - 1))) / bs;
+  const int idx = t0 / bs - win0;  // lane of the tile's block id in the window
   const int blk = block_at<SP>(lane_blocks, idx);
   const int64_t tok0 = int64_t(blk) * bs + (t0 & (bs - 1));
   const int n_live = t_end - t0 < TT ? t_end - t0 : TT;
@@ -253,24 +254,15 @@ __device__ __forceinline__ int i8_at(uint32_t w, int b) {
 // are rescaled; probabilities then stay below 2^8, exact enough for bf16 P.
 constexpr float kRescaleSlack = 8.0f;
 
+// Tokens [t_begin, t_end) of sequence seq (t_begin a multiple of 32) for kv
+// head kvh; writes the output
+// (slot < 0: the range is the whole sequence) or partial slot `slot`.
 template <int D, bool C8, bool SP>
-__device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int part, int kvh,
-                                            int lane) {
-  const int len = clamp_len(p, seq);
-  const int PT = p.part_tokens;
-  const int nparts = parts_of(len, PT);
+__device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int t_begin, int t_end,
+                                            int slot, int kvh, int lane) {
   const int c = lane & 15, g = lane >> 4;
   const int head = kvh * p.group + c;
   const bool head_live = c < p.group;
-
-  if (len <= 0) {  // no visible key: defined zero output
-    if (head_live) {
-#pragma unroll
-      for (int d0 = 8 * g; d0 < D; d0 += 32)
-        store_u32x4(p.out + (q_row_of(p, seq) * p.q_heads + head) * D + d0, u32x4{0, 0, 0, 0});
-    }
-    return;
-  }
 
   // B operand of QK^T: q[head][d0(s, g) + e], zero for padded heads.
   u32x4 qv[D / 32];
@@ -305,17 +297,21 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
       o.sc[j] = uint32_t(row) * p.kv_heads * 4;
     }
   }
-  const int t_begin = part * PT;
-  const int t_end = t_begin + PT < len ? t_begin + PT : len;
+  // Block ids of a window of 64 blocks (128 with 16-token pages) from block
+  // win0 of the sequence, one per lane; the window slides (one vector load)
+  // when a tile to be issued leaves it, so a range may span any number of
+  // blocks.
   LaneBlocks lane_blocks{0, 0};
-  {
-    const int first = t_begin / p.block_size;
-    const int nblk = (t_end - 1) / p.block_size - first + 1;  // <= 64, or 128 with SP (host-checked)
-    const int32_t *row = p.block_tables + int64_t(seq) * p.table_stride + first;
+  constexpr int kWin = SP ? 128 : 64;
+  const int32_t *table_row = p.block_tables + int64_t(seq) * p.table_stride;
+  const int nblk_end = (t_end - 1) / p.block_size + 1;  // blocks up to the range end
+  int win0 = t_begin / p.block_size;
+  auto load_window = [&]() {
     auto clamp = [&](int b) { return b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b); };
-    lane_blocks.lo = clamp(lane < nblk ? row[lane] : 0);
-    if constexpr (SP) lane_blocks.hi = clamp(lane + 64 < nblk ? row[lane + 64] : 0);
-  }
+    lane_blocks.lo = clamp(win0 + lane < nblk_end ? table_row[win0 + lane] : 0);
+    if constexpr (SP) lane_blocks.hi = clamp(win0 + lane + 64 < nblk_end ? table_row[win0 + lane + 64] : 0);
+  };
+  load_window();
 
   constexpr int NV = D / 16;  // PV MFMAs per tile (each yields 16 dims x 16 heads)
   f32x4 oacc[NV];
@@ -419,20 +415,26 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   };
 
   // Ring of kStages tile buffers: tiles t+1 .. t+kStages-1 are in flight while
-  // tile t is reduced. Tiles past the partition end reload the last tile (a
-  // cache hit) so every iteration has the same shape.
+  // tile t is reduced. Tiles past the range end reload the last tile (a cache
+  // hit) so every iteration has the same shape. Tiles are issued in order, so
+  // the block-id window only moves forward.
   constexpr int kStages = decode_stages<D>();
   TileRegs<D, C8> tr[kStages];
   auto clamp_tile = [&](int t) { return t < t_end ? t : t_end - 1 - ((t_end - 1 - t_begin) & (TT - 1)); };
+  auto issue = [&](TileRegs<D, C8> &t, int t0) {
+    if ((t0 + TT - 1) / p.block_size - win0 >= kWin) {
+      win0 = t0 / p.block_size;
+      load_window();
+    }
+    load_tile<D, C8, SP>(t, p, lane_blocks, win0, kvh, t0, t_end, o);
+  };
 #pragma unroll
-  for (int i = 0; i < kStages - 1; ++i)
-    load_tile<D, C8, SP>(tr[i], p, lane_blocks, t_begin, kvh, clamp_tile(t_begin + i * TT), t_end, o);
+  for (int i = 0; i < kStages - 1; ++i) issue(tr[i], clamp_tile(t_begin + i * TT));
   int t0 = t_begin;
   while (true) {
 #pragma unroll
     for (int i = 0; i < kStages; ++i) {
-      load_tile<D, C8, SP>(tr[(i + kStages - 1) % kStages], p, lane_blocks, t_begin, kvh,
-                       clamp_tile(t0 + (kStages - 1) * TT), t_end, o);
+      issue(tr[(i + kStages - 1) % kStages], clamp_tile(t0 + (kStages - 1) * TT));
       // Keep the prefetch issued ahead of this tile's math (the scheduler would
       // otherwise sink it below the QK^T MFMAs and shrink the loads in flight).
       __builtin_amdgcn_sched_barrier(0);
@@ -456,7 +458,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 #pragma unroll
     for (int b = 0; b < VPL; ++b) ov[r * VPL + b] = oacc[b][r];
   auto chunk_dim = [&](int k) { return 4 * g * VPL + 8 * k; };
-  if (nparts == 1) {
+  if (slot < 0) {
     const float inv = 1.0f / l_tot;
     uint16_t *op = p.out + (q_row_of(p, seq) * p.q_heads + head) * D;
 #pragma unroll
@@ -468,7 +470,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
                                            pack_bf16x2(v[6] * inv, v[7] * inv)});
     }
   } else {
-    const int64_t prow = (int64_t(seq) * p.max_parts + part) * p.q_heads + head;
+    const int64_t prow = int64_t(slot) * p.q_heads + head;
     float *po = p.part_o + prow * D;
 #pragma unroll
     for (int k = 0; k < D / 32; ++k) {
@@ -480,40 +482,54 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   }
 }
 
-// Persistent decode: each workgroup pulls (sequence, partition, kv-head group)
-// items from the queue built by the prologue kernel until it is exhausted. The
-// waves of a workgroup take the kv heads of one item, so the halves of every
-// cache row are fetched by sibling waves at the same time (whole rows stay
-// DRAM-page friendly; measured ~40% more bandwidth than independent waves).
+// Persistent decode: workgroup b takes workers b, b + grid, ...; worker v owns
+// the work units [v share, (v + 1) share), i.e. the 32-token tiles j of
+// sequence s with seq_pos[s] + seq_cost + 32 j in that range, walked from
+// start_seq[v] in sequence order. The waves of a workgroup take the kv heads of
+// one range, so the halves of every cache row are fetched by sibling waves at
+// the same time (whole rows stay DRAM-page friendly; measured ~40% more
+// bandwidth than independent waves). Every workgroup gets the same work; the
+// former longest-first work queue left half of them idle for the last third of
+// a config-2 step (a full 2048-token item at its end) and serialised 512
+// same-address atomics at the start.
 template <int D, bool C8, bool SP>
 __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kernel(
     DecodeParams p, int waves_per_wg) {
-  __shared__ int item_slot;
   const int lane = threadIdx.x & 63, wave = uniform(int(threadIdx.x >> 6));
   const int groups = (p.kv_heads + waves_per_wg - 1) / waves_per_wg;
-  const int total = p.queue[1] * groups;
-  // Every item, the first included, comes from the queue. (Handing the first
-  // item out by workgroup index and popping the next one at item start was
-  // measured slower here: 337.8 against 334.6 us per config-2 step.)
-  while (true) {
-    if (threadIdx.x == 0) item_slot = atomicAdd(p.queue, 1);
-    __syncthreads();
-    const int it = uniform(item_slot);
-    __syncthreads();
-    if (it >= total) break;
-    const uint32_t e = uniform(p.items[it / groups]);
-    const int seq = int(e >> 12);
-    const int kvh = uniform((it % groups) * waves_per_wg + wave);  // wave-uniform for SGPR descriptors
-    if (kvh < p.kv_heads) decode_item<D, C8, SP>(p, seq, int(e & 0xfffu), kvh, lane);
+  const int workers = uniform(p.plan[0]);
+  const int64_t share = share_of(p);
+  for (int v = blockIdx.x; v < workers; v += gridDim.x) {
+    const int64_t lo = int64_t(v) * share, hi = lo + share;
+    for (int seq = uniform(p.start_seq[v]); seq < p.num_seqs; ++seq) {
+      const int64_t first = p.seq_pos[seq] + p.seq_cost;  // unit of tile 0
+      if (first >= hi) break;
+      if (!decode_seq(p, seq)) continue;
+      const int len = uniform(clamp_len(p, seq));
+      if (len <= 0) continue;
+      const int tiles = (len + kSplitTile - 1) / kSplitTile;
+      const int64_t a = lo - first, b = hi - first;
+      const int j0 = a <= 0 ? 0 : int((a + kSplitTile - 1) / kSplitTile);
+      int j1 = b <= 0 ? 0 : int((b + kSplitTile - 1) / kSplitTile);
+      j1 = j1 < tiles ? j1 : tiles;
+      if (j0 >= j1) continue;
+      int slot = uniform(p.seq_slot[seq]);
+      if (slot >= 0) slot += v - int(first / share);
+      const int t_end = j1 * kSplitTile < len ? j1 * kSplitTile : len;
+      for (int grp = 0; grp < groups; ++grp) {
+        const int kvh = uniform(grp * waves_per_wg + wave);  // wave-uniform for SGPR descriptors
+        if (kvh < p.kv_heads) decode_item<D, C8, SP>(p, seq, j0 * kSplitTile, t_end, slot, kvh, lane);
+      }
+    }
   }
 }
 
 namespace {
 template <int D, bool C8>
 void launch_decode(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
-  launch_prologue(p, wr, s);  // p.static_items = 0: the queue hands out every item
+  launch_prologue(p, wr, s);
   const int waves = p.kv_heads < max_decode_waves(D) ? p.kv_heads : max_decode_waves(D);
-  const int grid = device_cus() * wgs_per_cu();
+  const int grid = p.grid;
   if (p.block_size == 16)  // the reference's bf16 page (paged_state_contract.h:25)
     paged_decode_kernel<D, C8, true><<<grid, 64 * waves, 0, s>>>(p, waves);
   else
@@ -552,7 +568,6 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   if (max_context <= 0 || num_blocks <= 0 || table_stride <= 0 ||
       int64_t(table_stride) * block_size < max_context)
     return fail(IFATTN_EINVAL, "paged decode: table_stride * block_size must cover max_context");
-  // Work items pack (sequence << 12 | partition) into 32 bits.
   if (num_seqs >= (1 << 20))
     return fail(IFATTN_EINVAL, "paged decode: num_seqs must be below 2^20");
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache))
@@ -574,12 +589,8 @@ int32_t decode_common(bool c8, const void *q, const void *k_cache, const void *v
   p.table_stride = table_stride;
   p.block_size = block_size;
   p.max_context = max_context;
-  p.part_tokens = part_tokens(c8);
-  p.max_parts = max_parts_for(max_context, c8);
   p.scale_log2 = scale * kLog2e;
-  if (p.max_parts > 4096) return fail(IFATTN_EINVAL, "paged decode: max_context above 1M tokens");
-  if (p.part_tokens > (block_size == 16 ? 128 : 64) * block_size)
-    return fail(IFATTN_EINVAL, "paged decode: partition spans more than 64 blocks (128 of 16 tokens)");
+  if (max_context > (1 << 20)) return fail(IFATTN_EINVAL, "paged decode: max_context above 1M tokens");
   const uint64_t need = ifattn_paged_decode_workspace_size(num_seqs, q_heads, head_dim, max_context);
   if (!workspace || workspace_bytes < need || !aligned16(workspace))
     return fail(IFATTN_EWORKSPACE, "paged decode: workspace missing, short or misaligned");

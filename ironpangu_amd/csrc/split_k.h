@@ -1,15 +1,24 @@
-// Split-K scheduling shared by the paged decode kernels (GQA and MLA):
-// per-call device work list in longest-processing-time order, a work queue
-// drained by persistent workgroups, (m, l, O) partials per (sequence,
-// partition, head) combined by a merge launch. The prologue kernel that builds
-// the work list also performs the step's slot-mapped row writes, so a decode
-// step is prologue -> decode -> merge from one host call.
+// Split-K scheduling of the paged GQA decode, and pieces shared with the MLA
+// and prefill planners. The decode splits the call's work into equal
+// contiguous shares: every decode sequence weighs its tokens plus a fixed
+// start cost, the prologue kernel prefix-sums the weights on the device and
+// cuts the total into `workers` shares of `share` units (one per persistent
+// workgroup, fewer for small calls), and the workgroups walk their shares tile
+// by tile. A sequence lying in one share writes its output
+// directly; one spread over several shares writes an (m, l, O) partial per
+// share into consecutive slots, which a merge launch combines. No work queue,
+// no atomics; all workgroups get the same work. The prologue kernel also
+// performs the step's slot-mapped row writes, so a decode step is prologue ->
+// decode -> merge from one host call.
 #pragma once
 #include <cstdlib>
 
 #include "common.h"
 
 namespace ifattn {
+
+// Tokens per unit of the split: shares end on 32-token tile boundaries.
+constexpr int kSplitTile = 32;
 
 struct DecodeParams {
   const uint16_t *q;
@@ -20,18 +29,22 @@ struct DecodeParams {
   const int32_t *block_tables;
   const int32_t *seq_lens;
   uint16_t *out;
-  int32_t *queue;    // [0] next item (atomic), [1] item count; set by the plan kernel
-  uint32_t *items;   // (seq << 12 | part) per (sequence, partition), in sequence order
-  float *part_o;     // [num_seqs, max_parts, q_heads, D]
-  float *part_ml;    // [num_seqs, max_parts, q_heads, 2]
+  // Written by the prologue: plan[0] = workers, plan[2..3] = share (int64
+  // units per worker).
+  int32_t *plan;
+  int64_t *seq_pos;    // [num_seqs] first work unit of each sequence
+  int32_t *seq_slot;   // [num_seqs] first partial slot of a sequence over several shares, else -1
+  int32_t *start_seq;  // [grid] first sequence not wholly before each worker's share
+  float *part_o;       // [2 * grid, q_heads, D]
+  float *part_ml;      // [2 * grid, q_heads, 2]
   // Packed varlen batches: when set, sequence s reads/writes q/out row
   // cu_seqlens[s+1]-1 and only sequences with exactly one query row are
   // scheduled here (longer chunks go to the prefill kernel).
   const int32_t *cu_seqlens;
   int64_t num_blocks;
-  int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_context, max_parts,
-      part_tokens;
-  int static_items;  // items below this index are not queued (0: the queue hands out every item)
+  int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_context, head_dim;
+  int seq_cost;      // work units charged per sequence on top of its tokens
+  int grid;          // persistent decode workgroups (the most workers)
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -39,13 +52,22 @@ __device__ __forceinline__ int clamp_len(const DecodeParams &p, int seq) {
   const int len = p.seq_lens[seq];
   return len > p.max_context ? p.max_context : len;
 }
-__device__ __forceinline__ int parts_of(int len, int pt) { return len > 0 ? (len + pt - 1) / pt : 1; }
 // q / out row of a sequence (identity for plain decode batches).
 __device__ __forceinline__ int64_t q_row_of(const DecodeParams &p, int seq) {
   return p.cu_seqlens ? int64_t(p.cu_seqlens[seq + 1]) - 1 : int64_t(seq);
 }
 __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
   return !p.cu_seqlens || p.cu_seqlens[seq + 1] - p.cu_seqlens[seq] == 1;
+}
+__device__ __forceinline__ int64_t share_of(const DecodeParams &p) {
+  return *reinterpret_cast<const int64_t *>(p.plan + 2);
+}
+// Workers holding the first and the last tile of a sequence whose tile 0 sits
+// at work unit `first` (tile j at first + 32 j).
+__device__ __forceinline__ void seq_workers(int64_t first, int len, int64_t share, int &wa, int &wb) {
+  const int tiles = (len + kSplitTile - 1) / kSplitTile;
+  wa = int(first / share);
+  wb = int((first + int64_t(kSplitTile) * (tiles - 1)) / share);
 }
 
 // Exclusive prefix of bucket[0..nb] (nb < 64 * PL) offset by `start`, by the
@@ -80,13 +102,6 @@ __device__ __forceinline__ int bucket_prefix(int *bucket, int nb, int start, int
   return total;
 }
 
-// Builds the compact work list on the device (graph-safe: lengths are read at
-// run time) and resets the work queue. Longest-processing-time order: every
-// full partition first, then the partial tail partitions by decreasing length
-// (a counting sort over 32-token buckets), so the last items pulled from the
-// queue are the shortest and the persistent workgroups finish together.
-// Sequences with no visible key get one zero-length item at the very end.
-// One workgroup of 1024 threads.
 // Slot-mapped row writes folded into the prologue (cache[slot[r]] = rows[r]).
 struct RowWrite {
   const uint8_t *k_rows, *v_rows;
@@ -113,72 +128,119 @@ __device__ __forceinline__ void prologue_write(const RowWrite &w) {
   }
 }
 
-// Workgroup 0 plans; workgroups 1.. perform the row writes (if any).
+// Smallest share the plan cuts (units): tiny calls use fewer workers instead of
+// spreading every sequence over many one-tile shares.
+constexpr int64_t kMinShareUnits = 512;
+
+// Workgroup-wide inclusive scan (sum or max) of one value per thread, 1024
+// threads: shuffles within the wave, wave totals through LDS. Returns the
+// inclusive value; *total gets the workgroup's total.
+template <typename T, bool MAX>
+__device__ __forceinline__ T block_scan(T x, T *wave_tot, T *total) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T y = __shfl_up(x, off, 64);
+    if (lane >= off) x = MAX ? (y > x ? y : x) : x + y;
+  }
+  if (lane == 63) wave_tot[wv] = x;
+  __syncthreads();
+  T before = MAX ? T(-1) : T(0), all = MAX ? T(-1) : T(0);
+  for (int w = 0; w < 16; ++w) {
+    const T t = wave_tot[w];
+    if (w < wv) before = MAX ? (t > before ? t : before) : before + t;
+    all = MAX ? (t > all ? t : all) : all + t;
+  }
+  __syncthreads();  // wave_tot is reused by the next scan
+  *total = all;
+  return MAX ? (before > x ? before : x) : before + x;
+}
+
+// Workgroup 0 plans the split; workgroups 1.. perform the row writes (if any).
+// Pass 1: weights (tokens + seq_cost for a decode sequence with keys, 0
+// otherwise) -> seq_pos by an exclusive scan; sequences without a visible key
+// get their defined zero output here. Then workers = grid, fewer for small
+// calls (at least kMinShareUnits per worker), and share = ceil(total /
+// workers). Pass 2: a
+// sequence whose first and last tiles fall in different shares gets
+// consecutive partial slots (one per share it touches); start_seq[v] = the
+// first sequence whose last tile lies in share v or later.
 template <int Unused = 0>
 __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, RowWrite wr) {
   if (blockIdx.x > 0) {
     prologue_write(wr);
     return;
   }
-  constexpr int kBuckets = 257;  // 32-token buckets of PT <= 8192, plus empty rows
-  __shared__ int bucket[kBuckets];
-  __shared__ int carry;
+  __shared__ long long s_tot64[16];
+  __shared__ int s_tot32[16];
+  __shared__ long long s_pos, s_share;
+  __shared__ int s_slot, s_emax, s_workers;
+  __shared__ int s_incl[1024];
   const int tid = threadIdx.x;
-  const int PT = p.part_tokens;
-  const int nb = PT / 32;  // bucket b holds remainders in (PT - 32(b+1), PT - 32b]
-  for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
-  if (tid == 0) carry = 0;
+  if (tid == 0) {
+    s_pos = 0;
+    s_slot = 0;
+    s_emax = -1;
+  }
   __syncthreads();
-  // Pass 1: full partitions in sequence order; histogram of partial ones.
-  __shared__ int wave_tot[16];
-  const int lane = tid & 63, wv = tid >> 6;
   for (int base = 0; base < p.num_seqs; base += 1024) {
     const int seq = base + tid;
-    int nfull = 0, bk = -1;
-    if (seq < p.num_seqs && decode_seq(p, seq)) {
-      const int len = clamp_len(p, seq);
-      nfull = len > 0 ? len / PT : 0;
-      const int rem = len > 0 ? len - nfull * PT : 0;
-      bk = len <= 0 ? nb : (rem > 0 ? (PT - rem) / 32 : -1);
-      if (bk >= 0) atomicAdd(&bucket[bk], 1);
+    const bool dec = seq < p.num_seqs && decode_seq(p, seq);
+    const int len = dec ? clamp_len(p, seq) : 0;
+    if (dec && len <= 0) {  // no visible key: defined zero output
+      uint16_t *o = p.out + q_row_of(p, seq) * p.q_heads * p.head_dim;
+      for (int i = 0; i < p.q_heads * p.head_dim; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
     }
-    // inclusive scan of nfull: within the wave by shuffles, then across waves
-    int x = nfull;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(x, off, 64);
-      x += lane >= off ? y : 0;
-    }
-    if (lane == 63) wave_tot[wv] = x;
+    const long long w = len > 0 ? (long long)len + p.seq_cost : 0;
+    long long tot;
+    const long long incl = block_scan<long long, false>(w, s_tot64, &tot);
+    if (seq < p.num_seqs) p.seq_pos[seq] = s_pos + incl - w;
     __syncthreads();
-    int before = carry;
-    for (int w2 = 0; w2 < wv; ++w2) before += wave_tot[w2];
-    const int start = before + x - nfull;
-    for (int k = 0; k < nfull; ++k) p.items[start + k] = (uint32_t(seq) << 12) | uint32_t(k);
-    __syncthreads();
-    if (tid == 1023) carry = start + nfull;
+    if (tid == 0) s_pos += tot;
     __syncthreads();
   }
-  // Exclusive scan of the bucket counts, offset by the full-item count.
-  {
-    const int run = bucket_prefix(bucket, nb, carry, tid);
+  if (tid == 0) {
+    const long long total = s_pos;
+    const long long small = (total + kMinShareUnits - 1) / kMinShareUnits;
+    long long workers = small < p.grid ? small : p.grid;
+    workers = workers < 1 ? 1 : workers;
+    const long long share = total > 0 ? (total + workers - 1) / workers : 1;
+    s_workers = int(workers);
+    s_share = share;
+    p.plan[0] = int(workers);
+    *reinterpret_cast<int64_t *>(p.plan + 2) = share;
+  }
+  __syncthreads();
+  const long long share = s_share;
+  for (int base = 0; base < p.num_seqs; base += 1024) {
+    const int seq = base + tid;
+    const bool dec = seq < p.num_seqs && decode_seq(p, seq);
+    const int len = dec ? clamp_len(p, seq) : 0;
+    int cnt = 0, e = -1;
+    if (len > 0) {
+      int wa, wb;
+      seq_workers(p.seq_pos[seq] + p.seq_cost, len, share, wa, wb);
+      cnt = wb > wa ? wb - wa + 1 : 0;
+      e = wb;
+    }
+    int tot;
+    const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
+    if (seq < p.num_seqs) p.seq_slot[seq] = cnt > 0 ? s_slot + incl - cnt : -1;
+    int emax;
+    s_incl[tid] = block_scan<int, true>(e, s_tot32, &emax);
+    __syncthreads();
+    // Largest last-tile worker of the sequences before this one.
+    int prev = tid > 0 ? s_incl[tid - 1] : -1;
+    prev = prev > s_emax ? prev : s_emax;
+    for (int v = prev + 1; v <= e; ++v) p.start_seq[v] = seq;
+    __syncthreads();
     if (tid == 0) {
-      p.queue[0] = p.static_items;
-      p.queue[1] = run;
+      s_slot += tot;
+      s_emax = emax > s_emax ? emax : s_emax;
     }
+    __syncthreads();
   }
-  __syncthreads();
-  // Pass 2: place each partial / empty item in its bucket.
-  for (int base = 0; base < p.num_seqs; base += 1024) {
-    const int seq = base + tid;
-    if (seq < p.num_seqs && decode_seq(p, seq)) {
-      const int len = clamp_len(p, seq);
-      const int nfull = len > 0 ? len / PT : 0;
-      const int rem = len > 0 ? len - nfull * PT : 0;
-      const int bk = len <= 0 ? nb : (rem > 0 ? (PT - rem) / 32 : -1);
-      if (bk >= 0) p.items[atomicAdd(&bucket[bk], 1)] = (uint32_t(seq) << 12) | uint32_t(nfull);
-    }
-  }
+  for (int v = s_emax + 1 + tid; v < s_workers; v += 1024) p.start_seq[v] = p.num_seqs;
 }
 
 // Merge the split-K partials of one (sequence, head) over the dims
@@ -187,13 +249,13 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
 // every partial-O slice is loaded before any is used; the weights reach the
 // other lanes by shuffle. Longer lists are taken kFast at a time.
 template <int D, int DW>
-__device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h, int nparts,
-                                           int dim0, int lane) {
+__device__ __forceinline__ void merge_head(const DecodeParams &p, int seq, int h, int slot0,
+                                           int nparts, int dim0, int lane) {
   constexpr int V = DW / 64;
   constexpr int kFast = 16;
-  // This sequence's partials: partition k, head h is row k * q_heads + h.
-  // Buffer offsets stay 32-bit and rows past nparts read as zero.
-  const int64_t seq_row = int64_t(seq) * p.max_parts * p.q_heads;
+  // This sequence's partials: share k (slot slot0 + k), head h is row
+  // k * q_heads + h. Buffer offsets stay 32-bit and rows past nparts read as zero.
+  const int64_t seq_row = int64_t(slot0) * p.q_heads;
   const uint32_t rows = uint32_t(nparts) * uint32_t(p.q_heads);
   const auto ro = make_rsrc(p.part_o + seq_row * D, rows * D * 4u);
   const auto rm = make_rsrc(p.part_ml + seq_row * 2, rows * 8u);
@@ -264,46 +326,21 @@ __global__ __launch_bounds__(256) void split_k_merge_kernel(DecodeParams p) {
   constexpr int DW = D < 128 ? D : 128;  // dims per wave
   const int seq = blockIdx.x, h = blockIdx.y;
   if (!decode_seq(p, seq)) return;
-  const int nparts = parts_of(clamp_len(p, seq), p.part_tokens);
-  if (nparts <= 1) return;
-  merge_head<D, DW>(p, seq, h, nparts, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
+  const int slot0 = p.seq_slot[seq];
+  if (slot0 < 0) return;  // the sequence lies in one share: output written by the decode
+  int wa, wb;
+  seq_workers(p.seq_pos[seq] + p.seq_cost, clamp_len(p, seq), share_of(p), wa, wb);
+  merge_head<D, DW>(p, seq, h, slot0, wb - wa + 1, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
 }
 
 // One workgroup per (sequence, head); one wave per 128 output dims.
 template <int D>
 inline void launch_merge(const DecodeParams &p, hipStream_t s) {
-  if (p.max_parts <= 1) return;
   constexpr int waves = D > 128 ? D / 128 : 1;
   split_k_merge_kernel<D><<<dim3(p.num_seqs, p.q_heads), 64 * waves, 0, s>>>(p);
 }
 
 constexpr uint64_t kQueueBytes = 64;
-
-// Tokens per split-K partition (a multiple of the 32-token tile): 2048 for
-// bf16 caches, 1536 for C8 caches. The longest-first list ends with the
-// partial partitions filling the workgroups' tails, and how well they fit
-// depends on the partition size: C8 over 256 sequences of U[1024, 16384]
-// tokens measured 234 us at 1536 against 253 us at 1024, 2048, 3072 and 4096;
-// bf16 over log-uniform [128, 32768] measured 2048 and 1792 alike, 1216 and
-// 2560 slower. The IFATTN_DECODE_PART_TOKENS environment variable overrides
-// both for tuning.
-inline int part_tokens(bool c8 = false) {
-  static int v = [] {
-    const char *e = getenv("IFATTN_DECODE_PART_TOKENS");
-    int x = e ? atoi(e) : 0;
-    return (x >= 32 && x <= 8192 && x % 32 == 0) ? x : 0;
-  }();
-  return v ? v : (c8 ? 1536 : 2048);
-}
-
-inline int max_parts_for(int max_context, bool c8 = false) {
-  return (max_context + part_tokens(c8) - 1) / part_tokens(c8);
-}
-// Partition count the workspace is sized for (either cache type).
-inline int max_parts_any(int max_context) {
-  const int a = max_parts_for(max_context, false), b = max_parts_for(max_context, true);
-  return a > b ? a : b;
-}
 
 inline uint64_t align16(uint64_t x) { return (x + 15) & ~uint64_t(15); }
 
@@ -333,24 +370,42 @@ inline int wgs_per_cu() {
   return v;
 }
 
-
-// Workspace layout: queue words | items | partial O | partial (m, l).
-inline uint64_t split_k_workspace_bytes(int num_seqs, int heads, int dims, int max_context) {
-  const uint64_t items = uint64_t(num_seqs) * uint64_t(max_parts_any(max_context));
-  const uint64_t partials = items > uint64_t(num_seqs)  // single-partition calls keep no partials
-                                ? items * heads * (uint64_t(dims) + 2) * sizeof(float)
-                                : 0;
-  return kQueueBytes + align16(items * 4) + partials;
+// Work units charged per sequence on top of its tokens: the item start of a
+// decode workgroup (q and block-id loads, the first tiles' latency) costs about
+// as much as streaming this many tokens. IFATTN_DECODE_SEQ_COST overrides it.
+inline int decode_seq_cost() {
+  static int v = [] {
+    const char *e = getenv("IFATTN_DECODE_SEQ_COST");
+    const int x = e ? atoi(e) : -1;
+    return (x >= 0 && x <= 65536) ? x : 64;
+  }();
+  return v;
 }
+inline int decode_grid() { return device_cus() * wgs_per_cu(); }
+
+// Workspace layout: plan words | seq_pos | seq_slot | start_seq | partial O |
+// partial (m, l); a sequence over k shares uses k slots, at most 2 per worker.
+inline uint64_t split_k_workspace_bytes(int num_seqs, int heads, int dims, int /*max_context*/) {
+  const uint64_t workers = uint64_t(decode_grid());
+  return kQueueBytes + align16(uint64_t(num_seqs) * 8) + align16(uint64_t(num_seqs) * 4) +
+         align16(workers * 4) + 2 * workers * heads * (uint64_t(dims) + 2) * sizeof(float);
+}
+// Fills the split fields of p (num_seqs set) and binds the workspace.
 inline void split_k_bind_workspace(DecodeParams &p, void *workspace, int heads, int dims) {
+  p.seq_cost = decode_seq_cost();
+  p.grid = decode_grid();
+  p.head_dim = dims;
   uint8_t *w = static_cast<uint8_t *>(workspace);
-  const uint64_t items = uint64_t(p.num_seqs) * p.max_parts;
-  p.queue = reinterpret_cast<int32_t *>(w);
+  p.plan = reinterpret_cast<int32_t *>(w);
   w += kQueueBytes;
-  p.items = reinterpret_cast<uint32_t *>(w);
-  w += align16(items * 4);
+  p.seq_pos = reinterpret_cast<int64_t *>(w);
+  w += align16(uint64_t(p.num_seqs) * 8);
+  p.seq_slot = reinterpret_cast<int32_t *>(w);
+  w += align16(uint64_t(p.num_seqs) * 4);
+  p.start_seq = reinterpret_cast<int32_t *>(w);
+  w += align16(uint64_t(p.grid) * 4);
   p.part_o = reinterpret_cast<float *>(w);
-  p.part_ml = p.part_o + items * heads * dims;
+  p.part_ml = p.part_o + uint64_t(2 * p.grid) * heads * dims;
 }
 
 // Prologue launch: planning workgroup plus enough writer workgroups for `wr`.

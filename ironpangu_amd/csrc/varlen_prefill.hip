@@ -536,11 +536,7 @@ extern "C" int32_t ifattn_varlen_prefill_bf16(const void *q, const void *k_cache
   d.table_stride = table_stride;
   d.block_size = block_size;
   d.max_context = max_kv_len;
-  d.part_tokens = part_tokens();
-  d.max_parts = max_parts_for(max_kv_len);
   d.scale_log2 = scale * kLog2e;
-  if (d.part_tokens > 64 * block_size)
-    return fail(IFATTN_EINVAL, "varlen prefill: decode partition spans more than 64 blocks");
   split_k_bind_workspace(d, workspace, q_heads, head_dim);
 
   PrefillParams p{};

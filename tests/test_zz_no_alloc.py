@@ -59,10 +59,11 @@ def test_noalloc_step_matches_workspace_step(order):
 def test_noalloc_step_rejects_calls_beyond_the_scratch():
     from ironpangu_amd._native import lib
     l = lib()
-    # 4096 sequences over 128k tokens need far more than 32 MiB of partials
-    need = l.ifattn_paged_decode_workspace_size(4096, 16, 128, 131072)
+    # partials for 128 q heads of 256 dims (two shares per persistent workgroup)
+    # take far more than 32 MiB
+    need = l.ifattn_paged_decode_workspace_size(64, 128, 256, 4096)
     assert need > (32 << 20)
     a = 0x10000
-    st = l.ifattn_paged_decode_step_bf16_noalloc(a, a, a, a, a, a, 5, 4096, a, 1024, a, a, 4096,
-                                                 16, 2, 128, 128, 1 << 20, 131072, 0.1, None)
+    st = l.ifattn_paged_decode_step_bf16_noalloc(a, a, a, a, a, a, 5, 64, a, 32, a, a, 64,
+                                                 128, 8, 256, 128, 1 << 20, 4096, 0.1, None)
     assert st == -1 and b"32 MiB" in l.ifattn_last_error()
