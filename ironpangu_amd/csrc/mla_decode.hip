@@ -58,19 +58,22 @@ struct MlaParams {
   const uint16_t *sink_k;       // [n_sinks, 576] bf16 or null
   const uint16_t *sink_v;       // [n_sinks, 512] bf16
   uint16_t *out;                // [rows, heads, 512]
-  int32_t *queue;               // [0] next item (atomic), [1] item count
-  uint32_t *items;              // (row << 12 | partition)
-  int32_t *row_seq;             // [rows] sequence of each row (plan output)
-  int32_t *row_pt;              // [rows] partition size of each row (plan output)
-  int32_t *row_slot;            // [rows] first partial slot of each row (plan output)
+  // Plan outputs: plan[0] = workers, plan[2..3] = share (int64 work units).
+  int32_t *plan;
+  int64_t *row_pos;             // [rows] first work unit of each row
+  int32_t *row_seq;             // [rows] sequence of each row
+  int32_t *row_slot;            // [rows] first partial slot, -1: the row writes its output directly
+  int32_t *start_row;           // [max_workers] first row not wholly before each worker's share
   float *part_o;                // [slots, heads, 512]
   float *part_ml;               // [slots, heads, 2]
   int64_t num_blocks;
   uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
-  int static_items;      // items 0..static_items-1 go to workgroups by index; the queue starts after
   int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks;
-  int part_tokens;   // largest partition the plan may pick (row_pt holds the chosen one)
-  int items_per_wg;  // plan target: items per persistent workgroup
+  int row_cost;     // work units charged per row start
+  int sink_units;   // work units of a row's sink block (0 without sinks)
+  int max_share;    // largest share: sparse segments fit the kSparsePart slot list
+  int max_workers;  // workers the workspace holds
+  int grid;         // persistent attention workgroups
   float scale_log2;
 };
 
@@ -111,146 +114,122 @@ __device__ __forceinline__ MlaSpan mla_span(const MlaParams &p, int row, int seq
   }
   return s;
 }
-// Partition field of a row's sink item. With sinks a row has at most 4095
-// partition slots, the last for the sinks, so partitions stay below it.
-constexpr uint32_t kSinkItem = 0xFFFu;
-
-__device__ __forceinline__ int mla_parts(const MlaSpan &s, int pt) {
-  return s.hi > s.lo ? (s.hi - s.base + pt - 1) / pt : 0;
+// Tiles of a row's keys (32-key tiles from `base`).
+__device__ __forceinline__ int mla_tiles(const MlaSpan &s) {
+  return s.hi > s.lo ? (s.hi - s.base + kMlaTile - 1) / kMlaTile : 0;
 }
-__device__ __forceinline__ int mla_part_size(const MlaSpan &s, int pt, int k) {
-  const int a = s.base + k * pt, b = a + pt;
-  return (s.hi < b ? s.hi : b) - (s.lo > a ? s.lo : a);
-}
-
-// Smallest partition the plan picks (a row shorter than this is one item).
-constexpr int kMinPart = 256;
-
-// Work list on the device (graph-safe: lengths are read at run time). The
-// partition size adapts to the call: with T keys over all rows and W
-// persistent workgroups it is S = T / (items_per_wg * W) keys (32-multiple,
-// clamped to [kMinPart, part_tokens]); rows are cut into partitions of S keys
-// from their tile-aligned start, the last one shorter. Items go out in
-// longest-processing-time order (counting sort over 32-key buckets): the full
-// partitions, then the shorter last ones, which fill the tail; rows without
-// keys last, sink items after every partition item. (Cutting each row into
-// equal parts instead measured slower: no short pieces are left for the
-// tail.) Also records each row's sequence, partition size and first partial
-// slot (the sink partial first, when there are sinks, then the partitions;
-// rows are packed by a scan, so at most items_per_wg * W + rows * (partitions
-// at part_tokens + 1) slots are used). One workgroup of 1024 threads.
-__global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
-  constexpr int kBuckets = 257;
-  __shared__ int bucket[kBuckets];
-  __shared__ int carry_full, carry_slot, sink_base, part_sh;
-  __shared__ unsigned long long total_keys;
-  __shared__ int wave_full[16], wave_slot[16];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int SMAX = p.part_tokens;
-  const int nb = SMAX / 32;  // bucket b: sizes in (SMAX - 32(b+1), SMAX - 32b]; nb: no keys
+// Work of row r in units: [row_pos, + sink_units) is its sink block (one
+// event at row_pos), then row_cost units of start, then its tiles, tile j at
+// unit first = row_pos + sink_units + row_cost + 32 j.
+struct MlaRowWork {
+  int tiles, wa, wb;  // tiles; workers of the first and last tile
+  int64_t first;      // unit of tile 0
+  int slots;          // partial slots: 1 for the sinks, then one per share the tiles touch
+};
+__device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const MlaSpan &sp, int64_t pos,
+                                                   int64_t share) {
+  MlaRowWork r;
+  r.tiles = mla_tiles(sp);
+  r.first = pos + p.sink_units + p.row_cost;
+  r.wa = r.wb = 0;
   const int sinks = p.n_sinks > 0 ? 1 : 0;
-  for (int b = tid; b < kBuckets; b += 1024) bucket[b] = 0;
+  r.slots = sinks;
+  if (r.tiles > 0) {
+    r.wa = int(r.first / share);
+    r.wb = int((r.first + int64_t(kMlaTile) * (r.tiles - 1)) / share);
+    if (sinks || r.wb > r.wa) r.slots += r.wb - r.wa + 1;
+  }
+  return r;
+}
+
+// Work split on the device (graph-safe: lengths are read at run time), the
+// same scheme as the GQA decode's: every row weighs its key tiles plus a start
+// cost (plus its sink block); an exclusive scan gives each row's first unit,
+// and the total is cut into `workers` equal contiguous shares, one per
+// persistent workgroup (fewer for small calls; more, in rounds, when sparse
+// shares must stay within the kSparsePart slot list). A workgroup walks its
+// shares row by row; a row whose tiles lie in one share and that has no sinks
+// writes its output directly, others write one (m, l, O) partial per share
+// (and one for the sinks) into consecutive slots, combined by the merge.
+// Rows without keys or sinks get their zero output here. (The former
+// longest-first queue of fixed partitions left a quarter of the workgroups'
+// time idle at the end of a config-5 call.) One workgroup of 1024 threads.
+__global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
+  __shared__ long long s_tot64[16];
+  __shared__ int s_tot32[16];
+  __shared__ long long s_pos, s_share;
+  __shared__ int s_slot, s_emax, s_workers;
+  __shared__ int s_incl[1024];
+  const int tid = threadIdx.x;
   if (tid == 0) {
-    carry_full = carry_slot = 0;
-    total_keys = 0ull;
+    s_pos = 0;
+    s_slot = 0;
+    s_emax = -1;
   }
   __syncthreads();
-  // Pass 1: sequence of each row and the call's key count. The span of each
-  // thread's first row stays in registers for the later passes (calls with
-  // more than 1024 rows recompute the others).
-  MlaSpan first{0, 0, 0, 0};
-  unsigned long long keys = 0ull;
-  for (int row = tid; row < p.num_rows; row += 1024) {
-    const int seq = mla_seq_of(p, row);
-    p.row_seq[row] = seq;
-    const MlaSpan s = mla_span(p, row, seq);
-    if (row == tid) first = s;
-    if (s.hi > s.lo) keys += uint64_t(s.hi - s.base);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) keys += __shfl_xor(keys, off, 64);
-  if (lane == 0) atomicAdd(&total_keys, keys);
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned long long per = uint64_t(p.items_per_wg) * uint64_t(p.static_items);
-    unsigned long long t = (total_keys + per - 1) / per;
-    t = (t + 31) & ~31ull;
-    part_sh = t < uint64_t(kMinPart) ? kMinPart : (t > uint64_t(SMAX) ? SMAX : int(t));
-  }
-  __syncthreads();
-  const int S = part_sh;
-  // Pass 2: full partitions go first in row order (positions by a scan),
-  // shorter ones are counted into their buckets; partial slots by a scan.
   for (int base = 0; base < p.num_rows; base += 1024) {
     const int row = base + tid;
-    int nfull = 0, slots = 0, np = 0;
-    MlaSpan s{0, 0, 0, 0};
+    long long w = 0;
     if (row < p.num_rows) {
-      s = base == 0 ? first : mla_span(p, row, p.row_seq[row]);
-      p.row_pt[row] = S;
-      np = mla_parts(s, S);
-      if (np == 0) atomicAdd(&bucket[nb], 1);
-      for (int k = 0; k < np; ++k) {
-        const int sz = mla_part_size(s, S, k);
-        if (sz == S) ++nfull;
-        else atomicAdd(&bucket[(SMAX - sz) / 32], 1);
+      const int seq = mla_seq_of(p, row);
+      p.row_seq[row] = seq;
+      const int tiles = mla_tiles(mla_span(p, row, seq));
+      w = (tiles > 0 ? (long long)p.row_cost + (long long)kMlaTile * tiles : 0) + p.sink_units;
+      if (w == 0) {  // no keys and no sinks: defined zero output
+        uint16_t *o = p.out + int64_t(row) * p.heads * 512;
+        for (int i = 0; i < p.heads * 512; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
       }
-      slots = np + sinks;
     }
-    int xf = nfull, xs = slots;  // inclusive scans: shuffles within the wave, then across waves
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int yf = __shfl_up(xf, off, 64), ys = __shfl_up(xs, off, 64);
-      xf += lane >= off ? yf : 0;
-      xs += lane >= off ? ys : 0;
-    }
-    if (lane == 63) {
-      wave_full[wv] = xf;
-      wave_slot[wv] = xs;
-    }
+    long long tot;
+    const long long incl = block_scan<long long, false>(w, s_tot64, &tot);
+    if (row < p.num_rows) p.row_pos[row] = s_pos + incl - w;
     __syncthreads();
-    int at = carry_full, slot = carry_slot;
-    for (int w2 = 0; w2 < wv; ++w2) {
-      at += wave_full[w2];
-      slot += wave_slot[w2];
-    }
-    at += xf - nfull;
-    slot += xs - slots;
-    if (row < p.num_rows) {
-      p.row_slot[row] = slot;
-      for (int k = 0; k < np && nfull > 0; ++k)
-        if (mla_part_size(s, S, k) == S) p.items[at++] = (uint32_t(row) << 12) | uint32_t(k);
-    }
-    __syncthreads();
-    if (tid == 1023) {
-      carry_full = at;
-      carry_slot = slot + slots;
-    }
+    if (tid == 0) s_pos += tot;
     __syncthreads();
   }
-  {
-    const int run = bucket_prefix(bucket, nb, carry_full, tid);
-    if (tid == 0) {
-      p.queue[0] = p.static_items;
-      p.queue[1] = run + (sinks ? p.num_rows : 0);
-      sink_base = run;
-    }
+  if (tid == 0) {
+    const long long total = s_pos;
+    const long long small = (total + kMinShareUnits - 1) / kMinShareUnits;
+    long long workers = small < p.grid ? small : p.grid;
+    const long long bound = (total + p.max_share - 1) / p.max_share;  // sparse share cap
+    workers = bound > workers ? bound : workers;
+    workers = workers < 1 ? 1 : (workers > p.max_workers ? p.max_workers : workers);
+    const long long share = total > 0 ? (total + workers - 1) / workers : 1;
+    s_workers = int(workers);
+    s_share = share;
+    p.plan[0] = int(workers);
+    *reinterpret_cast<int64_t *>(p.plan + 2) = share;
   }
   __syncthreads();
-  // One sink item per row after every partition item.
-  if (sinks)
-    for (int row = tid; row < p.num_rows; row += 1024)
-      p.items[sink_base + row] = (uint32_t(row) << 12) | kSinkItem;
-  // Pass 3: place the shorter partitions and the rows without keys.
-  for (int row = tid; row < p.num_rows; row += 1024) {
-    const MlaSpan s = row == tid ? first : mla_span(p, row, p.row_seq[row]);
-    const int np = mla_parts(s, S);
-    if (np == 0) p.items[atomicAdd(&bucket[nb], 1)] = uint32_t(row) << 12;
-    for (int k = 0; k < np; ++k) {
-      const int sz = mla_part_size(s, S, k);
-      if (sz != S) p.items[atomicAdd(&bucket[(SMAX - sz) / 32], 1)] = (uint32_t(row) << 12) | uint32_t(k);
+  const long long share = s_share;
+  for (int base = 0; base < p.num_rows; base += 1024) {
+    const int row = base + tid;
+    int cnt = 0, e = -1;
+    if (row < p.num_rows) {
+      const int64_t pos = p.row_pos[row];
+      const MlaRowWork rw = mla_row_work(p, mla_span(p, row, p.row_seq[row]), pos, share);
+      cnt = rw.slots;
+      // Worker of the row's last event (its last tile, or its sink block).
+      if (rw.tiles > 0) e = rw.wb;
+      else if (p.sink_units > 0) e = int(pos / share);
     }
+    int tot;
+    const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
+    if (row < p.num_rows) p.row_slot[row] = cnt > 0 ? s_slot + incl - cnt : -1;
+    int emax;
+    s_incl[tid] = block_scan<int, true>(e, s_tot32, &emax);
+    __syncthreads();
+    int prev = tid > 0 ? s_incl[tid - 1] : -1;
+    prev = prev > s_emax ? prev : s_emax;
+    for (int v = prev + 1; v <= e; ++v) p.start_row[v] = row;
+    __syncthreads();
+    if (tid == 0) {
+      s_slot += tot;
+      s_emax = emax > s_emax ? emax : s_emax;
+    }
+    __syncthreads();
   }
+  for (int v = s_emax + 1 + tid; v < s_workers; v += 1024) p.start_row[v] = p.num_rows;
 }
 
 template <bool C8>
@@ -485,9 +464,12 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
 // direct-to-LDS loads shared by the four waves through a ring of R::STAGES
 // slots; every wave reads its K operand (keys in rows) and its V operand (dims
 // in rows) from the same LDS bytes.
+// Tiles [j0, j1) of row `row` (span sp): output, or partial slot `slot` when
+// slot >= 0.
 template <bool C8, bool SPARSE, bool WIDE>
 __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
-                                         uint32_t *slot_list, int row, int part, int w, int lane) {
+                                         uint32_t *slot_list, int row, const MlaSpan &sp, int j0,
+                                         int j1, int slot, int w, int lane) {
   using R = MlaRow<C8>;
   using Cfg = MlaCfg<C8, SPARSE, WIDE>;
   constexpr int S = Cfg::STAGES;
@@ -495,22 +477,9 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   using Geo = MlaGeo<NW>;
   constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   constexpr int DV = 512;
-  const int PT = p.row_pt[row];
-  const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
-  const int nparts = mla_parts(sp, PT);
   const int c = lane & 15, g = lane >> 4;
   const bool head_live = c < p.heads;
-  const bool partials = nparts > 1 || p.n_sinks > 0;
-
-  if (nparts == 0) {  // no keys: zeros, or nothing when the merge adds sinks
-    if (head_live && !partials) {
-#pragma unroll
-      for (int k = 0; k < DPW / 32; ++k)
-        store_u32x4(p.out + (int64_t(row) * p.heads + c) * DV + DPW * w + (DPW / 4) * g + 8 * k,
-                    u32x4{0, 0, 0, 0});
-    }
-    return;
-  }
+  const bool partials = slot >= 0;
 
   // Q operand: latent dims DPW w + 32s + 8g (s < KS), rope dims 32w + 8g (w < 2).
   u32x4 qv[KS + 1];
@@ -538,10 +507,10 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     q_unscale = 1.0f / qs;
   }
 
-  const int tile0 = sp.base + part * PT;
+  const int tile0 = sp.base + j0 * kMlaTile;
   const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
-  const int t_end = sp.hi < tile0 + PT ? sp.hi : tile0 + PT;
-  const int n_tiles = (t_end - tile0 + kMlaTile - 1) / kMlaTile;
+  const int t_end = sp.hi < sp.base + j1 * kMlaTile ? sp.hi : sp.base + j1 * kMlaTile;
+  const int n_tiles = j1 - j0;
   const int bs = p.block_size;
   const int64_t seq_table = int64_t(sp.seq) * p.table_stride;
 
@@ -571,12 +540,17 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       slot_list[i] = slot;
     }
     __syncthreads();
-  } else {
-    const int first = tile0 / bs;
-    const int nblk = (t_end - 1) / bs - first + 1;  // <= 64 (host-checked partition size)
-    int b = lane < nblk ? p.block_tables[seq_table + first + lane] : 0;
-    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
   }
+  // Dense: block ids of a 64-block window from block wblk0 of the sequence,
+  // one per lane; the window slides (one vector load) when a tile to be
+  // issued leaves it, so a range may span any number of blocks.
+  const int nblk_end = (t_end - 1) / bs + 1;
+  int wblk0 = tile0 / bs;
+  auto load_window = [&]() {
+    int b = wblk0 + lane < nblk_end ? p.block_tables[seq_table + wblk0 + lane] : 0;
+    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+  };
+  if constexpr (!SPARSE) load_window();
 
   const uint32_t ring_base = lds_addr(ring);
   const int bs_log2 = __builtin_ctz(uint32_t(bs));  // block_size: host-checked power of two
@@ -608,6 +582,10 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       // base sits at its first live row: earlier rows wrap to offsets past the
       // extent and land as zeros, like rows past the end.
       const int halves = bs < kMlaTile ? 2 : 1;
+      if (((t0 + kMlaTile - 1) >> bs_log2) - wblk0 >= 64) {
+        wblk0 = t0 >> bs_log2;
+        load_window();
+      }
       u32x4 rc[2];
       uint32_t first_row[2];
 #pragma unroll
@@ -615,7 +593,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
         if (hb < halves) {
           const int r0 = hb * (kMlaTile / halves), r1 = r0 + kMlaTile / halves;
           const int a = lower > r0 ? lower : r0, b = upper < r1 ? upper : r1;
-          const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 >> bs_log2) - (tile0 >> bs_log2) + hb);
+          const int blk = __builtin_amdgcn_readlane(lane_blocks, (t0 >> bs_log2) - wblk0 + hb);
           const int64_t tok = int64_t(blk) * bs + (t0 & (bs - 1)) + (a - r0);
           rc[hb] = raw_rsrc(p.cache + tok * R::BYTES, b > a ? uint32_t(b - a) * R::BYTES : 0u);
           first_row[hb] = uint32_t(a);
@@ -763,7 +741,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
                                     pack_bf16x2(v[6] * inv, v[7] * inv)});
     }
   } else {
-    const int64_t prow = (int64_t(p.row_slot[row]) + (p.n_sinks > 0 ? 1 : 0) + part) * p.heads + c;
+    const int64_t prow = int64_t(slot) * p.heads + c;
     float *po = p.part_o + prow * DV + d0;
 #pragma unroll
     for (int k = 0; k < EPL; ++k)
@@ -852,43 +830,50 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
     __shared__ uint32_t sparse_slots[kSparsePart];
     slot_list = sparse_slots;
   }
-  // The item index travels through the score buffer, idle between items.
-  int *item_slot = reinterpret_cast<int *>(&xbuf[0][0]);
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
-  // Item blockIdx.x first (the plan starts the queue after the static items);
-  // each item pops its successor up front, so the queue round trip overlaps the
-  // item's own loads.
-  const int total = p.queue[1];
-  int it = blockIdx.x;
-  while (it < total) {
-    int next = 0;
-    if (threadIdx.x == 0) next = atomicAdd(p.queue, 1);
-    const uint32_t e = uniform(p.items[it]);
-    if (p.n_sinks > 0 && (e & 0xfffu) == kSinkItem)
-      mla_sink_item<NW>(p, xbuf, int(e >> 12), w, lane);
-    else
-      mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, int(e >> 12), int(e & 0xfffu), w, lane);
-    __syncthreads();  // every wave is done with xbuf (and the ring)
-    if (threadIdx.x == 0) *item_slot = next;
-    __syncthreads();
-    it = uniform(*item_slot);
+  // Workgroup b walks the shares b, b + grid, ... row by row: a row's sink
+  // block is one event at its first unit, its tiles j at first + 32 j.
+  const int workers = uniform(p.plan[0]);
+  const int64_t share = *reinterpret_cast<const int64_t *>(p.plan + 2);
+  const int sinks = p.n_sinks > 0 ? 1 : 0;
+  for (int v = blockIdx.x; v < workers; v += gridDim.x) {
+    const int64_t lo = int64_t(v) * share, hi = lo + share;
+    for (int row = uniform(p.start_row[v]); row < p.num_rows; ++row) {
+      const int64_t pos = p.row_pos[row];
+      if (pos >= hi) break;
+      if (sinks && pos >= lo) {
+        mla_sink_item<NW>(p, xbuf, row, w, lane);
+        __syncthreads();  // every wave is done with xbuf
+      }
+      const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
+      const MlaRowWork rw = mla_row_work(p, sp, pos, share);
+      if (rw.tiles == 0) continue;
+      const int64_t a = lo - rw.first, b = hi - rw.first;
+      const int j0 = a <= 0 ? 0 : int((a + kMlaTile - 1) / kMlaTile);
+      int j1 = b <= 0 ? 0 : int((b + kMlaTile - 1) / kMlaTile);
+      j1 = j1 < rw.tiles ? j1 : rw.tiles;
+      if (j0 >= j1) continue;
+      const int slot0 = uniform(p.row_slot[row]);
+      const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
+      mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
+      __syncthreads();  // every wave is done with xbuf (and the ring)
+    }
   }
 }
 
-// Combine one (row, head): the row's partition partials and, with sinks, the
-// sink partial in the row's first slot. Each thread owns 2 output dims.
+// Combine one (row, head): the row's partials (the sink partial first, when
+// there are sinks, then one per share its tiles touch). Each thread owns 2
+// output dims.
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
-  const int np = mla_parts(sp, p.row_pt[row]);
-  if (p.n_sinks == 0 && np <= 1) return;
-  const int sinks = p.n_sinks > 0 ? 1 : 0;
-  const int64_t prow0 = int64_t(p.row_slot[row]) * p.heads + h;
-  auto part_at = [&](int k) {  // k == np: the sink slot (the row's first)
-    return prow0 + int64_t(k < np ? sinks + k : 0) * p.heads;
-  };
-  const int total = np + (p.n_sinks > 0 ? 1 : 0);
+  const int slot0 = p.row_slot[row];
+  if (slot0 < 0) return;  // output written by the attention kernel or the plan
+  const int64_t share = *reinterpret_cast<const int64_t *>(p.plan + 2);
+  const MlaRowWork rw = mla_row_work(p, mla_span(p, row, p.row_seq[row]), p.row_pos[row], share);
+  const int total = rw.slots;
+  const int64_t prow0 = int64_t(slot0) * p.heads + h;
+  auto part_at = [&](int k) { return prow0 + int64_t(k) * p.heads; };
   // Largest partial max: threads stride over the partials, then a
   // workgroup reduction (4 waves).
   __shared__ float wmax[4];
@@ -900,7 +885,7 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   __syncthreads();
   const float Mt = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   uint32_t *op = reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512) + tid;
-  if (Mt == -INFINITY) {  // no keys and no sinks
+  if (Mt == -INFINITY) {  // nothing visible
     *op = 0u;
     return;
   }
@@ -942,65 +927,39 @@ struct MlaCall {
   void *stream;
 };
 
-// Largest dense partition (the plan picks smaller ones when a call has
-// fewer keys than items_per_wg items per workgroup of that size).
-constexpr int kMlaDensePart = 3072;
-// Target items per persistent workgroup (the plan's partition size is
-// T / (items_per_wg * workgroups)), and the most the workspace allows for.
-constexpr int kMlaItemsMax = 4;
-inline int mla_items_per_wg(bool c8, bool sparse) {
-  static const int v1 = [] { const char *e = getenv("IFATTN_MLA_K"); return e ? atoi(e) : 1; }();
-  static const int v2 = [] { const char *e = getenv("IFATTN_MLA_K_C8"); return e ? atoi(e) : 1; }();
-  const int k = c8 && !sparse ? v2 : v1;
-  return k < 1 ? 1 : (k > kMlaItemsMax ? kMlaItemsMax : k);
-}
-// IFATTN_MLA_PART overrides the largest dense partition for tuning: a
-// multiple of 32 in [kMinPart, 8192] (the plan sorts items into SMAX/32 + 1 of
-// its 257 buckets); other values keep the default.
-inline int mla_dense_cap() {
+// Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
+// share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
+// keep their index entries within the kSparsePart slot list.
+inline int mla_row_cost() {
   static const int v = [] {
-    const char *e = getenv("IFATTN_MLA_PART");
-    const int x = e ? atoi(e) : 0;
-    return (x >= kMinPart && x <= 8192 && x % 32 == 0) ? x : kMlaDensePart;
+    const char *e = getenv("IFATTN_MLA_ROW_COST");
+    const int x = e ? atoi(e) : -1;
+    return (x >= 0 && x <= 65536) ? x : 64;
   }();
   return v;
 }
-
-// Largest partition of a call: kSparsePart index entries, or the dense
-// default capped so that a partition starting on a 32-token tile spans at
-// most the 64 blocks one wave holds: 1 + ceil((PT - 32) / bs) <= 64, i.e.
-// PT <= 63 * bs + 32.
-inline int mla_part_cap(bool sparse, int block_size) {
-  if (sparse) return kSparsePart;
-  const int cap = (63 * block_size + 32) & ~31;
-  const int d = mla_dense_cap();
-  return d < cap ? d : cap;
+constexpr int kMlaSparseShare = kSparsePart - 2 * kMlaTile;
+inline int mla_sink_units(int n_sinks) {
+  return n_sinks > 0 ? kMlaTile * ((n_sinks + kMlaTile - 1) / kMlaTile) + mla_row_cost() : 0;
 }
-// Partitions of the longest possible row at partition size pt (default: the
-// largest).
-inline int mla_parts_per_row(bool sparse, int topk, int window, int max_context, int block_size,
-                             int pt = 0) {
-  if (pt <= 0) pt = mla_part_cap(sparse, block_size);
-  if (sparse) return (topk + pt - 1) / pt;
-  const int full = (max_context + pt - 1) / pt;
-  if (window <= 0) return full;
-  const int win = (window + 31 + pt - 1) / pt;
-  return win < full ? win : full;
+// Workers the workspace holds: the largest persistent grid, or for sparse
+// calls enough capped shares for rows of topk entries.
+inline uint64_t mla_max_workers(bool sparse, int rows, int topk, int n_sinks) {
+  const uint64_t grid = uint64_t(device_cus()) * kMlaWgsMax;
+  if (!sparse) return grid;
+  const uint64_t per_row = uint64_t(mla_sink_units(n_sinks)) + mla_row_cost() +
+                           uint64_t(kMlaTile) * ((uint64_t(topk) + kMlaTile - 1) / kMlaTile);
+  const uint64_t need = (uint64_t(rows) * per_row + kMlaSparseShare - 1) / kMlaSparseShare;
+  return need > grid ? need : grid;
 }
-// Items (and partial slots) a call can produce: the plan's partitions are
-// either the largest size (at most rows * ppr) or sized for items_per_wg per
-// workgroup (at most kMlaItemsMax * workgroups + rows), and never below
-// kMinPart keys (at most rows * ppr_min); plus one empty or sink item per row.
-inline uint64_t mla_item_cap(int rows, int ppr, int ppr_min) {
-  const uint64_t a = uint64_t(kMlaItemsMax) * uint64_t(device_cus()) * kMlaWgsMax + uint64_t(rows) * uint64_t(ppr + 3);
-  const uint64_t b = uint64_t(rows) * uint64_t(ppr_min + 3);
-  return a < b ? a : b;
-}
-inline uint64_t mla_workspace(int rows, int heads, int ppr, int ppr_min) {
-  const uint64_t items = mla_item_cap(rows, ppr, ppr_min);
-  uint64_t b = kQueueBytes + align16(items * 4) + 3 * align16(uint64_t(rows) * 4);
-  b += items * heads * (512 + 2) * sizeof(float);
-  return b;
+// Workspace: plan words | row_pos | row_seq | row_slot | start_row | partial
+// O | partial (m, l). Partial slots: one per row for the sinks, and at most
+// two per worker for the key shares.
+inline uint64_t mla_workspace(int rows, int heads, bool sparse, int topk, int n_sinks) {
+  const uint64_t workers = mla_max_workers(sparse, rows, topk, n_sinks);
+  const uint64_t slots = 2 * workers + (n_sinks > 0 ? uint64_t(rows) : 0);
+  return kQueueBytes + align16(uint64_t(rows) * 8) + 2 * align16(uint64_t(rows) * 4) +
+         align16(workers * 4) + slots * heads * (512 + 2) * sizeof(float);
 }
 
 int32_t mla_run(const MlaCall &c, const char *what) {
@@ -1033,16 +992,11 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   const int64_t span = (c.window > 0 && c.window < c.max_context) ? int64_t(c.window) + 31 : c.max_context;
   const bool wide = !c.c8 && !sparse && int64_t(c.num_rows) * span >= kMlaWideKeys;
   const int wgs = wgs_mla(c.c8, sparse, wide);
-  const int pt = mla_part_cap(sparse, c.block_size);
-  const int ppr = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size);
-  // Partition indices stay below the 12-bit sink marker: at most ppr at the
-  // largest size, at most items_per_wg * workgroups + 1 at smaller ones.
-  if (ppr >= 4095 || kMlaItemsMax * device_cus() * kMlaWgsMax + 1 >= 4095)
-    return fail(IFATTN_EINVAL, what, "more than 4094 partitions per row");
-  const int ppr_min = mla_parts_per_row(sparse, c.topk, c.window, c.max_context, c.block_size, kMinPart);
-  const uint64_t need = mla_workspace(c.num_rows, c.heads, ppr, ppr_min);
+  const uint64_t need = mla_workspace(c.num_rows, c.heads, sparse, c.topk, c.n_sinks);
   if (!c.workspace || c.workspace_bytes < need || !aligned16(c.workspace))
     return fail(IFATTN_EWORKSPACE, what, "workspace missing, short or misaligned");
+  const uint64_t max_workers = mla_max_workers(sparse, c.num_rows, c.topk, c.n_sinks);
+  if (max_workers > (uint64_t(1) << 28)) return fail(IFATTN_EINVAL, what, "too many rows for the work split");
   MlaParams p{};
   p.q = static_cast<const uint16_t *>(c.q);
   p.cache = static_cast<const uint8_t *>(c.cache);
@@ -1064,26 +1018,28 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.topk = c.topk;
   p.window = c.window;
   p.n_sinks = c.n_sinks;
-  p.part_tokens = pt;
-  p.items_per_wg = mla_items_per_wg(c.c8, sparse);
   p.scale_log2 = c.scale * kLog2e;
+  const int grid = device_cus() * wgs;
+  p.row_cost = mla_row_cost();
+  p.sink_units = mla_sink_units(c.n_sinks);
+  p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
+  p.max_workers = int(max_workers);
+  p.grid = grid;
   uint8_t *ws = static_cast<uint8_t *>(c.workspace);
-  const uint64_t items = mla_item_cap(c.num_rows, ppr, ppr_min);
-  p.queue = reinterpret_cast<int32_t *>(ws);
+  p.plan = reinterpret_cast<int32_t *>(ws);
   ws += kQueueBytes;
-  p.items = reinterpret_cast<uint32_t *>(ws);
-  ws += align16(items * 4);
+  p.row_pos = reinterpret_cast<int64_t *>(ws);
+  ws += align16(uint64_t(c.num_rows) * 8);
   p.row_seq = reinterpret_cast<int32_t *>(ws);
-  ws += align16(uint64_t(c.num_rows) * 4);
-  p.row_pt = reinterpret_cast<int32_t *>(ws);
   ws += align16(uint64_t(c.num_rows) * 4);
   p.row_slot = reinterpret_cast<int32_t *>(ws);
   ws += align16(uint64_t(c.num_rows) * 4);
+  p.start_row = reinterpret_cast<int32_t *>(ws);
+  ws += align16(max_workers * 4);
+  const uint64_t slots = 2 * max_workers + (c.n_sinks > 0 ? uint64_t(c.num_rows) : 0);
   p.part_o = reinterpret_cast<float *>(ws);
-  p.part_ml = p.part_o + items * c.heads * 512;
+  p.part_ml = p.part_o + slots * c.heads * 512;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
-  const int grid = device_cus() * wgs;
-  p.static_items = grid;  // the attention grid takes the first items by index
   mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
     if (sparse) mla_attention_kernel<true, true, false><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
@@ -1129,8 +1085,9 @@ using namespace ifattn;
 extern "C" uint64_t ifattn_mla_decode_workspace_size(int32_t num_seqs, int32_t heads,
                                                      int32_t max_context, int32_t block_size) {
   if (num_seqs <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
-  return mla_workspace(num_seqs, heads, mla_parts_per_row(false, 0, 0, max_context, block_size),
-                       mla_parts_per_row(false, 0, 0, max_context, block_size, kMinPart));
+  (void)max_context;
+  (void)block_size;
+  return mla_workspace(num_seqs, heads, false, 0, 0);
 }
 
 extern "C" int32_t ifattn_mla_decode_bf16(const void *q, const void *cache,
@@ -1162,10 +1119,10 @@ extern "C" uint64_t ifattn_mla_attention_workspace_size(int32_t num_rows, int32_
                                                         int32_t topk, int32_t n_sinks,
                                                         int32_t block_size) {
   if (num_rows <= 0 || heads <= 0 || max_context <= 0 || block_size <= 0) return 0;
-  const bool sparse = topk > 0;
-  (void)n_sinks;  // sink partials use the slots counted per row
-  return mla_workspace(num_rows, heads, mla_parts_per_row(sparse, topk, window, max_context, block_size),
-                       mla_parts_per_row(sparse, topk, window, max_context, block_size, kMinPart));
+  (void)max_context;
+  (void)window;
+  (void)block_size;
+  return mla_workspace(num_rows, heads, topk > 0, topk, n_sinks);
 }
 
 extern "C" int32_t ifattn_mla_window_attention_bf16(
