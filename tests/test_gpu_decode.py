@@ -80,6 +80,23 @@ def test_decode_many_partitions():
     assert_close(bf16_host(out), exp)
 
 
+def test_decode_shares_slide_the_block_window():
+    # 16-token pages hold 128 block ids per lane window (2048 tokens); two
+    # 600000-token sequences give each of the persistent workgroups a share of
+    # about 2350 tokens, so the window slides inside a share, and each
+    # sequence spreads over about 256 shares (many merge rounds).
+    lens = [600000, 599991]
+    bs, nb = 16, 2 * 37500 + 64
+    case = W.decode_host_case(19, num_seqs=len(lens), lo=1, hi=600000, dist="uniform", q_heads=8,
+                              kv_heads=1, head_dim=64, block_size=bs, pool_blocks=nb)
+    case.seq_lens[:] = lens
+    case.block_tables = W.block_tables_for(np.random.default_rng(9), case.seq_lens, bs, nb,
+                                           case.block_tables.shape[1])
+    case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(len(lens)), bs)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)
+
+
 def test_decode_many_sequences():
     # a large ragged batch of short sequences (more items than workgroups, and
     # sequence ids beyond 4096 in the work-item encoding)

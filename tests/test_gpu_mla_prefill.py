@@ -46,6 +46,28 @@ def test_mla_decode(heads, c8, bs):
     assert_close(bf16_host(out), exp)
 
 
+def test_mla_decode_shares_slide_the_block_window():
+    # 16-token pages: a lane window holds 64 block ids (1024 keys); four rows
+    # of about 100000 keys give each persistent workgroup a share of about
+    # 1560 keys, so the window slides inside a share.
+    import torch
+    from ironpangu_amd import ops
+    case = W.mla_host_case(5, num_seqs=4, lo=1, hi=100000, dist="uniform", heads=16,
+                           block_size=16, fixed={0: 100000, 1: 99999, 2: 98000, 3: 100000})
+    h = case.host
+    nb, bs = case.pool_blocks, case.block_size
+    pool = h["pool"].copy()
+    oracle.kv_write(h["row_new"], pool, case.slot_mapping)
+    cache = to_dev(h["pool"]).view(nb, bs, 576)
+    ops.kv_cache_write(to_dev(h["row_new"]), None, cache, None,
+                       to_dev(case.slot_mapping.astype(np.int64)))
+    out = ops.mla_decode(to_dev(h["q"]), cache, to_dev(case.block_tables),
+                         to_dev(case.seq_lens), case.max_context, case.scale)
+    torch.cuda.synchronize()
+    exp = oracle.mla_decode(h["q"], pool, case.block_tables, case.seq_lens, 16, bs, case.scale)
+    assert_close(bf16_host(out), exp)
+
+
 def _prefill(case):
     import torch
     from ironpangu_amd import ops
