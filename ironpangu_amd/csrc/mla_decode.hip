@@ -581,7 +581,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       // n = 4k + w < 18 moves rows 0..15 and the rest rows 16..31). Each part's
       // base sits at its first live row: earlier rows wrap to offsets past the
       // extent and land as zeros, like rows past the end.
-      const int halves = bs < kMlaTile ? 2 : 1;
+      // C8 blocks hold at least 32 rows (host-checked): one part per tile.
+      const int halves = !C8 && bs < kMlaTile ? 2 : 1;
       if (((t0 + kMlaTile - 1) >> bs_log2) - wblk0 >= 64) {
         wblk0 = t0 >> bs_log2;
         load_window();
