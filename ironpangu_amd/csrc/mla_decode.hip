@@ -62,7 +62,8 @@ struct MlaParams {
   int32_t *plan;
   int64_t *row_pos;             // [rows] first work unit of each row
   int32_t *row_seq;             // [rows] sequence of each row
-  int32_t *row_slot;            // [rows] first partial slot, -1: the row writes its output directly
+  int2 *row_slot;               // [rows] (first partial slot, slot count); (-1, 0): the row
+                                // writes its output directly
   int32_t *start_row;           // [max_workers] first row not wholly before each worker's share
   float *part_o;                // [slots, heads, 512]
   float *part_ml;               // [slots, heads, 2]
@@ -167,13 +168,19 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     s_emax = -1;
   }
   __syncthreads();
+  // The first chunk's spans stay in registers for pass 2 (calls with more than
+  // 1024 rows reload the others).
+  MlaSpan first_span{0, 0, 0, 0};
+  int64_t first_pos = 0;
   for (int base = 0; base < p.num_rows; base += 1024) {
     const int row = base + tid;
     long long w = 0;
     if (row < p.num_rows) {
       const int seq = mla_seq_of(p, row);
       p.row_seq[row] = seq;
-      const int tiles = mla_tiles(mla_span(p, row, seq));
+      const MlaSpan sp = mla_span(p, row, seq);
+      if (base == 0) first_span = sp;
+      const int tiles = mla_tiles(sp);
       w = (tiles > 0 ? (long long)p.row_cost + (long long)kMlaTile * tiles : 0) + p.sink_units;
       if (w == 0) {  // no keys and no sinks: defined zero output
         uint16_t *o = p.out + int64_t(row) * p.heads * 512;
@@ -183,6 +190,7 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     long long tot;
     const long long incl = block_scan<long long, false>(w, s_tot64, &tot);
     if (row < p.num_rows) p.row_pos[row] = s_pos + incl - w;
+    if (base == 0) first_pos = s_pos + incl - w;
     __syncthreads();
     if (tid == 0) s_pos += tot;
     __syncthreads();
@@ -206,8 +214,9 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     const int row = base + tid;
     int cnt = 0, e = -1;
     if (row < p.num_rows) {
-      const int64_t pos = p.row_pos[row];
-      const MlaRowWork rw = mla_row_work(p, mla_span(p, row, p.row_seq[row]), pos, share);
+      const int64_t pos = base == 0 ? first_pos : p.row_pos[row];
+      const MlaRowWork rw =
+          mla_row_work(p, base == 0 ? first_span : mla_span(p, row, p.row_seq[row]), pos, share);
       cnt = rw.slots;
       // Worker of the row's last event (its last tile, or its sink block).
       if (rw.tiles > 0) e = rw.wb;
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     }
     int tot;
     const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
-    if (row < p.num_rows) p.row_slot[row] = cnt > 0 ? s_slot + incl - cnt : -1;
+    if (row < p.num_rows) p.row_slot[row] = make_int2(cnt > 0 ? s_slot + incl - cnt : -1, cnt);
     int emax;
     s_incl[tid] = block_scan<int, true>(e, s_tot32, &emax);
     __syncthreads();
@@ -807,7 +816,7 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  const int64_t prow = int64_t(p.row_slot[row]) * p.heads + c;  // the row's first slot
+  const int64_t prow = int64_t(p.row_slot[row].x) * p.heads + c;  // the row's first slot
   float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
   for (int k = 0; k < EPL; ++k) {
@@ -855,7 +864,7 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
       int j1 = b <= 0 ? 0 : int((b + kMlaTile - 1) / kMlaTile);
       j1 = j1 < rw.tiles ? j1 : rw.tiles;
       if (j0 >= j1) continue;
-      const int slot0 = uniform(p.row_slot[row]);
+      const int slot0 = uniform(p.row_slot[row].x);
       const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
       mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
       __syncthreads();  // every wave is done with xbuf (and the ring)
@@ -868,11 +877,9 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
 // output dims.
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const int slot0 = p.row_slot[row];
-  if (slot0 < 0) return;  // output written by the attention kernel or the plan
-  const int64_t share = *reinterpret_cast<const int64_t *>(p.plan + 2);
-  const MlaRowWork rw = mla_row_work(p, mla_span(p, row, p.row_seq[row]), p.row_pos[row], share);
-  const int total = rw.slots;
+  const int2 slots = p.row_slot[row];
+  if (slots.x < 0) return;  // output written by the attention kernel or the plan
+  const int slot0 = slots.x, total = slots.y;
   const int64_t prow0 = int64_t(slot0) * p.heads + h;
   auto part_at = [&](int k) { return prow0 + int64_t(k) * p.heads; };
   // Largest partial max: threads stride over the partials, then a
@@ -959,7 +966,7 @@ inline uint64_t mla_max_workers(bool sparse, int rows, int topk, int n_sinks) {
 inline uint64_t mla_workspace(int rows, int heads, bool sparse, int topk, int n_sinks) {
   const uint64_t workers = mla_max_workers(sparse, rows, topk, n_sinks);
   const uint64_t slots = 2 * workers + (n_sinks > 0 ? uint64_t(rows) : 0);
-  return kQueueBytes + align16(uint64_t(rows) * 8) + 2 * align16(uint64_t(rows) * 4) +
+  return kQueueBytes + 2 * align16(uint64_t(rows) * 8) + align16(uint64_t(rows) * 4) +
          align16(workers * 4) + slots * heads * (512 + 2) * sizeof(float);
 }
 
@@ -1033,8 +1040,8 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   ws += align16(uint64_t(c.num_rows) * 8);
   p.row_seq = reinterpret_cast<int32_t *>(ws);
   ws += align16(uint64_t(c.num_rows) * 4);
-  p.row_slot = reinterpret_cast<int32_t *>(ws);
-  ws += align16(uint64_t(c.num_rows) * 4);
+  p.row_slot = reinterpret_cast<int2 *>(ws);
+  ws += align16(uint64_t(c.num_rows) * 8);
   p.start_row = reinterpret_cast<int32_t *>(ws);
   ws += align16(max_workers * 4);
   const uint64_t slots = 2 * max_workers + (c.n_sinks > 0 ? uint64_t(c.num_rows) : 0);

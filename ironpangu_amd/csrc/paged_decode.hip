@@ -513,7 +513,7 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
       int j1 = b <= 0 ? 0 : int((b + kSplitTile - 1) / kSplitTile);
       j1 = j1 < tiles ? j1 : tiles;
       if (j0 >= j1) continue;
-      int slot = uniform(p.seq_slot[seq]);
+      int slot = uniform(p.seq_slot[seq].x);
       if (slot >= 0) slot += v - int(first / share);
       const int t_end = j1 * kSplitTile < len ? j1 * kSplitTile : len;
       for (int grp = 0; grp < groups; ++grp) {

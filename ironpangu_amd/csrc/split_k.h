@@ -33,7 +33,8 @@ struct DecodeParams {
   // units per worker).
   int32_t *plan;
   int64_t *seq_pos;    // [num_seqs] first work unit of each sequence
-  int32_t *seq_slot;   // [num_seqs] first partial slot of a sequence over several shares, else -1
+  int2 *seq_slot;      // [num_seqs] (first partial slot, slot count) of a sequence over several
+                       // shares, (-1, 0) otherwise
   int32_t *start_seq;  // [grid] first sequence not wholly before each worker's share
   float *part_o;       // [2 * grid, q_heads, D]
   float *part_ml;      // [2 * grid, q_heads, 2]
@@ -225,7 +226,7 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
     }
     int tot;
     const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
-    if (seq < p.num_seqs) p.seq_slot[seq] = cnt > 0 ? s_slot + incl - cnt : -1;
+    if (seq < p.num_seqs) p.seq_slot[seq] = make_int2(cnt > 0 ? s_slot + incl - cnt : -1, cnt);
     int emax;
     s_incl[tid] = block_scan<int, true>(e, s_tot32, &emax);
     __syncthreads();
@@ -326,11 +327,9 @@ __global__ __launch_bounds__(256) void split_k_merge_kernel(DecodeParams p) {
   constexpr int DW = D < 128 ? D : 128;  // dims per wave
   const int seq = blockIdx.x, h = blockIdx.y;
   if (!decode_seq(p, seq)) return;
-  const int slot0 = p.seq_slot[seq];
-  if (slot0 < 0) return;  // the sequence lies in one share: output written by the decode
-  int wa, wb;
-  seq_workers(p.seq_pos[seq] + p.seq_cost, clamp_len(p, seq), share_of(p), wa, wb);
-  merge_head<D, DW>(p, seq, h, slot0, wb - wa + 1, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
+  const int2 slots = p.seq_slot[seq];
+  if (slots.x < 0) return;  // the sequence lies in one share: output written by the decode
+  merge_head<D, DW>(p, seq, h, slots.x, slots.y, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
 }
 
 // One workgroup per (sequence, head); one wave per 128 output dims.
@@ -387,7 +386,7 @@ inline int decode_grid() { return device_cus() * wgs_per_cu(); }
 // partial (m, l); a sequence over k shares uses k slots, at most 2 per worker.
 inline uint64_t split_k_workspace_bytes(int num_seqs, int heads, int dims, int /*max_context*/) {
   const uint64_t workers = uint64_t(decode_grid());
-  return kQueueBytes + align16(uint64_t(num_seqs) * 8) + align16(uint64_t(num_seqs) * 4) +
+  return kQueueBytes + align16(uint64_t(num_seqs) * 8) + align16(uint64_t(num_seqs) * 8) +
          align16(workers * 4) + 2 * workers * heads * (uint64_t(dims) + 2) * sizeof(float);
 }
 // Fills the split fields of p (num_seqs set) and binds the workspace.
@@ -400,8 +399,8 @@ inline void split_k_bind_workspace(DecodeParams &p, void *workspace, int heads, 
   w += kQueueBytes;
   p.seq_pos = reinterpret_cast<int64_t *>(w);
   w += align16(uint64_t(p.num_seqs) * 8);
-  p.seq_slot = reinterpret_cast<int32_t *>(w);
-  w += align16(uint64_t(p.num_seqs) * 4);
+  p.seq_slot = reinterpret_cast<int2 *>(w);
+  w += align16(uint64_t(p.num_seqs) * 8);
   p.start_seq = reinterpret_cast<int32_t *>(w);
   w += align16(uint64_t(p.grid) * 4);
   p.part_o = reinterpret_cast<float *>(w);
