@@ -55,6 +55,9 @@ def parse():
                     help="only run a plain 1 GiB device-to-device copy (counter calibration)")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only measure the HBM read ceiling (64 KiB blocks over an 8.6 GB footprint)")
+    ap.add_argument("--issue-probe", action="store_true",
+                    help="only measure how MFMA, VALU, exponentials and LDS reads share a SIMD "
+                         "(the prefill tile loop's instruction mix)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip configs 3-5 (reported under 'secondary')")
     ap.add_argument("--only", choices=sorted(SECONDARY),
@@ -726,6 +729,47 @@ def read_ceiling(steps, sweep=False):
     return out
 
 
+def issue_probe(steps):
+    """Time per iteration of the issue-overlap probe modes (probe/issue_overlap.hip):
+    256 workgroups of eight waves, two per SIMD, 20000 iterations each. The
+    'hidden' figures compare a combined mode with the sum and the max of its
+    parts: 0 when the parts serialise, 1 when the shorter part hides fully."""
+    import ctypes as C
+    import torch
+    lib = C.CDLL(str(ROOT / "ironpangu_amd" / "libifattn_probe.so"))
+    lib.ifattn_probe_issue.argtypes = [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]
+    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
+    iters = 20000
+    names = ["mfma16", "exp32", "fma32", "mfma16|exp32_other_wave", "mfma16|fma32_other_wave",
+             "mfma16+exp32_same_wave", "mfma16+fma32_same_wave", "lds_b128x8", "lds_tr_b64x16",
+             "lds_b128x8+mfma16"]
+    ns = {}
+    for mode, name in enumerate(names):
+        def run():
+            assert lib.ifattn_probe_issue(mode, iters, sink.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream) == 0
+        ns[name] = timed(run, steps, 1) * 1e6 / iters
+    one = {k: ns[k] / 2 for k in ("mfma16", "exp32", "fma32")}  # one wave's share of the SIMD
+
+    def hidden(both, a, b):
+        s, m = a + b, max(a, b)
+        return round((s - both) / (s - m), 2)
+    out = {"ns_per_iteration": {k: round(v, 1) for k, v in ns.items()},
+           "hidden": {
+               "exp_vs_mfma_other_wave": hidden(ns["mfma16|exp32_other_wave"], one["mfma16"], one["exp32"]),
+               "fma_vs_mfma_other_wave": hidden(ns["mfma16|fma32_other_wave"], one["mfma16"], one["fma32"]),
+               "exp_vs_mfma_same_wave": hidden(ns["mfma16+exp32_same_wave"], ns["mfma16"], ns["exp32"]),
+               "fma_vs_mfma_same_wave": hidden(ns["mfma16+fma32_same_wave"], ns["mfma16"], ns["fma32"]),
+               "lds_vs_mfma_same_wave": hidden(ns["lds_b128x8+mfma16"], ns["mfma16"], ns["lds_b128x8"])},
+           "lds_bytes_per_ns_per_cu": {
+               "b128": round(8 * 8 * 1024 / ns["lds_b128x8"], 1),
+               "tr_b64": round(8 * 16 * 512 / ns["lds_tr_b64x16"], 1)},
+           "note": "ns per iteration of eight waves per CU (two per SIMD); mfma16 = 16 MFMA "
+                   "16x16x32 bf16 per wave, exp32/fma32 = 32 v_exp_f32/v_fma_f32 per wave, lds = "
+                   "8 ds_read_b128 or 16 ds_read_b64_tr_b16 per wave (the prefill operand patterns)"}
+    return out
+
+
 # Secondary workloads, in report order.
 SECONDARY = {
     "c8_decode": bench_c8,
@@ -755,6 +799,10 @@ def main():
 
     if args.only:
         print(json.dumps({args.only: SECONDARY[args.only](args.seed, args.steps, args.warmup)}))
+        return
+
+    if args.issue_probe:
+        print(json.dumps(issue_probe(max(args.steps, 5))))
         return
 
     if args.read_ceiling:

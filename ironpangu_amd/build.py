@@ -98,9 +98,9 @@ def build(jobs: int | None = None, plugins: bool = True) -> Path:
                   f"-L{PKG}", "-lifattn_hip", "-Wl,-rpath,$ORIGIN", "-o", str(out)])
         with cf.ThreadPoolExecutor(jobs) as ex:
             list(ex.map(one, PLUGINS.items()))
-    probe = PKG / "probe" / "read_ceiling.hip"
-    if probe.exists():  # measurement-only library for bench.py --read-ceiling
-        _run([_hipcc(), *HIP_FLAGS, "-shared", str(probe), "-o", str(PKG / "libifattn_probe.so")])
+    probes = sorted((PKG / "probe").glob("*.hip"))
+    if probes:  # measurement-only library for bench.py --read-ceiling / --issue-probe
+        _run([_hipcc(), *HIP_FLAGS, "-shared", *map(str, probes), "-o", str(PKG / "libifattn_probe.so")])
     driver = CSRC.parent / "driver" / "ifattn_drive.cpp"
     if driver.exists():
         _run(["g++", *HOST_FLAGS, f"-I{ROCM}/include", str(driver), f"-L{ROCM}/lib",

@@ -155,7 +155,9 @@ struct PrefillRing {
   // a K operand read get 16 distinct keys, and so do the eight consecutive
   // rows of two 16-lane groups of a transposing V read, whose lanes touch
   // chunk pairs {2b, 2b+1}: keys that differ only in bit 0 (rows r, r^1 under
-  // a plain row key) would map both rows' pairs to the same banks.
+  // a plain row key) would map both rows' pairs to the same banks. Only row
+  // bits below SWB (at most 4) enter the key, so rows r and r + 16 share it.
+  static_assert(SWB <= 4, "rows 16 apart share a swizzle key");
   static __device__ __forceinline__ int swz(int row) {
     return ((row << 1) | ((row >> (SWB - 1)) & 1)) & SW;
   }
@@ -303,13 +305,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
 #pragma unroll
     for (int h = 0; h < KT; ++h) {
       const uint8_t *kt = step + h * RG::SLOT;
-      // One 16-token half at a time keeps 16 operand registers live.
+      // One 16-token half at a time keeps 16 operand registers live. Rows r
+      // and r + 16 share a swizzle key, so the second half is an immediate
+      // offset from the first (one set of per-lane addresses, not two).
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         u32x4 ka[D / 32];
 #pragma unroll
         for (int s = 0; s < D / 32; ++s)
-          ka[s] = load_u32x4(kt + RG::at(16 * mt + c, (D / 32) * g + s));
+          ka[s] = load_u32x4(kt + mt * 16 * D * 2 + RG::at(c, (D / 32) * g + s));
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           f32x4 acc = {0, 0, 0, 0};
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
     // of tile_token(g, 4 + (i>>2))), and lane c receives dim 16b + c of those
     // four tokens.
     const int tr_dim = 4 * (c & 3);
-    const int tr_row0 = pf_tile_token(g, c >> 2), tr_row1 = pf_tile_token(g, 4 + (c >> 2));
+    const int tr_row0 = pf_tile_token(g, c >> 2);  // pf_tile_token(g, 4 + (c >> 2)) = tr_row0 + 16
 #pragma unroll
     for (int h = 0; h < KT; ++h) {
       const __attribute__((address_space(3))) char *vt_lds =
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void varlen_prefill_kernel(Pref
       for (int b = 0; b < VPL; ++b) {
         const int d = 16 * b + tr_dim;
         const uint32_t o0 = RG::at(tr_row0, d >> 3) + 2 * (d & 7);
-        const uint32_t o1 = RG::at(tr_row1, d >> 3) + 2 * (d & 7);
+        const uint32_t o1 = o0 + 16 * D * 2;  // row tr_row0 + 16: same swizzle key
         typedef short s16x4 __attribute__((ext_vector_type(4)));
         typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(vt_lds + o0));
