@@ -206,6 +206,15 @@ __device__ __forceinline__ T uniform(T v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// Load of data no kernel writes while this one runs (plans, lengths, tables
+// written by an earlier launch), through the constant address space: at a
+// wave-uniform address it becomes a scalar load, which waits on its own
+// counter instead of behind the wave's outstanding vector stores.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(p);
+}
+
 __device__ __forceinline__ u32x4 load_u32x4(const void *p) {
   return *reinterpret_cast<const u32x4 *>(p);
 }

@@ -264,15 +264,18 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   const int head = kvh * p.group + c;
   const bool head_live = c < p.group;
 
-  // B operand of QK^T: q[head][d0(s, g) + e], zero for padded heads.
+  // B operand of QK^T: q[head][d0(s, g) + e], zero for padded heads. Buffer
+  // loads with an out-of-range offset for padded heads: unconditional loads
+  // issue together (loads behind a branch each got their own full wait).
   u32x4 qv[D / 32];
   {
-    const uint16_t *qr = p.q + (q_row_of(p, seq) * p.q_heads + (head_live ? head : 0)) * D;
+    const auto rq = make_rsrc(p.q + q_row_of(p, seq) * p.q_heads * D, uint32_t(p.q_heads) * D * 2);
+    const uint32_t qoff = head_live ? uint32_t(head) * D * 2 : 0x80000000u;
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) {
       // Dims of k-step s, lane group g (matching the K operand).
       const int d0 = k_lines<D, C8>() ? 32 * s + 8 * g : (D / 4) * g + 8 * s;
-      qv[s] = head_live ? load_u32x4(qr + d0) : u32x4{0, 0, 0, 0};
+      qv[s] = buf_load_x4(rq, qoff + uint32_t(d0) * 2);
     }
   }
 
@@ -306,10 +309,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
   const int32_t *table_row = p.block_tables + int64_t(seq) * p.table_stride;
   const int nblk_end = (t_end - 1) / p.block_size + 1;  // blocks up to the range end
   int win0 = t_begin / p.block_size;
+  // Entries past the range end read as 0 (buffer bounds), without a branch.
+  const auto rt = make_rsrc(table_row, uint32_t(nblk_end) * 4);
   auto load_window = [&]() {
     auto clamp = [&](int b) { return b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b); };
-    lane_blocks.lo = clamp(win0 + lane < nblk_end ? table_row[win0 + lane] : 0);
-    if constexpr (SP) lane_blocks.hi = clamp(win0 + lane + 64 < nblk_end ? table_row[win0 + lane + 64] : 0);
+    lane_blocks.lo = clamp(int(buf_load_x1(rt, uint32_t(win0 + lane) * 4)));
+    if constexpr (SP) lane_blocks.hi = clamp(int(buf_load_x1(rt, uint32_t(win0 + lane + 64) * 4)));
   };
   load_window();
 
@@ -497,12 +502,14 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
     DecodeParams p, int waves_per_wg) {
   const int lane = threadIdx.x & 63, wave = uniform(int(threadIdx.x >> 6));
   const int groups = (p.kv_heads + waves_per_wg - 1) / waves_per_wg;
-  const int workers = uniform(p.plan[0]);
+  // Plan entries through scalar loads (ld_const): vector loads here each
+  // waited behind the previous range's output stores.
+  const int workers = ld_const(p.plan);
   const int64_t share = share_of(p);
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const int64_t lo = int64_t(v) * share, hi = lo + share;
-    for (int seq = uniform(p.start_seq[v]); seq < p.num_seqs; ++seq) {
-      const int64_t first = p.seq_pos[seq] + p.seq_cost;  // unit of tile 0
+    for (int seq = ld_const(p.start_seq + v); seq < p.num_seqs; ++seq) {
+      const int64_t first = ld_const(p.seq_pos + seq) + p.seq_cost;  // unit of tile 0
       if (first >= hi) break;
       if (!decode_seq(p, seq)) continue;
       const int len = uniform(clamp_len(p, seq));
@@ -513,7 +520,7 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
       int j1 = b <= 0 ? 0 : int((b + kSplitTile - 1) / kSplitTile);
       j1 = j1 < tiles ? j1 : tiles;
       if (j0 >= j1) continue;
-      int slot = uniform(p.seq_slot[seq].x);
+      int slot = ld_const(&p.seq_slot[seq].x);
       if (slot >= 0) slot += v - int(first / share);
       const int t_end = j1 * kSplitTile < len ? j1 * kSplitTile : len;
       for (int grp = 0; grp < groups; ++grp) {

@@ -50,18 +50,18 @@ struct DecodeParams {
 };
 
 __device__ __forceinline__ int clamp_len(const DecodeParams &p, int seq) {
-  const int len = p.seq_lens[seq];
+  const int len = ld_const(p.seq_lens + seq);
   return len > p.max_context ? p.max_context : len;
 }
 // q / out row of a sequence (identity for plain decode batches).
 __device__ __forceinline__ int64_t q_row_of(const DecodeParams &p, int seq) {
-  return p.cu_seqlens ? int64_t(p.cu_seqlens[seq + 1]) - 1 : int64_t(seq);
+  return p.cu_seqlens ? int64_t(ld_const(p.cu_seqlens + seq + 1)) - 1 : int64_t(seq);
 }
 __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
-  return !p.cu_seqlens || p.cu_seqlens[seq + 1] - p.cu_seqlens[seq] == 1;
+  return !p.cu_seqlens || ld_const(p.cu_seqlens + seq + 1) - ld_const(p.cu_seqlens + seq) == 1;
 }
 __device__ __forceinline__ int64_t share_of(const DecodeParams &p) {
-  return *reinterpret_cast<const int64_t *>(p.plan + 2);
+  return ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
 }
 // Workers holding the first and the last tile of a sequence whose tile 0 sits
 // at work unit `first` (tile j at first + 32 j).
