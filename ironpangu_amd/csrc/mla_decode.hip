@@ -90,15 +90,15 @@ __device__ __forceinline__ int mla_seq_of(const MlaParams &p, int row) {
   int a = 0, b = p.num_seqs - 1;  // last sequence whose first row is <= row
   while (a < b) {
     const int m = (a + b + 1) >> 1;
-    if (p.cu_q[m] <= row) a = m; else b = m - 1;
+    if (ld_const(p.cu_q + m) <= row) a = m; else b = m - 1;
   }
   return a;
 }
 
 __device__ __forceinline__ MlaSpan mla_span(const MlaParams &p, int row, int seq) {
-  const int start = p.cu_q ? p.cu_q[seq] : row;
-  const int count = p.cu_q ? p.cu_q[seq + 1] - start : 1;
-  int kv = p.kv_lens[seq];
+  const int start = p.cu_q ? ld_const(p.cu_q + seq) : row;
+  const int count = p.cu_q ? ld_const(p.cu_q + seq + 1) - start : 1;
+  int kv = ld_const(p.kv_lens + seq);
   kv = kv > p.max_context ? p.max_context : kv;
   int causal = kv - count + (row - start) + 1;
   causal = causal < 0 ? 0 : (causal > p.max_context ? p.max_context : causal);
@@ -491,14 +491,68 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
   const bool partials = slot >= 0;
 
   // Q operand: latent dims DPW w + 32s + 8g (s < KS), rope dims 32w + 8g (w < 2).
+  // Unconditional buffer loads (padded heads and waves without rope dims read
+  // zeros from out-of-range offsets), issued together with the block ids or
+  // the slot list below; the C8 conversion waits for them after that.
   u32x4 qv[KS + 1];
   {
-    const uint16_t *qp = p.q + (int64_t(row) * p.heads + (head_live ? c : 0)) * 576;
+    const auto rq = make_rsrc(p.q + int64_t(row) * p.heads * 576, uint32_t(p.heads) * 576 * 2);
+    const uint32_t qh = head_live ? uint32_t(c) * 576 * 2 : 0x80000000u;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qv[s] = head_live ? load_u32x4(qp + DPW * w + 32 * s + 8 * g) : u32x4{0, 0, 0, 0};
-    qv[KS] = (head_live && w < 2) ? load_u32x4(qp + 512 + 32 * w + 8 * g) : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s) qv[s] = buf_load_x4(rq, qh + uint32_t(DPW * w + 32 * s + 8 * g) * 2);
+    qv[KS] = buf_load_x4(rq, (w < 2 ? qh : 0x80000000u) + uint32_t(512 + 32 * w + 8 * g) * 2);
   }
+  const int tile0 = sp.base + j0 * kMlaTile;
+  const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
+  const int t_end = sp.hi < sp.base + j1 * kMlaTile ? sp.hi : sp.base + j1 * kMlaTile;
+  const int n_tiles = j1 - j0;
+  const int bs = p.block_size;
+  const int64_t seq_table = int64_t(sp.seq) * p.table_stride;
+
+  int lane_blocks = 0;
+  if constexpr (SPARSE) {
+    // Physical rows of this partition's index entries (kNoRow for padding or
+    // out-of-table positions): all index loads, then all table loads, each
+    // batch issued before any result is used.
+    constexpr int PER = (kSparsePart + 64 * NW - 1) / (64 * NW);
+    const int n = t_end - tile0;
+    const auto ri = make_rsrc(p.indices + int64_t(row) * p.topk + tile0, uint32_t(n) * 4);
+    const auto rb = make_rsrc(p.block_tables + seq_table, uint32_t(p.table_stride) * 4);
+    int pos[PER], blk[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k)  // entries past n read as 0 and are not stored
+      pos[k] = int(buf_load_x1(ri, uint32_t(threadIdx.x + k * 64 * NW) * 4));
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const bool ok = pos[k] >= 0;  // pos / bs >= table_stride reads 0 (buffer bounds)
+      blk[k] = int(buf_load_x1(rb, ok ? uint32_t(pos[k] / bs) * 4 : 0x80000000u));
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = threadIdx.x + k * 64 * NW;
+      if (i < n) {
+        uint32_t slot = kNoRow;
+        if (pos[k] >= 0 && pos[k] / bs < p.table_stride) {
+          int b = blk[k];
+          b = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+          slot = uint32_t(b) * uint32_t(bs) + uint32_t(pos[k] & (bs - 1));
+        }
+        slot_list[i] = slot;
+      }
+    }
+  }
+  // Dense: block ids of a 64-block window from block wblk0 of the sequence,
+  // one per lane; the window slides (one vector load) when a tile to be
+  // issued leaves it, so a range may span any number of blocks. Entries past
+  // the range end read as 0 (buffer bounds).
+  const int nblk_end = (t_end - 1) / bs + 1;
+  int wblk0 = tile0 / bs;
+  const auto rw = make_rsrc(p.block_tables + seq_table, uint32_t(nblk_end) * 4);
+  auto load_window = [&]() {
+    const int b = int(buf_load_x1(rw, uint32_t(wblk0 + lane) * 4));
+    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
+  };
+  if constexpr (!SPARSE) load_window();
   // C8: the latent QK^T runs in fp16 on the biased codes (code + kI8Bias,
   // exact); the wave's q slice is scaled per head by a power of two into fp16
   // range, and kI8Bias * sum(q slice) leaves each partial score.
@@ -516,13 +570,6 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     q_unscale = 1.0f / qs;
   }
 
-  const int tile0 = sp.base + j0 * kMlaTile;
-  const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
-  const int t_end = sp.hi < sp.base + j1 * kMlaTile ? sp.hi : sp.base + j1 * kMlaTile;
-  const int n_tiles = j1 - j0;
-  const int bs = p.block_size;
-  const int64_t seq_table = int64_t(sp.seq) * p.table_stride;
-
   // Per-lane chunk of each direct-to-LDS load: tile row and byte within the row.
   uint32_t lrow[R::NI], lcol[R::NI];
 #pragma unroll
@@ -533,33 +580,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     lcol[k] = 16 * (C8 ? jj : (jj ^ R::key(lrow[k], jj)));
   }
 
-  int lane_blocks = 0;
-  if constexpr (SPARSE) {
-    // Physical rows of this partition's index entries (kNoRow for padding or
-    // out-of-table positions).
-    const int n = t_end - tile0;
-    for (int i = threadIdx.x; i < n; i += 64 * NW) {
-      const int pos = p.indices[int64_t(row) * p.topk + tile0 + i];
-      uint32_t slot = kNoRow;
-      if (pos >= 0 && pos / bs < p.table_stride) {
-        int b = p.block_tables[seq_table + pos / bs];
-        b = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
-        slot = uint32_t(b) * uint32_t(bs) + uint32_t(pos & (bs - 1));
-      }
-      slot_list[i] = slot;
-    }
-    __syncthreads();
-  }
-  // Dense: block ids of a 64-block window from block wblk0 of the sequence,
-  // one per lane; the window slides (one vector load) when a tile to be
-  // issued leaves it, so a range may span any number of blocks.
-  const int nblk_end = (t_end - 1) / bs + 1;
-  int wblk0 = tile0 / bs;
-  auto load_window = [&]() {
-    int b = wblk0 + lane < nblk_end ? p.block_tables[seq_table + wblk0 + lane] : 0;
-    lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
-  };
-  if constexpr (!SPARSE) load_window();
+  if constexpr (SPARSE) __syncthreads();  // slot list complete
 
   const uint32_t ring_base = lds_addr(ring);
   const int bs_log2 = __builtin_ctz(uint32_t(bs));  // block_size: host-checked power of two
@@ -816,7 +837,7 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  const int64_t prow = int64_t(p.row_slot[row].x) * p.heads + c;  // the row's first slot
+  const int64_t prow = int64_t(ld_const(&p.row_slot[row].x)) * p.heads + c;  // the row's first slot
   float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
   for (int k = 0; k < EPL; ++k) {
@@ -844,19 +865,21 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
   const int w = uniform(int(threadIdx.x >> 6));
   // Workgroup b walks the shares b, b + grid, ... row by row: a row's sink
   // block is one event at its first unit, its tiles j at first + 32 j.
-  const int workers = uniform(p.plan[0]);
-  const int64_t share = *reinterpret_cast<const int64_t *>(p.plan + 2);
+  // Plan entries through scalar loads (ld_const): vector loads here each
+  // waited behind the previous item's output stores.
+  const int workers = ld_const(p.plan);
+  const int64_t share = ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const int64_t lo = int64_t(v) * share, hi = lo + share;
-    for (int row = uniform(p.start_row[v]); row < p.num_rows; ++row) {
-      const int64_t pos = p.row_pos[row];
+    for (int row = ld_const(p.start_row + v); row < p.num_rows; ++row) {
+      const int64_t pos = ld_const(p.row_pos + row);
       if (pos >= hi) break;
       if (sinks && pos >= lo) {
         mla_sink_item<NW>(p, xbuf, row, w, lane);
         __syncthreads();  // every wave is done with xbuf
       }
-      const MlaSpan sp = mla_span(p, row, p.cu_q ? p.row_seq[row] : row);
+      const MlaSpan sp = mla_span(p, row, p.cu_q ? ld_const(p.row_seq + row) : row);
       const MlaRowWork rw = mla_row_work(p, sp, pos, share);
       if (rw.tiles == 0) continue;
       const int64_t a = lo - rw.first, b = hi - rw.first;
@@ -864,7 +887,7 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
       int j1 = b <= 0 ? 0 : int((b + kMlaTile - 1) / kMlaTile);
       j1 = j1 < rw.tiles ? j1 : rw.tiles;
       if (j0 >= j1) continue;
-      const int slot0 = uniform(p.row_slot[row].x);
+      const int slot0 = ld_const(&p.row_slot[row].x);
       const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
       mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
       __syncthreads();  // every wave is done with xbuf (and the ring)
