@@ -163,7 +163,7 @@ int32_t ifattn_gated_paged_attention_bf16(const void *q, const void *k, const vo
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): ifattn_paged_decode_step_bf16 without a workspace. The
- * call's scratch (work queue, work list, split-K partials) lives in a static
+ * call's scratch (split-K plan and partials) lives in a static
  * device array of IFATTN_NOALLOC_SCRATCH_BYTES per GPU, held until the process
  * ends; calls needing more (ifattn_paged_decode_workspace_size above it) fail
  * with IFATTN_EINVAL. The entry point allocates nothing. All calls on one GPU

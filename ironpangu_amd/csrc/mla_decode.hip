@@ -20,9 +20,11 @@
 // sparse rows read the logical positions of their index list
 // (min(causal, topk) candidates, -1 padding; openpangu_attention_metadata.h:13-33).
 //
-// Decomposition: a persistent workgroup of four waves takes (row, partition)
-// items from a device-built queue. A partition's 32-token tiles are copied
-// HBM -> LDS once by direct-to-LDS loads (dense: 32 consecutive rows of one
+// Decomposition: the plan kernel cuts the call's work (rows weighted by their
+// key tiles, a start cost and their sink block) into equal contiguous shares,
+// one per persistent workgroup of four waves, which walks its share row by
+// row. A share's 32-token tiles are copied HBM -> LDS once by direct-to-LDS
+// loads (dense: 32 consecutive rows of one
 // block; sparse: a gather of 32 rows named by the index list) through a ring
 // of slots; wave w then owns latent dims [128w, 128w+128) for QK^T and PV (K
 // and V are the same bytes) and waves 0 and 1 one 32-dim step of the rope part.
@@ -33,9 +35,9 @@
 // the N dimension; C8 latent scores use the fp16 MFMA on the codes biased by
 // 1152 (three VALU ops per four codes instead of a convert per code), with q
 // in fp16 and the bias term removed per head. Rows split over several
-// partitions, and rows with sinks, write (m, l, O) partials; a merge kernel
-// adds the sink rows and combines. The plan sizes partitions from the call's
-// key count; how many workgroups share a CU depends on the variant (MlaCfg).
+// shares, and rows with sinks, write (m, l, O) partials; a merge kernel
+// combines them with the sink partial. How many workgroups share a CU depends
+// on the variant (MlaCfg).
 #include "common.h"
 #include "ifattn_internal.h"
 #include "split_k.h"
@@ -784,9 +786,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 // Learned sink rows of one query row (keys [n, 576], values [n, 512] bf16,
 // shared by every row, so they are read from L2): the same tile math as the
 // cache keys, four waves per row, heads in the MFMA N dimension. The (m, l, O)
-// partial of the sinks alone goes to the row's first partial slot. Runs as one
-// item of the attention kernel's queue (after every partition item, so these
-// short items fill the tail).
+// partial of the sinks alone goes to the row's first partial slot. Runs as the
+// event at the start of the row's work units, in the share that holds it.
 template <int NW>
 __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int w,
                                               int lane) {

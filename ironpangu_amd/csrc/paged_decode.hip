@@ -117,7 +117,7 @@ struct TileRegs {
 };
 
 // Per-lane byte offsets inside a tile; identical for every tile, so
-// they are computed once per work item and the per-tile cost is one scalar
+// they are computed once per range and the per-tile cost is one scalar
 // buffer descriptor per cache.
 struct LaneOffsets {
   uint32_t k[2];  // K loads of row block mt (see k_lines)
@@ -681,12 +681,12 @@ extern "C" int32_t ifattn_paged_decode_step_bf16(
 
 // ---------------------------------------------------------------- no-allocation step
 //
-// Device scratch for ifattn_paged_decode_step_bf16_noalloc: the split-K work
-// queue, work list and partials of one call live here instead of in a caller
-// workspace. Every GPU the library runs on holds its own copy until the process
-// ends. Nothing in it has to start at zero (the prologue kernel writes the queue
-// words and the work list before the decode kernel reads them, and partials are
-// written before the merge reads them).
+// Device scratch for ifattn_paged_decode_step_bf16_noalloc: the split-K plan
+// (shares, per-sequence positions and slots) and partials of one call live here
+// instead of in a caller workspace. Every GPU the library runs on holds its own
+// copy until the process ends. Nothing in it has to start at zero (the
+// prologue kernel writes the plan before the decode kernel reads it, and
+// partials are written before the merge reads them).
 static __device__ __align__(256) uint8_t scratch[IFATTN_NOALLOC_SCRATCH_BYTES];
 
 namespace {
