@@ -77,6 +77,7 @@ struct MlaParams {
   int max_share;    // largest share: sparse segments fit the kSparsePart slot list
   int max_workers;  // workers the workspace holds
   int grid;         // persistent attention workgroups
+  int self_plan;    // the attention workgroups plan the call themselves (no plan launch)
   float scale_log2;
 };
 
@@ -145,6 +146,25 @@ __device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const Mla
   return r;
 }
 
+// Work units of a row (0: no keys and no sinks).
+__device__ __forceinline__ int64_t mla_row_weight(const MlaParams &p, const MlaSpan &sp) {
+  const int tiles = mla_tiles(sp);
+  return (tiles > 0 ? int64_t(p.row_cost) + int64_t(kMlaTile) * tiles : 0) + p.sink_units;
+}
+// Workers and share of a call of `total` units: the grid, fewer for small
+// calls (at least kMinShareUnits each), more for sparse calls whose shares
+// must fit the slot list, at most the workspace's max_workers.
+__device__ __forceinline__ void mla_split(const MlaParams &p, int64_t total, int &workers,
+                                          int64_t &share) {
+  const int64_t small = (total + kMinShareUnits - 1) / kMinShareUnits;
+  int64_t wk = small < p.grid ? small : p.grid;
+  const int64_t bound = (total + p.max_share - 1) / p.max_share;  // sparse share cap
+  wk = bound > wk ? bound : wk;
+  wk = wk < 1 ? 1 : (wk > p.max_workers ? p.max_workers : wk);
+  workers = int(wk);
+  share = total > 0 ? (total + wk - 1) / wk : 1;
+}
+
 // Work split on the device (graph-safe: lengths are read at run time), the
 // same scheme as the GQA decode's: every row weighs its key tiles plus a start
 // cost (plus its sink block); an exclusive scan gives each row's first unit,
@@ -182,8 +202,7 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
       p.row_seq[row] = seq;
       const MlaSpan sp = mla_span(p, row, seq);
       if (base == 0) first_span = sp;
-      const int tiles = mla_tiles(sp);
-      w = (tiles > 0 ? (long long)p.row_cost + (long long)kMlaTile * tiles : 0) + p.sink_units;
+      w = mla_row_weight(p, sp);
       if (w == 0) {  // no keys and no sinks: defined zero output
         uint16_t *o = p.out + int64_t(row) * p.heads * 512;
         for (int i = 0; i < p.heads * 512; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
@@ -198,16 +217,12 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     __syncthreads();
   }
   if (tid == 0) {
-    const long long total = s_pos;
-    const long long small = (total + kMinShareUnits - 1) / kMinShareUnits;
-    long long workers = small < p.grid ? small : p.grid;
-    const long long bound = (total + p.max_share - 1) / p.max_share;  // sparse share cap
-    workers = bound > workers ? bound : workers;
-    workers = workers < 1 ? 1 : (workers > p.max_workers ? p.max_workers : workers);
-    const long long share = total > 0 ? (total + workers - 1) / workers : 1;
-    s_workers = int(workers);
+    int workers;
+    int64_t share;
+    mla_split(p, s_pos, workers, share);
+    s_workers = workers;
     s_share = share;
-    p.plan[0] = int(workers);
+    p.plan[0] = workers;
     *reinterpret_cast<int64_t *>(p.plan + 2) = share;
   }
   __syncthreads();
@@ -294,12 +309,20 @@ struct MlaCfg {
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
   static constexpr int NW = kMlaWaves;
-  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : 4));
+#ifndef IFATTN_MLA_BF16_STAGES
+#define IFATTN_MLA_BF16_STAGES 4
+#endif
+#ifndef IFATTN_MLA_BF16_XB
+#define IFATTN_MLA_BF16_XB 1
+#endif
+  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : IFATTN_MLA_BF16_STAGES));
   static constexpr int SLOT = TIGHT ? 21 * 1024 : int(MlaRow<C8>::SLOT);
   static constexpr int LOADS = TIGHT ? 21 : 4 * MlaRow<C8>::NI;  // 1-KiB loads per tile
-  static constexpr int XB = (TIGHT || B2) ? 1 : 2;                // score buffers
+  static constexpr int XB = (TIGHT || B2) ? 1 : (!C8 && !SPARSE ? IFATTN_MLA_BF16_XB : 2);  // score buffers
   static constexpr int RING = SLOT * STAGES;
-  static constexpr int LDS = RING + XB * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0);
+  // (+ the self-plan arrays: two ints per planned row, except the wide variant)
+  static constexpr int LDS = RING + XB * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0) +
+                             (B2 ? 0 : 2 * 4 * 64 * kMlaWaves + 64);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
 };
 // Persistent workgroups per CU of the kernel variant a call runs (the grid is
@@ -789,8 +812,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 // partial of the sinks alone goes to the row's first partial slot. Runs as the
 // event at the start of the row's work units, in the share that holds it.
 template <int NW>
-__device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int w,
-                                              int lane) {
+__device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int slot0,
+                                              int w, int lane) {
   using Geo = MlaGeo<NW>;
   constexpr int DPW = Geo::DPW, KS = Geo::KS, EPL = Geo::EPL;
   const int c = lane & 15, g = lane >> 4, n = p.n_sinks;
@@ -838,7 +861,7 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
-  const int64_t prow = int64_t(ld_const(&p.row_slot[row].x)) * p.heads + c;  // the row's first slot
+  const int64_t prow = int64_t(slot0) * p.heads + c;  // the row's first slot
   float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
   for (int k = 0; k < EPL; ++k) {
@@ -847,6 +870,82 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
         f32x4{acc.o[b][r], acc.o[b + 1][r], acc.o[b + 2][r], acc.o[b + 3][r]};
   }
   if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
+}
+
+// Rows a workgroup plans for itself (one per thread): calls of at most this
+// many rows skip the plan launch.
+constexpr int kMlaSelfPlanRows = 64 * kMlaWaves;
+// Workgroup-wide scan over kMlaSelfPlanRows threads (sum or max, inclusive),
+// wave totals through `wt`; *total gets the workgroup's total.
+template <bool MAX>
+__device__ __forceinline__ int wg_scan(int x, int *wt, int *total) {
+  constexpr int NWV = kMlaSelfPlanRows / 64;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x = MAX ? (y > x ? y : x) : x + y;
+  }
+  if (lane == 63) wt[wv] = x;
+  __syncthreads();
+  int before = MAX ? -1 : 0, all = MAX ? -1 : 0;
+#pragma unroll
+  for (int u = 0; u < NWV; ++u) {
+    const int t = wt[u];
+    if (u < wv) before = MAX ? (t > before ? t : before) : before + t;
+    all = MAX ? (t > all ? t : all) : all + t;
+  }
+  __syncthreads();  // wt is reused by the next scan
+  *total = all;
+  return MAX ? (before > x ? before : x) : before + x;
+}
+// The plan of a call of at most kMlaSelfPlanRows rows, computed by every
+// attention workgroup for itself (the same arithmetic as mla_plan_kernel, in
+// 32-bit units: the host allows it only when every prefix fits): s_pos = first
+// unit of each row; s_se = (first partial slot + 1) << 16 | (running max of
+// the rows' last-event workers + 1), both below 2^16 (host-checked): slot -1
+// means the output is written directly, and the start row of worker v is the
+// first row whose running max reaches v. Workgroup 0 also stores the rows'
+// slots for the merge and zeroes the output of rows without keys and sinks.
+// (Two ints per row keep three dense C8 workgroups within a CU's LDS.)
+__device__ __forceinline__ int mla_se_slot(int se) { return (se >> 16) - 1; }
+__device__ __forceinline__ int mla_se_e(int se) { return (se & 0xFFFF) - 1; }
+__device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, int *s_se, int *s_wt,
+                                              int &workers, int64_t &share) {
+  const int row = threadIdx.x;
+  const bool live = row < p.num_rows;
+  MlaSpan sp{0, 0, 0, 0};
+  int w = 0;
+  if (live) {
+    sp = mla_span(p, row, mla_seq_of(p, row));
+    w = int(mla_row_weight(p, sp));
+  }
+  int total;
+  const int pos = wg_scan<false>(w, s_wt, &total) - w;
+  mla_split(p, total, workers, share);
+  int cnt = 0, e = -1;
+  if (live) {
+    const MlaRowWork rw = mla_row_work(p, sp, pos, share);
+    cnt = rw.slots;
+    if (rw.tiles > 0) e = rw.wb;
+    else if (p.sink_units > 0) e = int(pos / share);
+  }
+  int nslots;
+  const int slot = wg_scan<false>(cnt, s_wt, &nslots) - cnt;
+  int emax;
+  const int einc = wg_scan<true>(e, s_wt, &emax);
+  if (live) {
+    s_pos[row] = pos;
+    s_se[row] = ((cnt > 0 ? slot : -1) + 1) << 16 | (einc + 1);
+    if (blockIdx.x == 0) {
+      p.row_slot[row] = make_int2(cnt > 0 ? slot : -1, cnt);
+      if (w == 0) {  // no keys and no sinks: defined zero output
+        uint16_t *o = p.out + int64_t(row) * p.heads * 512;
+        for (int i = 0; i < p.heads * 512; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
+      }
+    }
+  }
+  __syncthreads();
 }
 
 template <bool C8, bool SPARSE, bool WIDE>
@@ -864,23 +963,46 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
   }
   const int lane = threadIdx.x & 63;
   const int w = uniform(int(threadIdx.x >> 6));
+  // Small calls: the plan in this workgroup's LDS (the wide variant has no LDS
+  // to spare and serves large calls only).
+  static_assert(NW * 64 == kMlaSelfPlanRows, "one planned row per thread");
+  constexpr int SPR = Cfg::B2 ? 1 : kMlaSelfPlanRows;
+  __shared__ int s_pos[SPR], s_se[SPR], s_wt[NW];
+  int workers;
+  int64_t share;
+  const bool self = !Cfg::B2 && p.self_plan;
+  if (self) {
+    mla_self_plan(p, s_pos, s_se, s_wt, workers, share);
+  } else {
+    // Plan entries through scalar loads (ld_const): vector loads here each
+    // waited behind the previous item's output stores.
+    workers = ld_const(p.plan);
+    share = ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
+  }
+  auto start_row = [&](int v) {
+    if (!self) return int(ld_const(p.start_row + v));
+    int a = 0, b = p.num_rows;  // first row whose running last-event worker reaches v
+    while (a < b) {
+      const int m = (a + b) >> 1;
+      if (mla_se_e(s_se[m]) >= v) b = m; else a = m + 1;
+    }
+    return a;
+  };
   // Workgroup b walks the shares b, b + grid, ... row by row: a row's sink
   // block is one event at its first unit, its tiles j at first + 32 j.
-  // Plan entries through scalar loads (ld_const): vector loads here each
-  // waited behind the previous item's output stores.
-  const int workers = ld_const(p.plan);
-  const int64_t share = ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const int64_t lo = int64_t(v) * share, hi = lo + share;
-    for (int row = ld_const(p.start_row + v); row < p.num_rows; ++row) {
-      const int64_t pos = ld_const(p.row_pos + row);
+    for (int row = start_row(v); row < p.num_rows; ++row) {
+      const int64_t pos = self ? int64_t(s_pos[row]) : ld_const(p.row_pos + row);
       if (pos >= hi) break;
+      const int slot0 = self ? mla_se_slot(s_se[row]) : ld_const(&p.row_slot[row].x);
       if (sinks && pos >= lo) {
-        mla_sink_item<NW>(p, xbuf, row, w, lane);
+        mla_sink_item<NW>(p, xbuf, row, slot0, w, lane);
         __syncthreads();  // every wave is done with xbuf
       }
-      const MlaSpan sp = mla_span(p, row, p.cu_q ? ld_const(p.row_seq + row) : row);
+      const int seq = !p.cu_q ? row : (self ? mla_seq_of(p, row) : ld_const(p.row_seq + row));
+      const MlaSpan sp = mla_span(p, row, seq);
       const MlaRowWork rw = mla_row_work(p, sp, pos, share);
       if (rw.tiles == 0) continue;
       const int64_t a = lo - rw.first, b = hi - rw.first;
@@ -888,7 +1010,6 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
       int j1 = b <= 0 ? 0 : int((b + kMlaTile - 1) / kMlaTile);
       j1 = j1 < rw.tiles ? j1 : rw.tiles;
       if (j0 >= j1) continue;
-      const int slot0 = ld_const(&p.row_slot[row].x);
       const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
       mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
       __syncthreads();  // every wave is done with xbuf (and the ring)
@@ -1057,6 +1178,12 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
   p.max_workers = int(max_workers);
   p.grid = grid;
+  // Self-planned calls: few rows, a variant with the LDS for the plan, and
+  // every prefix of row units within 32 bits.
+  p.self_plan = !wide && c.num_rows <= kMlaSelfPlanRows &&
+                int64_t(c.num_rows) * (int64_t(c.max_context) + p.row_cost + p.sink_units + kMlaTile) <
+                    (int64_t(1) << 31) &&
+                2 * max_workers + uint64_t(c.num_rows) < 0xFFFFu;
   uint8_t *ws = static_cast<uint8_t *>(c.workspace);
   p.plan = reinterpret_cast<int32_t *>(ws);
   ws += kQueueBytes;
@@ -1072,7 +1199,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_o = reinterpret_cast<float *>(ws);
   p.part_ml = p.part_o + slots * c.heads * 512;
   hipStream_t s = static_cast<hipStream_t>(c.stream);
-  mla_plan_kernel<<<1, 1024, 0, s>>>(p);
+  if (!p.self_plan) mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
     if (sparse) mla_attention_kernel<true, true, false><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
     else mla_attention_kernel<true, false, false><<<grid, 64 * MlaCfg<true, false>::NW, 0, s>>>(p);
