@@ -497,19 +497,132 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 // former longest-first work queue left half of them idle for the last third of
 // a config-2 step (a full 2048-token item at its end) and serialised 512
 // same-address atomics at the start.
+// Workgroup-wide exclusive scan (sum, or max with identity -1) over the
+// workgroup's waves (at most four), wave totals through `wt`; *total gets the
+// workgroup's total.
+template <bool MAX>
+__device__ __forceinline__ int decode_wg_scan(int x, int *wt, int *total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  constexpr int kId = MAX ? -1 : 0;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x = MAX ? (y > x ? y : x) : x + y;
+  }
+  int excl = __shfl_up(x, 1, 64);
+  excl = lane == 0 ? kId : excl;
+  if (lane == 63) wt[wv] = x;
+  __syncthreads();
+  int before = kId, all = kId;
+  for (int u = 0; u < nw; ++u) {
+    const int t = wt[u];
+    if (u < wv) before = MAX ? (t > before ? t : before) : before + t;
+    all = MAX ? (t > all ? t : all) : all + t;
+  }
+  __syncthreads();  // wt is reused by the next scan
+  *total = all;
+  return MAX ? (before > excl ? before : excl) : before + excl;
+}
+
+// The decode plan of a call of at most kSelfPlanPerThread sequences per
+// thread, computed by every decode workgroup for itself (the prologue's
+// arithmetic in 32-bit units, which the host allows only when every prefix
+// fits): s_pos = first unit of each sequence; s_se = (first partial slot + 1)
+// << 16 | (running max of the sequences' last-tile workers + 1), so the first
+// sequence of worker v is the first whose running max reaches v. Thread t
+// takes sequences K t .. K t + K - 1 (in unit order). Workgroup 0 also stores
+// the sequences' slots for the merge and zeroes the output of sequences
+// without a visible key.
+__device__ __forceinline__ void decode_self_plan_wg(const DecodeParams &p, int *s_pos, int *s_se,
+                                                    int *s_wt, int &workers, int64_t &share) {
+  constexpr int K = kSelfPlanPerThread;
+  const int s0 = threadIdx.x * K;
+  int len[K], sum = 0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int seq = s0 + k;
+    const bool dec = seq < p.num_seqs && decode_seq(p, seq);
+    len[k] = dec ? clamp_len(p, seq) : 0;
+    if (blockIdx.x == 0 && dec && len[k] <= 0) {  // no visible key: defined zero output
+      uint16_t *o = p.out + q_row_of(p, seq) * p.q_heads * p.head_dim;
+      for (int i = 0; i < p.q_heads * p.head_dim; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
+    }
+    sum += len[k] > 0 ? len[k] + p.seq_cost : 0;
+  }
+  int total;
+  const int pos0 = decode_wg_scan<false>(sum, s_wt, &total);
+  {
+    const int64_t small = (int64_t(total) + kMinShareUnits - 1) / kMinShareUnits;
+    workers = int(small < p.grid ? small : p.grid);
+    workers = workers < 1 ? 1 : workers;
+    share = total > 0 ? (int64_t(total) + workers - 1) / workers : 1;
+  }
+  int cnt[K], last[K], csum = 0, emine = -1;
+  int pos = pos0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    cnt[k] = 0;
+    last[k] = -1;
+    if (len[k] > 0) {
+      int wa, wb;
+      seq_workers(int64_t(pos) + p.seq_cost, len[k], share, wa, wb);
+      cnt[k] = wb > wa ? wb - wa + 1 : 0;
+      last[k] = wb;
+      emine = wb;  // nondecreasing along the thread's sequences
+      pos += len[k] + p.seq_cost;
+    }
+    csum += cnt[k];
+  }
+  int nslots, emax;
+  int slot = decode_wg_scan<false>(csum, s_wt, &nslots);
+  int erun = decode_wg_scan<true>(emine, s_wt, &emax);  // over earlier threads
+  pos = pos0;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int seq = s0 + k;
+    if (seq < p.num_seqs) {
+      erun = last[k] > erun ? last[k] : erun;
+      s_pos[seq] = pos;
+      s_se[seq] = ((cnt[k] > 0 ? slot : -1) + 1) << 16 | (erun + 1);
+      if (blockIdx.x == 0) p.seq_slot[seq] = make_int2(cnt[k] > 0 ? slot : -1, cnt[k]);
+    }
+    if (len[k] > 0) pos += len[k] + p.seq_cost;
+    slot += cnt[k];
+  }
+  __syncthreads();
+}
+
 template <int D, bool C8, bool SP>
 __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kernel(
     DecodeParams p, int waves_per_wg) {
   const int lane = threadIdx.x & 63, wave = uniform(int(threadIdx.x >> 6));
   const int groups = (p.kv_heads + waves_per_wg - 1) / waves_per_wg;
-  // Plan entries through scalar loads (ld_const): vector loads here each
-  // waited behind the previous range's output stores.
-  const int workers = ld_const(p.plan);
-  const int64_t share = share_of(p);
+  // Small calls plan in LDS (decode_self_plan_wg); others read the
+  // prologue's plan through scalar loads (ld_const: as vector loads each
+  // waited behind the previous range's output stores).
+  __shared__ int s_pos[kSelfPlanMaxSeqs], s_se[kSelfPlanMaxSeqs], s_wt[max_decode_waves(D)];
+  int workers;
+  int64_t share;
+  if (p.self_plan) {
+    decode_self_plan_wg(p, s_pos, s_se, s_wt, workers, share);
+  } else {
+    workers = ld_const(p.plan);
+    share = share_of(p);
+  }
+  auto start_seq = [&](int v) {
+    if (!p.self_plan) return int(ld_const(p.start_seq + v));
+    int a = 0, b = p.num_seqs;  // first sequence whose running last-tile worker reaches v
+    while (a < b) {
+      const int m = (a + b) >> 1;
+      if ((s_se[m] & 0xFFFF) - 1 >= v) b = m; else a = m + 1;
+    }
+    return a;
+  };
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const int64_t lo = int64_t(v) * share, hi = lo + share;
-    for (int seq = ld_const(p.start_seq + v); seq < p.num_seqs; ++seq) {
-      const int64_t first = ld_const(p.seq_pos + seq) + p.seq_cost;  // unit of tile 0
+    for (int seq = start_seq(v); seq < p.num_seqs; ++seq) {
+      const int64_t first =
+          (p.self_plan ? int64_t(s_pos[seq]) : ld_const(p.seq_pos + seq)) + p.seq_cost;  // tile 0
       if (first >= hi) break;
       if (!decode_seq(p, seq)) continue;
       const int len = uniform(clamp_len(p, seq));
@@ -520,7 +633,7 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
       int j1 = b <= 0 ? 0 : int((b + kSplitTile - 1) / kSplitTile);
       j1 = j1 < tiles ? j1 : tiles;
       if (j0 >= j1) continue;
-      int slot = ld_const(&p.seq_slot[seq].x);
+      int slot = p.self_plan ? (s_se[seq] >> 16) - 1 : ld_const(&p.seq_slot[seq].x);
       if (slot >= 0) slot += v - int(first / share);
       const int t_end = j1 * kSplitTile < len ? j1 * kSplitTile : len;
       for (int grp = 0; grp < groups; ++grp) {
@@ -533,9 +646,11 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
 
 namespace {
 template <int D, bool C8>
-void launch_decode(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
+void launch_decode(const DecodeParams &p0, const RowWrite &wr, hipStream_t s) {
+  const int waves = p0.kv_heads < max_decode_waves(D) ? p0.kv_heads : max_decode_waves(D);
+  DecodeParams p = p0;
+  p.self_plan = decode_self_plan(p, 64 * waves) ? 1 : 0;
   launch_prologue(p, wr, s);
-  const int waves = p.kv_heads < max_decode_waves(D) ? p.kv_heads : max_decode_waves(D);
   const int grid = p.grid;
   if (p.block_size == 16)  // the reference's bf16 page (paged_state_contract.h:25)
     paged_decode_kernel<D, C8, true><<<grid, 64 * waves, 0, s>>>(p, waves);

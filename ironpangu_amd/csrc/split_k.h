@@ -46,6 +46,7 @@ struct DecodeParams {
   int num_seqs, q_heads, kv_heads, group, table_stride, block_size, max_context, head_dim;
   int seq_cost;      // work units charged per sequence on top of its tokens
   int grid;          // persistent decode workgroups (the most workers)
+  int self_plan;     // the decode workgroups plan the call themselves (prologue: row writes only)
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -172,6 +173,7 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
     prologue_write(wr);
     return;
   }
+  if (p.self_plan) return;  // the decode workgroups plan for themselves
   __shared__ long long s_tot64[16];
   __shared__ int s_tot32[16];
   __shared__ long long s_pos, s_share;
@@ -407,12 +409,27 @@ inline void split_k_bind_workspace(DecodeParams &p, void *workspace, int heads, 
   p.part_ml = p.part_o + uint64_t(2 * p.grid) * heads * dims;
 }
 
-// Prologue launch: planning workgroup plus enough writer workgroups for `wr`.
+// Prologue launch: planning workgroup plus enough writer workgroups for `wr`
+// (none at all for a self-planned call without rows to write).
 inline void launch_prologue(const DecodeParams &p, const RowWrite &wr, hipStream_t s) {
   const int64_t vecs = wr.rows * wr.row_vecs * (wr.v_rows ? 2 : 1);
   const int64_t writers = vecs > 0 ? (vecs + 1023) / 1024 : 0;
+  if (p.self_plan && writers == 0) return;
   const int grid = 1 + int(writers < 1024 ? writers : 1024);
   decode_prologue_kernel<><<<grid, 1024, 0, s>>>(p, wr);
+}
+
+// Self-planned decode calls: at most kSelfPlanPerThread sequences per thread
+// of a decode workgroup.
+constexpr int kSelfPlanPerThread = 4;
+constexpr int kSelfPlanMaxSeqs = kSelfPlanPerThread * 256;
+// Host check: may a call of num_seqs sequences on workgroups of `threads`
+// threads plan inside the decode kernel (every prefix of units in 32 bits,
+// partial slots and workers below 2^16)?
+inline bool decode_self_plan(const DecodeParams &p, int threads) {
+  return p.num_seqs <= kSelfPlanPerThread * threads &&
+         int64_t(p.num_seqs) * (int64_t(p.max_context) + p.seq_cost) < (int64_t(1) << 31) &&
+         2 * p.grid < 0xFFFF;
 }
 
 // Launches plan + decode + merge for the single-row sequences of a packed
