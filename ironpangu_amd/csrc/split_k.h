@@ -9,7 +9,9 @@
 // share into consecutive slots, which a merge launch combines. No work queue,
 // no atomics; all workgroups get the same work. The prologue kernel also
 // performs the step's slot-mapped row writes, so a decode step is prologue ->
-// decode -> merge from one host call.
+// decode -> merge from one host call. Calls of up to kSelfPlanPerThread
+// sequences per decode thread plan inside the decode workgroups instead (the
+// same arithmetic), and the prologue then launches only for row writes.
 #pragma once
 #include <cstdlib>
 
