@@ -277,3 +277,23 @@ def test_decode_random_shapes(seed):
     case.slot_mapping = W.slots_of(case.block_tables, case.seq_lens - 1, np.arange(n), bs)
     *_, out, exp = _step(case)
     assert_close(bf16_host(out), exp, what=f"hd {hd} hkv {hkv} group {group} bs {bs} lens {list(lens)}")
+
+
+@pytest.mark.parametrize("hkv,num_seqs", [(1, 256), (1, 257), (2, 512), (2, 513)])
+def test_decode_self_plan_limit(hkv, num_seqs):
+    # calls of up to four sequences per decode thread (one wave per kv head)
+    # plan inside the decode workgroups; one more sequence takes the prologue's
+    # plan; zero-length sequences and sequences over several shares included
+    case = W.decode_host_case(41 + num_seqs, num_seqs=num_seqs, lo=1, hi=3000, dist="loguniform",
+                              q_heads=8 * hkv, kv_heads=hkv, head_dim=128, block_size=64,
+                              pool_blocks=num_seqs * (3000 // 64 + 1) + 4)
+    case.seq_lens[::53] = 0
+    case.seq_lens[7::61] = 3000
+    case.block_tables = W.block_tables_for(np.random.default_rng(num_seqs), case.seq_lens, 64,
+                                           case.pool_blocks, case.block_tables.shape[1])
+    live = np.nonzero(case.seq_lens > 0)[0]
+    case.slot_mapping = np.full(num_seqs, -1, np.int64)
+    case.slot_mapping[live] = W.slots_of(case.block_tables[live], case.seq_lens[live] - 1,
+                                         np.arange(len(live)), 64)
+    *_, out, exp = _step(case)
+    assert_close(bf16_host(out), exp)

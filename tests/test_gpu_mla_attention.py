@@ -180,3 +180,29 @@ def test_many_rows(c8, with_sinks, window):
                 idx[t, :n] = rng.choice(max(causal, 1), size=n, replace=False)
     got, exp = run(q, cache, table, kv, maxc, cu=cu, idx=idx, window=window, sk=sk, sv=sv)
     assert_close(got, exp)
+
+
+@pytest.mark.parametrize("rows,c8", [(256, False), (257, False), (256, True), (257, True)])
+def test_self_plan_row_limit(rows, c8):
+    """Calls of at most 256 rows plan inside the attention workgroups, larger
+    ones through the plan launch: both sides of the limit, with sinks, rows
+    without keys and rows spread over several shares (C8 rows take top-200
+    index lists)."""
+    rng = np.random.default_rng(31 + rows)
+    counts = [1] * (rows - 4) + [2, 2]
+    kv = rng.integers(0, 900, len(counts)).astype(np.int32)
+    kv[::41] = 0                                                   # rows without keys
+    kv[5::37] = rng.integers(2500, 4000, len(kv[5::37]))         # rows over several shares
+    q, cache, table, kv, cu, maxc = batch(29, counts, kv, 32, 16, c8)
+    sk, sv = sinks(40, 12)
+    idx = None
+    if c8:
+        topk = 200
+        idx = np.full((int(sum(counts)), topk), -1, np.int32)
+        for s in range(len(counts)):
+            for t in range(cu[s], cu[s + 1]):
+                causal = int(kv[s]) - counts[s] + (t - cu[s]) + 1
+                n = min(max(causal, 0), topk)
+                idx[t, :n] = rng.choice(max(causal, 1), size=n, replace=False)
+    got, exp = run(q, cache, table, kv, maxc, cu=cu, idx=idx, sk=sk, sv=sv)
+    assert_close(got, exp)
