@@ -67,7 +67,7 @@ struct MlaParams {
   int2 *row_slot;               // [rows] (first partial slot, slot count); (-1, 0): the row
                                 // writes its output directly
   int32_t *start_row;           // [max_workers] first row not wholly before each worker's share
-  float *part_o;                // [slots, heads, 512]
+  uint16_t *part_o;             // [slots, heads, 512] bf16 O / l of each partial
   float *part_ml;               // [slots, heads, 2]
   int64_t num_blocks;
   uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
@@ -797,11 +797,19 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
                                     pack_bf16x2(v[6] * inv, v[7] * inv)});
     }
   } else {
+    // Partials store O / l in bf16 (half the partial traffic; the merge
+    // weighs them by l), (m, l) in fp32.
     const int64_t prow = int64_t(slot) * p.heads + c;
-    float *po = p.part_o + prow * DV + d0;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t *po = p.part_o + prow * DV + d0;
 #pragma unroll
-    for (int k = 0; k < EPL; ++k)
-      *reinterpret_cast<f32x4 *>(po + 4 * k) = f32x4{ov[4 * k], ov[4 * k + 1], ov[4 * k + 2], ov[4 * k + 3]};
+    for (int k = 0; k < EPL / 2; ++k) {
+      const float *v = ov + 8 * k;
+      store_u32x4(po + 8 * k, u32x4{pack_bf16x2(v[0] * inv, v[1] * inv),
+                                    pack_bf16x2(v[2] * inv, v[3] * inv),
+                                    pack_bf16x2(v[4] * inv, v[5] * inv),
+                                    pack_bf16x2(v[6] * inv, v[7] * inv)});
+    }
     if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
   }
 }
@@ -862,12 +870,14 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   l_tot = sum_xor32(l_tot);
   if (!head_live) return;
   const int64_t prow = int64_t(slot0) * p.heads + c;  // the row's first slot
-  float *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  uint16_t *po = p.part_o + prow * 512 + DPW * w + 4 * EPL * g;
 #pragma unroll
   for (int k = 0; k < EPL; ++k) {
     const int r = (4 * k) / EPL, b = (4 * k) % EPL;  // dims EPL r + b .. + 3 of the lane's run
-    *reinterpret_cast<f32x4 *>(po + 4 * k) =
-        f32x4{acc.o[b][r], acc.o[b + 1][r], acc.o[b + 2][r], acc.o[b + 3][r]};
+    *reinterpret_cast<u32x2 *>(po + 4 * k) =
+        u32x2{pack_bf16x2(acc.o[b][r] * inv, acc.o[b + 1][r] * inv),
+              pack_bf16x2(acc.o[b + 2][r] * inv, acc.o[b + 3][r] * inv)};
   }
   if (w == 0 && g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(acc.m, l_tot);
 }
@@ -1047,11 +1057,11 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   for (int k = 0; k < total; ++k) {
     const int64_t pr = part_at(k);
     const float2 m_l = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
-    const float2 o = *reinterpret_cast<const float2 *>(p.part_o + pr * 512 + 2 * tid);
-    const float wk = fast_exp2(m_l.x - Mt);
-    L += wk * m_l.y;
-    o0 += wk * o.x;
-    o1 += wk * o.y;
+    const uint32_t o = *reinterpret_cast<const uint32_t *>(p.part_o + pr * 512 + 2 * tid);
+    const float wk = fast_exp2(m_l.x - Mt) * m_l.y;  // partials hold O / l
+    L += wk;
+    o0 += wk * bf16_bits_to_f32(o & 0xFFFFu);
+    o1 += wk * bf16_bits_to_f32(o >> 16);
   }
   const float inv = 1.0f / L;
   *op = pack_bf16x2(o0 * inv, o1 * inv);
@@ -1112,7 +1122,7 @@ inline uint64_t mla_workspace(int rows, int heads, bool sparse, int topk, int n_
   const uint64_t workers = mla_max_workers(sparse, rows, topk, n_sinks);
   const uint64_t slots = 2 * workers + (n_sinks > 0 ? uint64_t(rows) : 0);
   return kQueueBytes + 2 * align16(uint64_t(rows) * 8) + align16(uint64_t(rows) * 4) +
-         align16(workers * 4) + slots * heads * (512 + 2) * sizeof(float);
+         align16(workers * 4) + slots * heads * (512 * sizeof(uint16_t) + 2 * sizeof(float));
 }
 
 int32_t mla_run(const MlaCall &c, const char *what) {
@@ -1196,8 +1206,8 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.start_row = reinterpret_cast<int32_t *>(ws);
   ws += align16(max_workers * 4);
   const uint64_t slots = 2 * max_workers + (c.n_sinks > 0 ? uint64_t(c.num_rows) : 0);
-  p.part_o = reinterpret_cast<float *>(ws);
-  p.part_ml = p.part_o + slots * c.heads * 512;
+  p.part_o = reinterpret_cast<uint16_t *>(ws);
+  p.part_ml = reinterpret_cast<float *>(p.part_o + slots * c.heads * 512);
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   if (!p.self_plan) mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   if (c.c8) {
