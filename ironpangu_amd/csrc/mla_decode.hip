@@ -1032,11 +1032,44 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
 // output dims.
 __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   const int row = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const int2 slots = p.row_slot[row];
+  const int2 slots = make_int2(ld_const(&p.row_slot[row].x), ld_const(&p.row_slot[row].y));
   if (slots.x < 0) return;  // output written by the attention kernel or the plan
   const int slot0 = slots.x, total = slots.y;
   const int64_t prow0 = int64_t(slot0) * p.heads + h;
   auto part_at = [&](int k) { return prow0 + int64_t(k) * p.heads; };
+  uint32_t *op = reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512) + tid;
+  constexpr int kFast = 8;
+  if (total <= kFast) {
+    // One round trip: every (m, l) and O word of the row's partials is loaded
+    // together (indices past the last partial repeat it with weight 0) and
+    // each thread takes the max itself.
+    float2 m_l[kFast];
+    uint32_t o[kFast];
+#pragma unroll
+    for (int k = 0; k < kFast; ++k) {
+      const int64_t pr = part_at(k < total ? k : total - 1);
+      m_l[k] = *reinterpret_cast<const float2 *>(p.part_ml + pr * 2);
+      o[k] = *reinterpret_cast<const uint32_t *>(p.part_o + pr * 512 + 2 * tid);
+    }
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kFast; ++k) Mt = fmaxf(Mt, m_l[k].x);
+    if (Mt == -INFINITY) {  // nothing visible
+      *op = 0u;
+      return;
+    }
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kFast; ++k) {
+      const float wk = k < total ? fast_exp2(m_l[k].x - Mt) * m_l[k].y : 0.0f;  // partials hold O / l
+      L += wk;
+      o0 += wk * bf16_bits_to_f32(o[k] & 0xFFFFu);
+      o1 += wk * bf16_bits_to_f32(o[k] >> 16);
+    }
+    const float inv = 1.0f / L;
+    *op = pack_bf16x2(o0 * inv, o1 * inv);
+    return;
+  }
   // Largest partial max: threads stride over the partials, then a
   // workgroup reduction (4 waves).
   __shared__ float wmax[4];
@@ -1047,7 +1080,6 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
   if ((tid & 63) == 0) wmax[tid >> 6] = mp;
   __syncthreads();
   const float Mt = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-  uint32_t *op = reinterpret_cast<uint32_t *>(p.out + (int64_t(row) * p.heads + h) * 512) + tid;
   if (Mt == -INFINITY) {  // nothing visible
     *op = 0u;
     return;

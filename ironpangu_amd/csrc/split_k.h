@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256) void split_k_merge_kernel(DecodeParams p) {
   constexpr int DW = D < 128 ? D : 128;  // dims per wave
   const int seq = blockIdx.x, h = blockIdx.y;
   if (!decode_seq(p, seq)) return;
-  const int2 slots = p.seq_slot[seq];
+  const int2 slots = make_int2(ld_const(&p.seq_slot[seq].x), ld_const(&p.seq_slot[seq].y));
   if (slots.x < 0) return;  // the sequence lies in one share: output written by the decode
   merge_head<D, DW>(p, seq, h, slots.x, slots.y, (threadIdx.x >> 6) * DW, threadIdx.x & 63);
 }
