@@ -75,6 +75,7 @@ struct MlaParams {
   int row_cost;     // work units charged per row start
   int sink_units;   // work units of a row's sink block (0 without sinks)
   int max_share;    // largest share: sparse segments fit the kSparsePart slot list
+  int skew_pm;      // share skew between odd and even workers (Shares), permille
   int max_workers;  // workers the workspace holds
   int grid;         // persistent attention workgroups
   int self_plan;    // the attention workgroups plan the call themselves (no plan launch)
@@ -130,8 +131,12 @@ struct MlaRowWork {
   int64_t first;      // unit of tile 0
   int slots;          // partial slots: 1 for the sinks, then one per share the tiles touch
 };
+__device__ __forceinline__ Shares mla_shares(const MlaParams &p, int64_t share) {
+  return Shares{share, share * p.skew_pm / 1000};
+}
 __device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const MlaSpan &sp, int64_t pos,
                                                    int64_t share) {
+  const Shares sh = mla_shares(p, share);
   MlaRowWork r;
   r.tiles = mla_tiles(sp);
   r.first = pos + p.sink_units + p.row_cost;
@@ -139,8 +144,8 @@ __device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const Mla
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   r.slots = sinks;
   if (r.tiles > 0) {
-    r.wa = int(r.first / share);
-    r.wb = int((r.first + int64_t(kMlaTile) * (r.tiles - 1)) / share);
+    r.wa = sh.worker(r.first);
+    r.wb = sh.worker(r.first + int64_t(kMlaTile) * (r.tiles - 1));
     if (sinks || r.wb > r.wa) r.slots += r.wb - r.wa + 1;
   }
   return r;
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
       cnt = rw.slots;
       // Worker of the row's last event (its last tile, or its sink block).
       if (rw.tiles > 0) e = rw.wb;
-      else if (p.sink_units > 0) e = int(pos / share);
+      else if (p.sink_units > 0) e = mla_shares(p, share).worker(pos);
     }
     int tot;
     const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
@@ -938,7 +943,7 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
     const MlaRowWork rw = mla_row_work(p, sp, pos, share);
     cnt = rw.slots;
     if (rw.tiles > 0) e = rw.wb;
-    else if (p.sink_units > 0) e = int(pos / share);
+    else if (p.sink_units > 0) e = mla_shares(p, share).worker(pos);
   }
   int nslots;
   const int slot = wg_scan<false>(cnt, s_wt, &nslots) - cnt;
@@ -1002,7 +1007,8 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
   // block is one event at its first unit, its tiles j at first + 32 j.
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
-    const int64_t lo = int64_t(v) * share, hi = lo + share;
+    const Shares sh = mla_shares(p, share);
+    const int64_t lo = sh.lo(v), hi = sh.lo(v + 1);
     for (int row = start_row(v); row < p.num_rows; ++row) {
       const int64_t pos = self ? int64_t(s_pos[row]) : ld_const(p.row_pos + row);
       if (pos >= hi) break;
@@ -1125,6 +1131,19 @@ struct MlaCall {
 // Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
 // share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
 // keep their index entries within the kSparsePart slot list.
+// Share skew (permille) of dense bf16 calls, as for the GQA decode: odd
+// workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
+// 0.4225 ms with 3%, 0.4307 ms with -3%). C8 and sparse calls keep equal
+// shares (sparse shares are capped by the slot list).
+// IFATTN_MLA_XCD_SKEW (-200..200) overrides the bf16 default.
+inline int mla_skew_pm(bool equal) {
+  static const int v = [] {
+    const char *e = getenv("IFATTN_MLA_XCD_SKEW");
+    const int x = e ? atoi(e) : 1000;
+    return (x >= -200 && x <= 200) ? x : 1000;
+  }();
+  return equal ? 0 : (v != 1000 ? v : 30);
+}
 inline int mla_row_cost() {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_ROW_COST");
@@ -1218,6 +1237,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.row_cost = mla_row_cost();
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
+  p.skew_pm = mla_skew_pm(c.c8 != 0 || sparse);
   p.max_workers = int(max_workers);
   p.grid = grid;
   // Self-planned calls: few rows, a variant with the LDS for the plan, and

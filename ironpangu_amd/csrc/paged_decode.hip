@@ -488,7 +488,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
 }
 
 // Persistent decode: workgroup b takes workers b, b + grid, ...; worker v owns
-// the work units [v share, (v + 1) share), i.e. the 32-token tiles j of
+// the work units [lo(v), lo(v + 1)) of Shares (share units each, skewed
+// between odd and even workers for bf16), i.e. the 32-token tiles j of
 // sequence s with seq_pos[s] + seq_cost + 32 j in that range, walked from
 // start_seq[v] in sequence order. The waves of a workgroup take the kv heads of
 // one range, so the halves of every cache row are fetched by sibling waves at
@@ -565,7 +566,7 @@ __device__ __forceinline__ void decode_self_plan_wg(const DecodeParams &p, int *
     last[k] = -1;
     if (len[k] > 0) {
       int wa, wb;
-      seq_workers(int64_t(pos) + p.seq_cost, len[k], share, wa, wb);
+      seq_workers(int64_t(pos) + p.seq_cost, len[k], make_shares(p, share), wa, wb);
       cnt[k] = wb > wa ? wb - wa + 1 : 0;
       last[k] = wb;
       emine = wb;  // nondecreasing along the thread's sequences
@@ -619,7 +620,8 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
     return a;
   };
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
-    const int64_t lo = int64_t(v) * share, hi = lo + share;
+    const Shares sh = make_shares(p, share);
+    const int64_t lo = sh.lo(v), hi = sh.lo(v + 1);
     for (int seq = start_seq(v); seq < p.num_seqs; ++seq) {
       const int64_t first =
           (p.self_plan ? int64_t(s_pos[seq]) : ld_const(p.seq_pos + seq)) + p.seq_cost;  // tile 0
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(64 * max_decode_waves(D), 1) void paged_decode_kern
       j1 = j1 < tiles ? j1 : tiles;
       if (j0 >= j1) continue;
       int slot = p.self_plan ? (s_se[seq] >> 16) - 1 : ld_const(&p.seq_slot[seq].x);
-      if (slot >= 0) slot += v - int(first / share);
+      if (slot >= 0) slot += v - sh.worker(first);
       const int t_end = j1 * kSplitTile < len ? j1 * kSplitTile : len;
       for (int grp = 0; grp < groups; ++grp) {
         const int kvh = uniform(grp * waves_per_wg + wave);  // wave-uniform for SGPR descriptors
@@ -650,6 +652,7 @@ void launch_decode(const DecodeParams &p0, const RowWrite &wr, hipStream_t s) {
   const int waves = p0.kv_heads < max_decode_waves(D) ? p0.kv_heads : max_decode_waves(D);
   DecodeParams p = p0;
   p.self_plan = decode_self_plan(p, 64 * waves) ? 1 : 0;
+  p.skew_pm = decode_skew_pm(C8, D);
   launch_prologue(p, wr, s);
   const int grid = p.grid;
   if (p.block_size == 16)  // the reference's bf16 page (paged_state_contract.h:25)

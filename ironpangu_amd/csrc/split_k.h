@@ -1,13 +1,14 @@
 // Split-K scheduling of the paged GQA decode, and pieces shared with the MLA
-// and prefill planners. The decode splits the call's work into equal
+// and prefill planners. The decode splits the call's work into
 // contiguous shares: every decode sequence weighs its tokens plus a fixed
 // start cost, the prologue kernel prefix-sums the weights on the device and
 // cuts the total into `workers` shares of `share` units (one per persistent
 // workgroup, fewer for small calls), and the workgroups walk their shares tile
-// by tile. A sequence lying in one share writes its output
+// by tile (bf16 calls give odd workers, on odd XCDs, slightly smaller shares:
+// see decode_skew_pm). A sequence lying in one share writes its output
 // directly; one spread over several shares writes an (m, l, O) partial per
 // share into consecutive slots, which a merge launch combines. No work queue,
-// no atomics; all workgroups get the same work. The prologue kernel also
+// no atomics. The prologue kernel also
 // performs the step's slot-mapped row writes, so a decode step is prologue ->
 // decode -> merge from one host call. Calls of up to kSelfPlanPerThread
 // sequences per decode thread plan inside the decode workgroups instead (the
@@ -49,6 +50,7 @@ struct DecodeParams {
   int seq_cost;      // work units charged per sequence on top of its tokens
   int grid;          // persistent decode workgroups (the most workers)
   int self_plan;     // the decode workgroups plan the call themselves (prologue: row writes only)
+  int skew_pm;       // share skew d = S * skew_pm / 1000 (see Shares)
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -66,12 +68,25 @@ __device__ __forceinline__ bool decode_seq(const DecodeParams &p, int seq) {
 __device__ __forceinline__ int64_t share_of(const DecodeParams &p) {
   return ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
 }
+// Contiguous shares of S units, worker pairs (2i, 2i + 1) splitting 2S units
+// as S + d and S - d: worker v starts at unit v S + (v odd ? d : 0).
+struct Shares {
+  int64_t S, d;
+  __device__ int64_t lo(int v) const { return int64_t(v) * S + ((v & 1) ? d : 0); }
+  __device__ int worker(int64_t u) const {  // the worker whose share holds unit u
+    const int64_t pair = u / (2 * S);
+    return int(2 * pair + (u - 2 * S * pair >= S + d ? 1 : 0));
+  }
+};
+__device__ __forceinline__ Shares make_shares(const DecodeParams &p, int64_t share) {
+  return Shares{share, share * p.skew_pm / 1000};
+}
 // Workers holding the first and the last tile of a sequence whose tile 0 sits
 // at work unit `first` (tile j at first + 32 j).
-__device__ __forceinline__ void seq_workers(int64_t first, int len, int64_t share, int &wa, int &wb) {
+__device__ __forceinline__ void seq_workers(int64_t first, int len, const Shares &sh, int &wa, int &wb) {
   const int tiles = (len + kSplitTile - 1) / kSplitTile;
-  wa = int(first / share);
-  wb = int((first + int64_t(kSplitTile) * (tiles - 1)) / share);
+  wa = sh.worker(first);
+  wb = sh.worker(first + int64_t(kSplitTile) * (tiles - 1));
 }
 
 // Exclusive prefix of bucket[0..nb] (nb < 64 * PL) offset by `start`, by the
@@ -224,7 +239,7 @@ __global__ __launch_bounds__(1024) void decode_prologue_kernel(DecodeParams p, R
     int cnt = 0, e = -1;
     if (len > 0) {
       int wa, wb;
-      seq_workers(p.seq_pos[seq] + p.seq_cost, len, share, wa, wb);
+      seq_workers(p.seq_pos[seq] + p.seq_cost, len, make_shares(p, share), wa, wb);
       cnt = wb > wa ? wb - wa + 1 : 0;
       e = wb;
     }
@@ -383,6 +398,21 @@ inline int decode_seq_cost() {
     return (x >= 0 && x <= 65536) ? x : 64;
   }();
   return v;
+}
+// Share skew (permille) of bf16 decode at head_dim <= 128: workgroups are
+// dispatched round-robin over the 8 XCDs, so odd workers run on odd XCDs,
+// whose tiles measured 4-8% slower; giving odd workers 3% fewer units ends the
+// shares closer together (config-2 step 0.2987 -> 0.2956 ms, 16-token pages
+// 1% faster; 1.5% and 4.5% gained less, -3% lost). Head_dim 256 (1.8% slower
+// with the skew) and C8 (no gain) keep equal shares.
+// IFATTN_DECODE_XCD_SKEW (-200..200) overrides every variant.
+inline int decode_skew_pm(bool c8, int head_dim) {
+  static const int v = [] {
+    const char *e = getenv("IFATTN_DECODE_XCD_SKEW");
+    const int x = e ? atoi(e) : 1000;
+    return (x >= -200 && x <= 200) ? x : 1000;
+  }();
+  return v != 1000 ? v : (c8 || head_dim > 128 ? 0 : 30);
 }
 inline int decode_grid() { return device_cus() * wgs_per_cu(); }
 
