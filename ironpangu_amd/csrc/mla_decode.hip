@@ -1133,16 +1133,17 @@ struct MlaCall {
 // keep their index entries within the kSparsePart slot list.
 // Share skew (permille) of dense bf16 calls, as for the GQA decode: odd
 // workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
-// 0.4225 ms with 3%, 0.4307 ms with -3%). C8 and sparse calls keep equal
-// shares (sparse shares are capped by the slot list).
-// IFATTN_MLA_XCD_SKEW (-200..200) overrides the bf16 default.
-inline int mla_skew_pm(bool equal) {
+// 0.4225 ms with 3%, 0.4307 ms with -3%). C8 calls keep equal shares (3%
+// and 6% measured 0.5-1.5% slower), and so do sparse calls (their shares are
+// capped by the slot list). IFATTN_MLA_XCD_SKEW (-200..200) overrides the
+// default of dense calls.
+inline int mla_skew_pm(bool c8, bool sparse) {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_XCD_SKEW");
     const int x = e ? atoi(e) : 1000;
     return (x >= -200 && x <= 200) ? x : 1000;
   }();
-  return equal ? 0 : (v != 1000 ? v : 30);
+  return sparse ? 0 : (v != 1000 ? v : (c8 ? 0 : 30));
 }
 inline int mla_row_cost() {
   static const int v = [] {
@@ -1237,7 +1238,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.row_cost = mla_row_cost();
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
-  p.skew_pm = mla_skew_pm(c.c8 != 0 || sparse);
+  p.skew_pm = mla_skew_pm(c.c8 != 0, sparse);
   p.max_workers = int(max_workers);
   p.grid = grid;
   // Self-planned calls: few rows, a variant with the LDS for the plan, and
