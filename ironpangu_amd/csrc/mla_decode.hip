@@ -1128,23 +1128,23 @@ struct MlaCall {
   void *stream;
 };
 
-// Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
-// share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
-// keep their index entries within the kSparsePart slot list.
 // Share skew (permille) of dense bf16 calls, as for the GQA decode: odd
 // workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
-// 0.4225 ms with 3%, 0.4307 ms with -3%). C8 calls keep equal shares (3%
-// and 6% measured 0.5-1.5% slower), and so do sparse calls (their shares are
-// capped by the slot list). IFATTN_MLA_XCD_SKEW (-200..200) overrides the
-// default of dense calls.
+// 0.4225 ms with 3%; 0.4307 ms with the opposite skew). C8 calls keep equal
+// shares (3% and 6% measured 0.5-1.5% slower), and so do sparse calls (their
+// shares are capped by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides
+// the default of dense calls.
 inline int mla_skew_pm(bool c8, bool sparse) {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_XCD_SKEW");
     const int x = e ? atoi(e) : 1000;
-    return (x >= -200 && x <= 200) ? x : 1000;
+    return (x >= 0 && x <= 200) ? x : 1000;
   }();
   return sparse ? 0 : (v != 1000 ? v : (c8 ? 0 : 30));
 }
+// Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
+// share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
+// keep their index entries within the kSparsePart slot list.
 inline int mla_row_cost() {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_ROW_COST");

@@ -69,7 +69,9 @@ __device__ __forceinline__ int64_t share_of(const DecodeParams &p) {
   return ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
 }
 // Contiguous shares of S units, worker pairs (2i, 2i + 1) splitting 2S units
-// as S + d and S - d: worker v starts at unit v S + (v odd ? d : 0).
+// as S + d and S - d: worker v starts at unit v S + (v odd ? d : 0). With
+// 0 <= d < S the n = ceil(total / S) workers cover every unit: lo(n) is n S
+// (n even) or n S + d (n odd), both >= total.
 struct Shares {
   int64_t S, d;
   __device__ int64_t lo(int v) const { return int64_t(v) * S + ((v & 1) ? d : 0); }
@@ -403,14 +405,14 @@ inline int decode_seq_cost() {
 // dispatched round-robin over the 8 XCDs, so odd workers run on odd XCDs,
 // whose tiles measured 4-8% slower; giving odd workers 3% fewer units ends the
 // shares closer together (config-2 step 0.2987 -> 0.2956 ms, 16-token pages
-// 1% faster; 1.5% and 4.5% gained less, -3% lost). Head_dim 256 (1.8% slower
-// with the skew) and C8 (no gain) keep equal shares.
-// IFATTN_DECODE_XCD_SKEW (-200..200) overrides every variant.
+// 1% faster; 1.5% and 4.5% gained less, the opposite skew lost). Head_dim 256
+// (1.8% slower with the skew) and C8 (no gain) keep equal shares.
+// IFATTN_DECODE_XCD_SKEW (0..200) overrides every variant.
 inline int decode_skew_pm(bool c8, int head_dim) {
   static const int v = [] {
     const char *e = getenv("IFATTN_DECODE_XCD_SKEW");
     const int x = e ? atoi(e) : 1000;
-    return (x >= -200 && x <= 200) ? x : 1000;
+    return (x >= 0 && x <= 200) ? x : 1000;
   }();
   return v != 1000 ? v : (c8 || head_dim > 128 ? 0 : 30);
 }
