@@ -532,9 +532,11 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     for (int s = 0; s < KS; ++s) qv[s] = buf_load_x4(rq, qh + uint32_t(DPW * w + 32 * s + 8 * g) * 2);
     qv[KS] = buf_load_x4(rq, (w < 2 ? qh : 0x80000000u) + uint32_t(512 + 32 * w + 8 * g) * 2);
   }
-  const int tile0 = sp.base + j0 * kMlaTile;
-  const int t_begin = sp.lo > tile0 ? sp.lo : tile0;
-  const int t_end = sp.hi < sp.base + j1 * kMlaTile ? sp.hi : sp.base + j1 * kMlaTile;
+  // Wave-uniform (scalar) range bounds: the tile address arithmetic below
+  // then runs on the scalar unit.
+  const int tile0 = uniform(sp.base + j0 * kMlaTile);
+  const int t_begin = uniform(sp.lo > tile0 ? sp.lo : tile0);
+  const int t_end = uniform(sp.hi < sp.base + j1 * kMlaTile ? sp.hi : sp.base + j1 * kMlaTile);
   const int n_tiles = j1 - j0;
   const int bs = p.block_size;
   const int64_t seq_table = int64_t(sp.seq) * p.table_stride;
