@@ -206,3 +206,24 @@ def test_self_plan_row_limit(rows, c8):
                 idx[t, :n] = rng.choice(max(causal, 1), size=n, replace=False)
     got, exp = run(q, cache, table, kv, maxc, cu=cu, idx=idx, sk=sk, sv=sv)
     assert_close(got, exp)
+
+
+@pytest.mark.parametrize("c8,with_sinks", [(False, False), (False, True), (True, False)])
+def test_merge_partial_counts(c8, with_sinks):
+    """One row split over 6 to 11 shares (at least 512 units per share): the
+    merge's one-round-trip path (at most 8 partials, counting the sink
+    partial) and its general path on both sides of the limit. C8 rows go
+    through the dense decode entry (the general entry takes index lists)."""
+    import torch
+    from ironpangu_amd import ops
+    sk, sv = sinks(128, 31) if with_sinks else (None, None)
+    for kv in (2900, 3300, 3552, 3800, 4064, 4400, 4700, 5400):
+        q, cache, table, kvs, cu, maxc = batch(kv, [1], [kv], 64, 16, c8)
+        if c8:
+            out = ops.mla_decode(to_dev(q), to_dev(cache), to_dev(table), to_dev(kvs), maxc)
+            torch.cuda.synchronize()
+            got = bf16_host(out)
+            exp = oracle.mla_decode(q, cache.reshape(-1, 656), table, kvs, 16, 64, SCALE, c8=True)
+        else:
+            got, exp = run(q, cache, table, kvs, maxc, cu=cu, sk=sk, sv=sv)
+        assert_close(got, exp, what=f"kv {kv}")
