@@ -26,6 +26,12 @@ import test_gpu_mla_attention as m
 for shape in [(16, 2, 128, 128), (16, 2, 128, 32), (8, 8, 64, 32), (32, 2, 128, 64)]:
     d.test_decode_shapes(*shape)
 d.test_decode_many_partitions()
+d.test_decode_shares_slide_the_block_window()
+d.test_decode_many_sequences()
+d.test_decode_16_token_pages(128, False)
+d.test_decode_step_matches_write_then_decode()
+for seed in range(4):
+    d.test_decode_random_shapes(seed)
 d.test_decode_self_plan_limit(2, 513)
 for rows in (1, 4, 16):
     m.test_window_ring_probe(rows)
@@ -42,6 +48,6 @@ def test_extreme_skew(wgs):
     env = dict(os.environ, IFATTN_DECODE_XCD_SKEW="200", IFATTN_MLA_XCD_SKEW="200",
                IFATTN_DECODE_WGS_PER_CU=wgs)
     r = subprocess.run([sys.executable, "-c", CASES.format(tests=str(TESTS))], env=env,
-                       capture_output=True, text=True, timeout=100)
+                       capture_output=True, text=True, timeout=200)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
     assert "skew cases passed" in r.stdout
