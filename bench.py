@@ -53,11 +53,6 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=64)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (counter calibration)")
-    ap.add_argument("--read-ceiling", action="store_true",
-                    help="only measure the HBM read ceiling (64 KiB blocks over an 8.6 GB footprint)")
-    ap.add_argument("--issue-probe", action="store_true",
-                    help="only measure how MFMA, VALU, exponentials and LDS reads share a SIMD "
-                         "(the prefill tile loop's instruction mix)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip configs 3-5 (reported under 'secondary')")
     ap.add_argument("--only", choices=sorted(SECONDARY),
@@ -661,116 +656,6 @@ def bench_norm_rope_write(seed, steps, warmup):
                          "note": "launch-bound at this size (8.5 MB per call)"}}
 
 
-def read_ceiling(steps, sweep=False):
-    """HBM read ceiling for the decode's access pattern: every 64 KiB block of an
-    8.6 GB footprint (config 2's K + V pools) read once per launch, in order or
-    in a random order, with the default and the nontemporal cache policy. The
-    best of a few launch shapes (workgroups per CU, blocks in flight) is kept."""
-    import ctypes as C
-    import torch
-    lib = C.CDLL(str(ROOT / "ironpangu_amd" / "libifattn_probe.so"))
-    lib.ifattn_probe_read_blocks.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
-                                             C.c_int32, C.c_void_p, C.c_int32, C.c_void_p]
-    nblocks = 2 * 65536
-    buf = torch.ones(nblocks * 65536, dtype=torch.uint8, device="cuda")
-    sink = torch.zeros(4096, dtype=torch.uint8, device="cuda")
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    g = torch.Generator(device="cuda")
-    g.manual_seed(1)
-    orders = {"sequential": torch.arange(nblocks, dtype=torch.int32, device="cuda"),
-              "random_64KiB": torch.randperm(nblocks, generator=g, device="cuda").to(torch.int32)}
-    res, shapes = {}, {}
-    for name, order in orders.items():
-        for nt in (0, 1):
-            best = None
-            for wgs in (2, 4, 8):
-                for unroll in (1, 2):
-                    def run():
-                        st = lib.ifattn_probe_read_blocks(buf.data_ptr(), order.data_ptr(), nblocks,
-                                                          nt, unroll, sink.data_ptr(), cus * wgs,
-                                                          torch.cuda.current_stream().cuda_stream)
-                        assert st == 0
-                    gbps = nblocks * 65536 / timed(run, steps, 2) / 1e6
-                    if sweep:
-                        shapes[f"{name}_{'nt' if nt else 'default'}_wg{wgs}_u{unroll}"] = round(gbps, 1)
-                    best = max(best or 0.0, gbps)
-            res[f"{name}_{'nontemporal' if nt else 'default'}_GBps"] = round(best, 1)
-    # Row gathers at random row offsets: the per-position K/V half rows of the
-    # gated attention (512 of 1024 B), packed C8 MLA rows (656 B) and bf16 MLA
-    # rows (1152 B); about 750 MB per launch from a pool of the buffer's size.
-    lib.ifattn_probe_gather_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32,
-                                             C.c_int64, C.c_int32, C.c_void_p, C.c_int32,
-                                             C.c_void_p]
-    for row_bytes, stride in ((512, 1024), (656, 656), (1152, 1152)):
-        pool = buf.numel() // stride
-        nrows = (750 << 20) // row_bytes
-        order = torch.randint(0, pool, (nrows,), generator=g, device="cuda", dtype=torch.int32)
-        for nt in (0, 1):
-            best = None
-            for wgs in (4, 8, 16):
-                def run():
-                    st = lib.ifattn_probe_gather_rows(buf.data_ptr(), order.data_ptr(), nrows,
-                                                      row_bytes, stride, nt, sink.data_ptr(),
-                                                      cus * wgs, torch.cuda.current_stream().cuda_stream)
-                    assert st == 0
-                gbps = nrows * row_bytes / timed(run, steps, 2) / 1e6
-                if sweep:
-                    shapes[f"rows{row_bytes}_{'nt' if nt else 'default'}_wg{wgs}"] = round(gbps, 1)
-                best = max(best or 0.0, gbps)
-            res[f"random_rows_{row_bytes}B_{'nontemporal' if nt else 'default'}_GBps"] = round(best, 1)
-        del order
-    out = {"read_ceiling": res, "bytes_per_launch": nblocks * 65536,
-           "note": "blocks: best over 2/4/8 four-wave workgroups per CU and 1/2 blocks in flight "
-                   "per workgroup, 16-byte loads over whole 64 KiB blocks; rows: about 750 MB of "
-                   "rows at random offsets (stride 1024, 656, 1152 B), 8 loads in flight per "
-                   "thread, best over 4/8/16 workgroups per CU"}
-    if sweep:
-        out["shapes"] = shapes
-    return out
-
-
-def issue_probe(steps):
-    """Time per iteration of the issue-overlap probe modes (probe/issue_overlap.hip):
-    256 workgroups of eight waves, two per SIMD, 20000 iterations each. The
-    'hidden' figures compare a combined mode with the sum and the max of its
-    parts: 0 when the parts serialise, 1 when the shorter part hides fully."""
-    import ctypes as C
-    import torch
-    lib = C.CDLL(str(ROOT / "ironpangu_amd" / "libifattn_probe.so"))
-    lib.ifattn_probe_issue.argtypes = [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]
-    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
-    iters = 20000
-    names = ["mfma16", "exp32", "fma32", "mfma16|exp32_other_wave", "mfma16|fma32_other_wave",
-             "mfma16+exp32_same_wave", "mfma16+fma32_same_wave", "lds_b128x8", "lds_tr_b64x16",
-             "lds_b128x8+mfma16"]
-    ns = {}
-    for mode, name in enumerate(names):
-        def run():
-            assert lib.ifattn_probe_issue(mode, iters, sink.data_ptr(),
-                                          torch.cuda.current_stream().cuda_stream) == 0
-        ns[name] = timed(run, steps, 1) * 1e6 / iters
-    one = {k: ns[k] / 2 for k in ("mfma16", "exp32", "fma32")}  # one wave's share of the SIMD
-
-    def hidden(both, a, b):
-        s, m = a + b, max(a, b)
-        return round((s - both) / (s - m), 2)
-    out = {"ns_per_iteration": {k: round(v, 1) for k, v in ns.items()},
-           "hidden": {
-               "exp_vs_mfma_other_wave": hidden(ns["mfma16|exp32_other_wave"], one["mfma16"], one["exp32"]),
-               "fma_vs_mfma_other_wave": hidden(ns["mfma16|fma32_other_wave"], one["mfma16"], one["fma32"]),
-               "exp_vs_mfma_same_wave": hidden(ns["mfma16+exp32_same_wave"], ns["mfma16"], ns["exp32"]),
-               "fma_vs_mfma_same_wave": hidden(ns["mfma16+fma32_same_wave"], ns["mfma16"], ns["fma32"]),
-               "lds_vs_mfma_same_wave": hidden(ns["lds_b128x8+mfma16"], ns["mfma16"], ns["lds_b128x8"])},
-           "lds_bytes_per_ns_per_cu": {
-               "b128": round(8 * 8 * 1024 / ns["lds_b128x8"], 1),
-               "tr_b64": round(8 * 16 * 512 / ns["lds_tr_b64x16"], 1)},
-           "note": "ns per iteration of eight waves per CU (two per SIMD); mfma16 = 16 MFMA "
-                   "16x16x32 bf16 per wave, exp32/fma32 = 32 v_exp_f32/v_fma_f32 per wave, lds = "
-                   "8 ds_read_b128 or 16 ds_read_b64_tr_b16 per wave (the prefill operand patterns)"}
-    return out
-
-
-# Secondary workloads, in report order.
 SECONDARY = {
     "c8_decode": bench_c8,
     "mla_decode": bench_mla,
@@ -799,14 +684,6 @@ def main():
 
     if args.only:
         print(json.dumps({args.only: SECONDARY[args.only](args.seed, args.steps, args.warmup)}))
-        return
-
-    if args.issue_probe:
-        print(json.dumps(issue_probe(max(args.steps, 5))))
-        return
-
-    if args.read_ceiling:
-        print(json.dumps(read_ceiling(max(args.steps, 5), sweep=True)))
         return
 
     if args.calibrate_copy:

@@ -160,6 +160,20 @@ int32_t ifattn_gated_paged_attention_bf16(const void *q, const void *k, const vo
                                           int64_t slots, int64_t context, void *workspace,
                                           uint64_t workspace_bytes, void *stream);
 
+/* The producer of the Qwen attention's q, k and gate: per-head zero-centred RMS
+ * norm (eps 1e-6, fp32 gamma = 1 + checkpoint weight), partial RoPE on the first
+ * 64 of 256 channels (theta 1e7, cos/sin rounded to bf16) and the sigmoid gate,
+ * in one launch. Replaces inferfabric_acl_attention_qk_prepare's ACLNN steps
+ * (native/src/inferfabric_acl.cpp:1236-1341; CPU statement
+ * crates/inferfabric-cli/src/npu_probe/attention.rs:35-64), same operands:
+ *   packed_q [batch, 8, 512] bf16 (256 query then 256 gate channels per head);
+ *   k [batch, 2, 256] bf16; q_gamma, k_gamma [256] fp32; positions [batch] int64;
+ *   q_out [batch, 8, 256], k_out [batch, 2, 256], gate [batch, 8, 256] bf16.
+ * batch 1..64 as the reference. */
+int32_t ifattn_qk_norm_rope_gate_bf16(const void *packed_q, const void *k, const float *q_gamma,
+                                      const float *k_gamma, const int64_t *positions, void *q_out,
+                                      void *k_out, void *gate, int64_t batch, void *stream);
+
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): ifattn_paged_decode_step_bf16 without a workspace. The

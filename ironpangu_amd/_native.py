@@ -58,6 +58,7 @@ SIGNATURES = {
     "ifattn_gated_paged_attention_workspace_size": (u64, [i64, i64]),
     "ifattn_gated_paged_attention_bf16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64,
                                                 i64, vp, u64, vp]),
+    "ifattn_qk_norm_rope_gate_bf16": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
     "ifattn_varlen_prefill_workspace_size": (u64, [i32, i32, i32, i32, i32]),
     "ifattn_varlen_prefill_bf16": (i32, [vp, vp, vp, vp, i32, vp, vp, vp, i32, i32, i32, i32, i32,
                                          i32, i32, i32, i64, f32, vp, u64, vp]),

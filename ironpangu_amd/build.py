@@ -3,8 +3,9 @@
 Every ``csrc/*.hip`` file is compiled for gfx950 with hipcc and every
 ``csrc/*.cpp`` file as host C++, in parallel, into ``_build/``; the objects
 are linked into ``ironpangu_amd/libifattn_hip.so`` next to this file. The
-IFKernelV1 plug-in shims (one ``libifk_<name>.so`` per operator contract) are
-linked against it with an ``$ORIGIN`` rpath.
+IFKernelV1 plug-in shims (one ``libifk_<name>.so`` per operator contract) and
+the session-ABI library ``libinferfabric_acl.so`` are linked against it with an
+``$ORIGIN`` rpath.
 """
 from __future__ import annotations
 
@@ -18,6 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libifattn_hip.so"
+SESSION_LIB = PKG / "libinferfabric_acl.so"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 
@@ -98,9 +100,14 @@ def build(jobs: int | None = None, plugins: bool = True) -> Path:
                   f"-L{PKG}", "-lifattn_hip", "-Wl,-rpath,$ORIGIN", "-o", str(out)])
         with cf.ThreadPoolExecutor(jobs) as ex:
             list(ex.map(one, PLUGINS.items()))
-    probes = sorted((PKG / "probe").glob("*.hip"))
-    if probes:  # measurement-only library for bench.py --read-ceiling / --issue-probe
-        _run([_hipcc(), *HIP_FLAGS, "-shared", *map(str, probes), "-o", str(PKG / "libifattn_probe.so")])
+    session = PKG / "session" / "inferfabric_acl.cpp"
+    if session.exists():  # the reference's session ABI, over libifattn_hip.so
+        exports = BUILD / "inferfabric_acl.map"  # export the ABI's symbols only
+        exports.write_text("{ global: inferfabric_acl_*; local: *; };\n")
+        _run(["g++", *HOST_FLAGS, f"-Wl,--version-script={exports}", f"-I{ROCM}/include",
+              "-shared", str(session), f"-L{PKG}",
+              "-lifattn_hip", f"-L{ROCM}/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+              f"-Wl,-rpath,{ROCM}/lib", "-o", str(SESSION_LIB)])
     driver = CSRC.parent / "driver" / "ifattn_drive.cpp"
     if driver.exists():
         _run(["g++", *HOST_FLAGS, f"-I{ROCM}/include", str(driver), f"-L{ROCM}/lib",

@@ -258,6 +258,28 @@ def gated_paged_attention(q, k, v, gate, keys, values, append, table, mask, out=
     return out
 
 
+def qk_norm_rope_gate(packed_q, k, q_gamma, k_gamma, positions, stream=None):
+    """Qwen attention producer (inferfabric_acl_attention_qk_prepare): per-head
+    RMS norm of q (packed [batch, 8, 512], query then gate channels) and k
+    [batch, 2, 256], partial RoPE at ``positions`` [batch] int64, sigmoid gate.
+    Returns (q [batch, 8, 256], k [batch, 2, 256], gate [batch, 8, 256]) bf16."""
+    _dev(packed_q, k, q_gamma, k_gamma, positions)
+    _req(packed_q.dtype == torch.bfloat16 and packed_q.dim() == 3
+         and tuple(packed_q.shape[1:]) == (8, 512), "packed_q: bf16 [batch, 8, 512]")
+    batch = packed_q.shape[0]
+    _req(k.dtype == torch.bfloat16 and tuple(k.shape) == (batch, 2, 256), "k: bf16 [batch, 2, 256]")
+    for g, n in ((q_gamma, "q_gamma"), (k_gamma, "k_gamma")):
+        _req(g.dtype == torch.float32 and g.numel() == 256, f"{n}: fp32 [256]")
+    _req(positions.dtype == torch.int64 and positions.numel() == batch, "positions: int64 [batch]")
+    q_out = torch.empty((batch, 8, 256), dtype=torch.bfloat16, device=packed_q.device)
+    k_out = torch.empty((batch, 2, 256), dtype=torch.bfloat16, device=packed_q.device)
+    gate = torch.empty_like(q_out)
+    check(lib().ifattn_qk_norm_rope_gate_bf16(
+        _ptr(packed_q), _ptr(k), _ptr(q_gamma), _ptr(k_gamma), _ptr(positions), _ptr(q_out),
+        _ptr(k_out), _ptr(gate), batch, _stream(stream)), "ifattn_qk_norm_rope_gate_bf16")
+    return q_out, k_out, gate
+
+
 # ---------------------------------------------------------------- varlen prefill
 
 def prefill_workspace(num_seqs, total_q, q_heads, head_dim, max_kv_len, device="cuda"):

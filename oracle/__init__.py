@@ -49,10 +49,11 @@ def lib():
                                            vp, vp, i32, vp, i32, i32, f32, i32]
         l.oracle_gated_attention.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32,
                                              f32, i32]
+        l.oracle_qk_norm_rope_gate.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i32]
         l.oracle_hardware_threads.restype = i32
         for f in ("oracle_kv_write", "oracle_quant_rows", "oracle_quant_legacy",
                   "oracle_dequant_legacy", "oracle_mla_pack_c8", "oracle_mla_norm_rope_write",
-                  "oracle_paged_decode", "oracle_gated_attention",
+                  "oracle_paged_decode", "oracle_gated_attention", "oracle_qk_norm_rope_gate",
                   "oracle_varlen_prefill", "oracle_mla_decode", "oracle_mla_attention"):
             getattr(l, f).restype = None
         _lib = l
@@ -245,3 +246,21 @@ def gated_attention(q, keys, values, table, mask, gate, hq=8, hkv=2, d=256, scal
     lib().oracle_gated_attention(_p(q), _p(keys), _p(values), _p(table), _p(mask), _p(gate),
                                  _p(out), batch, context, hq, hkv, d, float(scale), threads)
     return out
+
+
+def qk_norm_rope_gate(packed_q, k, q_gamma, k_gamma, positions):
+    """(q [batch, 8, 256], k [batch, 2, 256], gate [batch, 8, 256]) as bf16 bits from
+    packed q bf16 bits [batch, 8, 512], k bf16 bits [batch, 2, 256], fp32 gammas [256]
+    and int64 positions [batch]."""
+    packed_q = _c(packed_q, np.uint16)
+    k = _c(k, np.uint16)
+    q_gamma = _c(q_gamma, np.float32)
+    k_gamma = _c(k_gamma, np.float32)
+    positions = _c(positions, np.int64)
+    batch = positions.shape[0]
+    q_out = np.zeros((batch, 8, 256), np.uint16)
+    k_out = np.zeros((batch, 2, 256), np.uint16)
+    gate = np.zeros((batch, 8, 256), np.uint16)
+    lib().oracle_qk_norm_rope_gate(_p(packed_q), _p(k), _p(q_gamma), _p(k_gamma), _p(positions),
+                                   _p(q_out), _p(k_out), _p(gate), batch)
+    return q_out, k_out, gate

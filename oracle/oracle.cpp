@@ -32,6 +32,11 @@
 //                          Pinned: equality with oracle_paged_decode when the mask opens
 //                          a prefix (gate 1), mask-shift invariance, gate linearity,
 //                          a two-position closed form with mask and gate.
+//   oracle_qk_norm_rope_gate  the Qwen attention producer, inferfabric_acl.cpp:1236-1341
+//                          and its CPU statement attention.rs:35-64. Pinned: position 0
+//                          leaves the norm unrotated, rotation preserves pair norms,
+//                          gamma 1 gives unit RMS, constant rows, sigmoid(0) = 1/2,
+//                          a hand-computed rotation at position 1.
 //   oracle_varlen_prefill  causal rule of openpangu_attention_metadata.h:20-22.
 //                          Pinned: q = 0 causal prefix means, decode-row equivalence.
 //   oracle_mla_decode      packed_cache_probe.cpp:47-66 / sliding_window_probe.cpp:144-163
@@ -353,6 +358,50 @@ void oracle_gated_attention(const uint16_t *q, const uint16_t *keys, const uint1
     const uint16_t *gh = gate + (int64_t(b) * hq + h) * d;
     for (int e = 0; e < d; ++e) o[e] *= bf(gh[e]);
   });
+}
+
+// Qwen q/k producer (inferfabric_acl_attention_qk_prepare,
+// native/src/inferfabric_acl.cpp:1236-1341; CPU statement
+// crates/inferfabric-cli/src/npu_probe/attention.rs:35-64). Per request r and head:
+// n_j = bf16((x_j * inv) * gamma_j), inv = 1 / sqrt(sum(x^2) / 256 + 1e-6);
+// for j < 32 angle = position[r] * f_j with f_j = 1 / 1e7^(j/32) in fp32
+// (the C++ operator's table, :1249-1257; the Rust statement divides by 1e7^(j/32)
+// instead), c, s = bf16(cos), bf16(sin);
+// out_j = bf16(bf16(n_j c) - bf16(n_{j+32} s)), out_{j+32} = bf16(bf16(n_{j+32} c) + bf16(n_j s)).
+// q heads read channels [0, 256) of a 512-wide packed head whose upper half is
+// the gate: gate = bf16(1 / (1 + exp(-g))) (:1329-1339). Outputs are bf16 bits.
+void oracle_qk_norm_rope_gate(const uint16_t *packed_q, const uint16_t *k, const float *q_gamma,
+                              const float *k_gamma, const int64_t *positions, uint16_t *q_out,
+                              uint16_t *k_out, uint16_t *gate, int32_t batch) {
+  constexpr int kD = 256;
+  float freq[32];
+  for (int i = 0; i < 32; ++i) freq[i] = 1.0f / std::pow(10000000.0f, float(i) / 32.0f);
+  for (int r = 0; r < batch; ++r) {
+    for (int which = 0; which < 2; ++which) {
+      const int heads = which == 0 ? 8 : 2, stride = which == 0 ? 2 * kD : kD;
+      const float *gamma = which == 0 ? q_gamma : k_gamma;
+      for (int h = 0; h < heads; ++h) {
+        const uint16_t *x = (which == 0 ? packed_q : k) + (int64_t(r) * heads + h) * stride;
+        uint16_t *o = (which == 0 ? q_out : k_out) + (int64_t(r) * heads + h) * kD;
+        float ss = 0.0f;
+        for (int j = 0; j < kD; ++j) ss += bf(x[j]) * bf(x[j]);
+        const float inv = 1.0f / std::sqrt(ss / float(kD) + 1e-6f);
+        float n[kD];
+        for (int j = 0; j < kD; ++j) n[j] = round_bf((bf(x[j]) * inv) * gamma[j]);
+        for (int j = 0; j < kD; ++j) o[j] = to_bf(n[j]);
+        for (int j = 0; j < 32; ++j) {
+          const float angle = float(positions[r]) * freq[j];
+          const float c = round_bf(std::cos(angle)), sn = round_bf(std::sin(angle));
+          o[j] = to_bf(round_bf(n[j] * c) - round_bf(n[j + 32] * sn));
+          o[j + 32] = to_bf(round_bf(n[j + 32] * c) + round_bf(n[j] * sn));
+        }
+        if (which == 0)
+          for (int j = 0; j < kD; ++j)
+            gate[(int64_t(r) * heads + h) * kD + j] =
+                to_bf(1.0f / (1.0f + std::exp(-bf(x[kD + j]))));
+      }
+    }
+  }
 }
 
 // Packed varlen causal attention over paged bf16 caches. Row t of sequence s
