@@ -296,6 +296,26 @@ int32_t ifattn_mla_window_attention_bf16(const void *q, const void *cache,
                                          int32_t max_context, float scale, void *workspace,
                                          uint64_t workspace_bytes, void *stream);
 
+/* The same window attention over row-quantized latent rows, as if_cache_quantize
+ * writes them (native/kernels/cache_quantization.cpp:12-38): row i of the cache
+ * is 576 int8 codes (bits 8, 576 bytes) or 576 int4 codes (bits 4, 288 bytes,
+ * two's complement, element 2b in the low nibble of byte b), with one fp32 scale
+ * row_scales[i]; value = code * scale. The codes are dequantized in registers,
+ * so the cache is read once as stored. Replaces the reference's integer-cache
+ * path, which dequantizes the whole cache to bf16 (if_cache_dequantize,
+ * token_executor.h:806-822) before the window attention (:863-906). The cache
+ * must be below 4 GiB; block_size a power of two >= 16. Workspace as
+ * ifattn_mla_attention_workspace_size (topk 0). */
+int32_t ifattn_mla_window_attention_rowq(const void *q, const void *cache, const float *row_scales,
+                                         int32_t bits, const int32_t *block_tables,
+                                         int32_t table_stride, const int32_t *cu_seqlens_q,
+                                         const int32_t *kv_lens, int32_t num_seqs, int32_t num_rows,
+                                         int32_t window, const void *sink_keys,
+                                         const void *sink_values, int32_t n_sinks, void *out,
+                                         int32_t heads, int32_t block_size, int64_t num_blocks,
+                                         int32_t max_context, float scale, void *workspace,
+                                         uint64_t workspace_bytes, void *stream);
+
 /* Packed C8 rows (656 bytes) over each row's candidate list indices[row][0..topk):
  * logical positions of its sequence, the first min(causal, topk) distinct and
  * < causal, then -1 (openpangu_attention_metadata.h:10-37); -1 or out-of-table

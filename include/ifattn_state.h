@@ -83,9 +83,10 @@ int32_t ifattn_attention_state_set_length(ifattn_attention_state *state, int32_t
 /* Attention of the query buffer into the output buffer over the device table
  * and length: bf16 states run the window attention (window 0 = every cached
  * key), packed C8 states the sparse attention over the indices buffer; with
- * sinks != 0 the 128 sink rows join the softmax. Row-quantized states are
- * dequantized by the caller first (if_cache_dequantize) and are rejected here.
- * Scale 1/sqrt(192). */
+ * sinks != 0 the 128 sink rows join the softmax. Row-quantized states run the
+ * window attention over their int8 / int4 codes and row scales directly
+ * (ifattn_mla_window_attention_rowq), where the reference first dequantizes
+ * the cache to bf16 (token_executor.h:806-822). Scale 1/sqrt(192). */
 int32_t ifattn_attention_state_attend(ifattn_attention_state *state, int32_t window,
                                       int32_t sinks, void *stream);
 

@@ -70,6 +70,8 @@ SIGNATURES = {
     "ifattn_mla_attention_workspace_size": (u64, [i32, i32, i32, i32, i32, i32, i32]),
     "ifattn_mla_window_attention_bf16": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, vp, i32,
                                                vp, i32, i32, i64, i32, f32, vp, u64, vp]),
+    "ifattn_mla_window_attention_rowq": (i32, [vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, i32, vp,
+                                               vp, i32, vp, i32, i32, i64, i32, f32, vp, u64, vp]),
     "ifattn_mla_sparse_attention_c8": (i32, [vp, vp, vp, i32, vp, i32, vp, vp, i32, i32, vp, vp,
                                              i32, vp, i32, i32, i64, i32, f32, vp, u64, vp]),
     "ifattn_page_reset": (i32, [vp, u64, vp, u64, vp]),

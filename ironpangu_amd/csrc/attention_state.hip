@@ -4,6 +4,7 @@
 // (native/src/openpangu_decoder_state.h:16-48). Geometry and the host metadata
 // (append, blocks) follow that class; attention runs the gfx950 MLA kernels of
 // mla_decode.hip over the state's own buffers.
+#include <cstdlib>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -31,29 +32,47 @@ struct ifattn_attention_state {
   void *workspace = nullptr;
   uint64_t workspace_bytes = 0;
   int device = -1;
+  bool ready = false;  // every device buffer allocated and initialised
   std::mutex alloc_mutex;
   std::vector<int32_t> host_table;
 
   ~ifattn_attention_state() {
+    free_buffers();
+    ifattn_pages_destroy(pages);
+  }
+  void free_buffers() {
     void *ptrs[] = {buf.cache, buf.table, buf.scales, buf.query, buf.out, buf.indices,
                     buf.kv_len, buf.sink_keys, buf.sink_values, workspace};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
-    ifattn_pages_destroy(pages);
+    buf = ifattn_attention_state_buffers{};
+    workspace = nullptr;
+    workspace_bytes = 0;
+    ready = false;
   }
   bool sparse() const { return geo.format == IFATTN_STATE_PACKED_C8; }
   uint32_t max_context() const { return geo.table_entries * geo.page_tokens; }
 
-  // Device buffers on the current device, once.
+  // Device buffers on the current device, once. A failure part way frees
+  // what was allocated, so the next call starts again from nothing.
   int32_t ensure_buffers() {
     std::lock_guard<std::mutex> lock(alloc_mutex);
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return fail(IFATTN_ELAUNCH, "attention state: no device");
-    if (buf.cache) {
+    if (ready) {
       if (dev != device) return reject("attention state: buffers live on another device");
       return IFATTN_OK;
     }
+    const int32_t st = allocate_buffers();
+    if (st != IFATTN_OK) {
+      free_buffers();
+      return st;
+    }
     device = dev;
+    ready = true;
+    return IFATTN_OK;
+  }
+  int32_t allocate_buffers() {
     struct Req {
       void **ptr;
       uint64_t bytes;
@@ -69,15 +88,22 @@ struct ifattn_attention_state {
                              {reinterpret_cast<void **>(&buf.sink_values), uint64_t(kSinks) * 512 * 2}};
     if (geo.format == IFATTN_STATE_ROW_QUANT)
       reqs.push_back({reinterpret_cast<void **>(&buf.scales), uint64_t(capacity) * 4});
-    else {
-      workspace_bytes = ifattn_mla_attention_workspace_size(1, int32_t(geo.heads), int32_t(max_context()),
-                                                            0, sparse() ? kTopK : 0, int32_t(kSinks),
-                                                            int32_t(geo.page_tokens));
-      reqs.push_back({&workspace, workspace_bytes});
-    }
+    workspace_bytes = ifattn_mla_attention_workspace_size(1, int32_t(geo.heads), int32_t(max_context()),
+                                                          0, sparse() ? kTopK : 0, int32_t(kSinks),
+                                                          int32_t(geo.page_tokens));
+    reqs.push_back({&workspace, workspace_bytes});
+    // Test hook: IFATTN_STATE_FAIL_ALLOCATION=i fails the i-th allocation, so
+    // a test can force the clean-up path from the host.
+    const char *hook = getenv("IFATTN_STATE_FAIL_ALLOCATION");
+    const int fail_allocation_at = hook ? atoi(hook) : -1;
     for (auto &r : reqs) {
-      if (hipMalloc(r.ptr, r.bytes ? r.bytes : 16) != hipSuccess ||
-          hipMemset(*r.ptr, 0, r.bytes ? r.bytes : 16) != hipSuccess)
+      if (fail_allocation_at >= 0 && int(&r - reqs.data()) == fail_allocation_at)
+        return fail(IFATTN_ELAUNCH, "attention state: device allocation failed");
+      if (hipMalloc(r.ptr, r.bytes ? r.bytes : 16) != hipSuccess) {
+        *r.ptr = nullptr;
+        return fail(IFATTN_ELAUNCH, "attention state: device allocation failed");
+      }
+      if (hipMemset(*r.ptr, 0, r.bytes ? r.bytes : 16) != hipSuccess)
         return fail(IFATTN_ELAUNCH, "attention state: device allocation failed");
     }
     // The reference's initial table: entry i -> page i mod (capacity / page).
@@ -212,14 +238,19 @@ extern "C" int32_t ifattn_attention_state_set_length(ifattn_attention_state *sta
 extern "C" int32_t ifattn_attention_state_attend(ifattn_attention_state *state, int32_t window,
                                                  int32_t sinks, void *stream) {
   if (!state) return reject("attention state: null state");
-  if (state->geo.format == IFATTN_STATE_ROW_QUANT)
-    return reject("attention state: row-quantized caches are dequantized before attention");
   if (window < 0) return reject("attention state: window must be >= 0");
   if (const int32_t st = state->ensure_buffers()) return st;
   const auto &b = state->buf;
   const auto &g = state->geo;
   const float scale = 0.07216878364870322f;  // 1/sqrt(192)
   const int32_t n_sinks = sinks ? int32_t(kSinks) : 0;
+  if (g.format == IFATTN_STATE_ROW_QUANT)  // codes dequantized in registers
+    return ifattn_mla_window_attention_rowq(
+        b.query, b.cache, b.scales, int32_t(state->bits), b.table, int32_t(g.table_entries), nullptr,
+        b.kv_len, 1, 1, window, sinks ? b.sink_keys : nullptr, sinks ? b.sink_values : nullptr,
+        n_sinks, b.out, int32_t(g.heads), int32_t(g.page_tokens),
+        int64_t(state->capacity / g.page_tokens), int32_t(state->max_context()), scale,
+        state->workspace, state->workspace_bytes, stream);
   if (state->sparse())
     return ifattn_mla_sparse_attention_c8(
         b.query, b.cache, b.indices, kTopK, b.table, int32_t(g.table_entries), nullptr, b.kv_len, 1,

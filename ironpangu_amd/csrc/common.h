@@ -90,6 +90,14 @@ __device__ __forceinline__ void lds_dma16(u32x4 rsrc, uint32_t voff, uint32_t ld
                  : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
                  : "memory");
 }
+// Direct-to-LDS dword load: lane i's 4 bytes at offset voff land at LDS byte
+// lds_base + 4*i (zeros past the buffer end); same rules as lds_dma16.
+__device__ __forceinline__ void lds_dma4(u32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
+               : "memory");
+}
 template <int N>
 __device__ __forceinline__ void lds_dma_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -130,6 +138,16 @@ constexpr float kI8Bias = 1152.0f;
 __device__ __forceinline__ u32x2 i8x4_to_f16_biased(uint32_t w) {
   const uint32_t u = w ^ 0x80808080u;
   return u32x2{perm_b32(0x64646464u, u, 0x05010400u), perm_b32(0x64646464u, u, 0x05030402u)};
+}
+// Eight int4 codes (two's complement nibbles, element 2b in the low nibble of
+// byte b, as if_cache_quantize packs them) -> eight int8 codes (element i in
+// byte i of the pair). A nibble v becomes (v ^ 8) + 120 = code + 128, which
+// stays within a byte (no carries), and the sign flip makes it the int8 code.
+__device__ __forceinline__ u32x2 i4x8_to_i8x8(uint32_t x) {
+  const uint32_t e = x & 0x0F0F0F0Fu, o = (x >> 4) & 0x0F0F0F0Fu;
+  const uint32_t lo = perm_b32(o, e, 0x05010400u), hi = perm_b32(o, e, 0x07030602u);
+  return u32x2{((lo ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u,
+               ((hi ^ 0x08080808u) + 0x78787878u) ^ 0x80808080u};
 }
 __device__ __forceinline__ u32x4 i8x8_to_f16_biased(uint32_t lo, uint32_t hi) {
   const u32x2 a = i8x4_to_f16_biased(lo), b = i8x4_to_f16_biased(hi);

@@ -1,4 +1,5 @@
-// Packed-MLA latent-cache attention for gfx950 (bf16 rows and packed C8 rows).
+// Packed-MLA latent-cache attention for gfx950 (bf16 rows, packed C8 rows and
+// row-quantized int8 / int4 rows).
 //
 // For each query row r and head h (all heads share one cache row per key):
 //   s_j = scale * q[r,h,0:576] . key_j[0:576]
@@ -34,7 +35,13 @@
 // folded into its probabilities for PV. MFMA 16x16x32 bf16 with the heads in
 // the N dimension; C8 latent scores use the fp16 MFMA on the codes biased by
 // 1152 (three VALU ops per four codes instead of a convert per code), with q
-// in fp16 and the bias term removed per head. Rows split over several
+// in fp16 and the bias term removed per head. Row-quantized rows (576 int8 or
+// int4 codes and one fp32 scale per row, as if_cache_quantize writes them,
+// native/kernels/cache_quantization.cpp:12-38) are gathered row by row with
+// their scales staged behind the tile; keys are dequantized in registers to
+// the bf16 values if_cache_dequantize would write (the reference attends over
+// that dequantized cache, token_executor.h:806-822), V stays in codes with the
+// row scale folded into the probabilities. Rows split over several
 // shares, and rows with sinks, write (m, l, O) partials; a merge kernel
 // combines them with the sink partial. How many workgroups share a CU depends
 // on the variant (MlaCfg).
@@ -52,7 +59,8 @@ constexpr int kMaxSinks = 128;
 
 struct MlaParams {
   const uint16_t *q;            // [rows, heads, 576]
-  const uint8_t *cache;         // key rows of 1152 (bf16) or 656 (C8) bytes
+  const uint8_t *cache;         // key rows of 1152 (bf16), 656 (C8), 576 (Rq8) or 288 (Rq4) bytes
+  const float *row_scales;      // [cache rows] fp32 scales of row-quantized rows
   const int32_t *block_tables;  // [seqs, table_stride]
   const int32_t *kv_lens;       // [seqs] cached keys after this step's writes
   const int32_t *cu_q;          // [seqs + 1] query rows per sequence; null: one row each
@@ -70,7 +78,8 @@ struct MlaParams {
   uint16_t *part_o;             // [slots, heads, 512] bf16 O / l of each partial
   float *part_ml;               // [slots, heads, 2]
   int64_t num_blocks;
-  uint32_t cache_bytes;  // sparse gathers: byte extent of the cache (< 4 GiB - 16)
+  uint32_t cache_bytes;  // sparse and row-quantized gathers: byte extent of the cache (< 4 GiB - 16)
+  uint32_t scale_bytes;  // row-quantized rows: byte extent of row_scales
   int num_seqs, num_rows, heads, table_stride, block_size, max_context, topk, window, n_sinks;
   int row_cost;     // work units charged per row start
   int sink_units;   // work units of a row's sink block (0 without sinks)
@@ -263,28 +272,44 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
   for (int v = s_emax + 1 + tid; v < s_workers; v += 1024) p.start_row[v] = p.num_rows;
 }
 
-template <bool C8>
+// Key-row formats of the cache.
+enum MlaFmt : int {
+  kFmtBf16 = 0,  // 1152-B rows: bf16[576]
+  kFmtC8 = 1,    // 656-B rows: int8 latent[512], bf16 rope[64], f32 scale[4] (one per 128 dims)
+  kFmtRq8 = 2,   // 576-B rows: int8[576] with one fp32 scale per row in a separate array
+  kFmtRq4 = 3,   // 288-B rows: int4[576] (two's complement, low nibble first), scale as Rq8
+};
+// Formats whose latent dims are integer codes (scored with the biased fp16 MFMA).
+constexpr bool mla_int(int F) { return F != kFmtBf16; }
+// Row-quantized formats (if_cache_quantize rows): the rope dims are codes too,
+// the scale lives outside the row, and dense tiles are gathered row by row.
+constexpr bool mla_rq(int F) { return F == kFmtRq8 || F == kFmtRq4; }
+
+template <int F>
 struct MlaRow {
-  static constexpr uint32_t BYTES = C8 ? 656 : 1152;
-  static constexpr uint32_t CHUNKS = BYTES / 16;  // 72 or 41
-  // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16) / 1312 (C8) 16-byte chunks.
-  static constexpr int NI = C8 ? 6 : 9;
+  static constexpr uint32_t BYTES = F == kFmtC8 ? 656 : (F == kFmtRq8 ? 576 : (F == kFmtRq4 ? 288 : 1152));
+  static constexpr uint32_t CHUNKS = BYTES / 16;  // 72, 41, 36 or 18
+  // Direct-to-LDS loads per wave per tile: 32 rows = 2304 (bf16), 1312 (C8),
+  // 1152 (Rq8) or 576 (Rq4) 16-byte chunks.
+  static constexpr int NI = F == kFmtC8 ? 6 : (F == kFmtRq8 ? 5 : (F == kFmtRq4 ? 3 : 9));
   static constexpr uint32_t SLOT = 4 * NI * 1024;  // LDS bytes per staged tile
   // LDS byte of 16-byte chunk j of tile row r. bf16 rows (1152 B: odd rows
   // start half a bank period in) XOR the latent chunk index with the row's low
   // 4 bits, which puts the 16 rows of one K read on 16 distinct bank groups;
   // the 8 rope chunks (j >= 64) use the low 3 bits to stay inside the row.
-  // C8 rows (656 B) are not swizzled.
+  // Integer rows are not swizzled.
   static __device__ __forceinline__ uint32_t key(uint32_t r, uint32_t j) {
     return j < 64 ? (r & 15) : (r & 7);
   }
   static __device__ __forceinline__ uint32_t chunk(uint32_t r, uint32_t j) {
-    return C8 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ key(r, j));
+    return F != kFmtBf16 ? r * BYTES + 16 * j : r * BYTES + 16 * (j ^ key(r, j));
   }
 };
-static_assert(MlaRow<false>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
+static_assert(MlaRow<kFmtBf16>::NI * 4 * 64 == 32 * 72, "bf16 tile = 2304 chunks");
 static_assert(18 * 64 == 16 * 72, "bf16 loads 0..17 move exactly tile rows 0..15");
-static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
+static_assert(MlaRow<kFmtC8>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
+static_assert(MlaRow<kFmtRq8>::NI * 4 * 64 >= 32 * 36 && MlaRow<kFmtRq4>::NI * 4 * 64 >= 32 * 18,
+              "row-quantized tiles fit the slot");
 
 // Ring depth and persistent workgroups per CU of each kernel variant. bf16
 // runs one workgroup of four waves per CU with a 4-tile ring (its 36-KB tiles
@@ -294,22 +319,28 @@ static_assert(MlaRow<true>::NI * 4 * 64 >= 32 * 41, "C8 tile fits the slot");
 // 128 rows: C8 decode over log-uniform [1024, 65536] keys 582 us with one
 // workgroup and 6 stages, 456 us with two and 3 stages; sparse top-2048
 // 95.9 us with one workgroup and 6 stages, 75.9 us with two and 2 stages.
-template <bool C8, bool SPARSE, bool WIDE = false>
+template <int F, bool SPARSE, bool WIDE = false>
 struct MlaCfg {
-  // Dense C8 runs three workgroups per CU (three waves per SIMD): 21-KiB ring
-  // slots (the 21 loads a 20992-B tile needs) and one score buffer (two
-  // barriers per tile) fit three in the LDS, and the tile math of one
-  // workgroup hides behind the other two (config-5 shapes 380-386 -> 349-356 us
-  // against two workgroups with double score buffers). Sparse C8 keeps two:
-  // three (with 512-entry slot lists) measured 81 against 72 us on top-2048,
-  // and two with 3-slot rings of 21-KiB slots and one score buffer 74 us.
+  static constexpr bool C8 = mla_int(F);
+  // Dense integer formats run three workgroups per CU (three waves per SIMD):
+  // ring slots of exactly the 1-KiB loads a tile needs (21 for a 20992-B C8
+  // tile) and one score buffer (two barriers per tile) fit three in the LDS,
+  // and the tile math of one workgroup hides behind the other two (config-5
+  // shapes 380-386 -> 349-356 us against two workgroups with double score
+  // buffers). Sparse C8 keeps two: three (with 512-entry slot lists) measured
+  // 81 against 72 us on top-2048, and two with 3-slot rings of 21-KiB slots and
+  // one score buffer 74 us. Row-quantized slots end with the tile's 32 row
+  // scales (256 bytes: the direct-to-LDS scale load writes a dword per lane).
   static constexpr bool TIGHT = C8 && !SPARSE;
   // Large dense bf16 calls (WIDE) run two workgroups per CU, each with a
   // 2-slot ring and one score buffer (exactly 160 KiB): config-5 decode 507-510
   // -> 489-491 us. Small calls keep one workgroup with a 4-slot ring (window
   // 2048 over 128 rows: 79 against 83 us with two).
   static constexpr bool B2 = !C8 && !SPARSE && WIDE;
-  static constexpr int WGS = C8 ? ((TIGHT && !SPARSE) ? 3 : 2) : (B2 ? 2 : 1);
+  // Row-quantized tiles run two workgroups with 3-slot rings: their gather
+  // addressing and the rope codes' extra MFMAs need more than the 168
+  // registers of three workgroups (they spilled there).
+  static constexpr int WGS = mla_rq(F) ? 2 : (C8 ? ((TIGHT && !SPARSE) ? 3 : 2) : (B2 ? 2 : 1));
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
@@ -320,23 +351,32 @@ struct MlaCfg {
 #ifndef IFATTN_MLA_BF16_XB
 #define IFATTN_MLA_BF16_XB 1
 #endif
-  static constexpr int STAGES = C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : IFATTN_MLA_BF16_STAGES));
-  static constexpr int SLOT = TIGHT ? 21 * 1024 : int(MlaRow<C8>::SLOT);
-  static constexpr int LOADS = TIGHT ? 21 : 4 * MlaRow<C8>::NI;  // 1-KiB loads per tile
+  static constexpr int STAGES = mla_rq(F) ? 3 : (C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : IFATTN_MLA_BF16_STAGES)));
+  // 1-KiB loads per tile
+  static constexpr int LOADS = TIGHT ? int((32 * MlaRow<F>::BYTES + 1023) / 1024) : 4 * MlaRow<F>::NI;
+  static constexpr int SCALES = mla_rq(F) ? LOADS * 1024 : 0;  // LDS byte of the row scales
+  static constexpr int SLOT = TIGHT ? LOADS * 1024 + (mla_rq(F) ? 256 : 0) : int(MlaRow<F>::SLOT);
   static constexpr int XB = (TIGHT || B2) ? 1 : (!C8 && !SPARSE ? IFATTN_MLA_BF16_XB : 2);  // score buffers
   static constexpr int RING = SLOT * STAGES;
   // (+ the self-plan arrays: two ints per planned row, except the wide variant)
   static constexpr int LDS = RING + XB * NW * 64 * 32 + (SPARSE ? 4 * kSparsePart : 0) +
                              (B2 ? 0 : 2 * 4 * 64 * kMlaWaves + 64);
   static_assert(LDS * WGS <= 160 * 1024, "LDS per CU");
+  static_assert(!mla_rq(F) || !SPARSE, "row-quantized rows are attended densely");
+  // Waves that issue NI loads per tile (the rest issue NI - 1; with row
+  // scales, the last wave issues the scale load on top of its NI - 1).
+  static constexpr int FULL_WAVES = TIGHT ? LOADS - 4 * (MlaRow<F>::NI - 1) : 4;
+  static_assert(!mla_rq(F) || FULL_WAVES < 4, "the scale load goes to a wave with NI - 1 loads");
 };
 // Persistent workgroups per CU of the kernel variant a call runs (the grid is
 // that many per CU, all resident at once).
-inline int wgs_mla(bool c8, bool sparse, bool wide) {
-  if (!c8) return sparse ? MlaCfg<false, true>::WGS
-                         : (wide ? MlaCfg<false, false, true>::WGS : MlaCfg<false, false>::WGS);
-  return sparse ? MlaCfg<true, true>::WGS : MlaCfg<true, false>::WGS;
+inline int wgs_mla(int fmt, bool sparse, bool wide) {
+  if (mla_rq(fmt)) return MlaCfg<kFmtRq8, false>::WGS;
+  if (fmt != kFmtBf16) return sparse ? MlaCfg<kFmtC8, true>::WGS : MlaCfg<kFmtC8, false>::WGS;
+  return sparse ? MlaCfg<kFmtBf16, true>::WGS
+                : (wide ? MlaCfg<kFmtBf16, false, true>::WGS : MlaCfg<kFmtBf16, false>::WGS);
 }
+static_assert(MlaCfg<kFmtRq8, false>::WGS == MlaCfg<kFmtRq4, false>::WGS, "one grid per format");
 constexpr int kMlaWgsMax = 3;  // most persistent workgroups per CU of any variant
 constexpr int64_t kMlaWideKeys = int64_t(1) << 21;
 // Wave geometry of a workgroup of NW waves: wave w owns the latent dims
@@ -356,6 +396,19 @@ __device__ __forceinline__ int mla_tile_token(int g, int j) {
   return j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
 }
 
+// Eight int8 codes (byte i = element i) times a row scale, as bf16 values
+// bf16(code * scale) rounded to nearest even, packed in element order.
+__device__ __forceinline__ u32x4 i8x8_dequant_bf16(u32x2 x, float scale) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int32_t wd = int32_t(x[i >> 1]);
+    const int sh = 16 * (i & 1);
+    const float a = float((wd << (24 - sh)) >> 24), b = float((wd << (16 - sh)) >> 24);
+    r[i] = pack_bf16x2(a * scale, b * scale);
+  }
+  return r;
+}
 __device__ __forceinline__ uint32_t mla_i8pair(int a, int b) {
   return perm_b32(__float_as_uint(float(b)), __float_as_uint(float(a)), 0x07060302u);
 }
@@ -505,12 +558,14 @@ __device__ __forceinline__ void mla_tile_math(MlaAcc<MlaGeo<NW>::EPL> &acc,
 // in rows) from the same LDS bytes.
 // Tiles [j0, j1) of row `row` (span sp): output, or partial slot `slot` when
 // slot >= 0.
-template <bool C8, bool SPARSE, bool WIDE>
+template <int F, bool SPARSE, bool WIDE>
 __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, float (*xbuf)[8],
                                          uint32_t *slot_list, int row, const MlaSpan &sp, int j0,
                                          int j1, int slot, int w, int lane) {
-  using R = MlaRow<C8>;
-  using Cfg = MlaCfg<C8, SPARSE, WIDE>;
+  constexpr bool C8 = mla_int(F);  // integer latent codes (C8 or row-quantized)
+  constexpr bool RQ = mla_rq(F);
+  using R = MlaRow<F>;
+  using Cfg = MlaCfg<F, SPARSE, WIDE>;
   constexpr int S = Cfg::STAGES;
   constexpr int NW = Cfg::NW;
   using Geo = MlaGeo<NW>;
@@ -585,11 +640,12 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     lane_blocks = b < 0 ? 0 : (b >= p.num_blocks ? int(p.num_blocks - 1) : b);
   };
   if constexpr (!SPARSE) load_window();
-  // C8: the latent QK^T runs in fp16 on the biased codes (code + kI8Bias,
-  // exact); the wave's q slice is scaled per head by a power of two into fp16
-  // range, and kI8Bias * sum(q slice) leaves each partial score.
+  // C8 rows: the latent QK^T runs in fp16 on the biased codes (code +
+  // kI8Bias, exact); the wave's q slice is scaled per head by a power of two
+  // into fp16 range, and kI8Bias * sum(q slice) leaves each partial score.
+  // (Row-quantized keys are dequantized to bf16 instead; see score().)
   float k_corr = 0.0f, q_unscale = 1.0f;
-  if constexpr (C8) {
+  if constexpr (C8 && !RQ) {
     float amax = 0.0f;
 #pragma unroll
     for (int s = 0; s < KS; ++s) amax = fmaxf(amax, bf16x8_absmax(qv[s]));
@@ -632,6 +688,36 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
         const uint32_t slot = r < 32u && t0 + int(r) < t_end ? slot_list[ti * kMlaTile + r] : kNoRow;
         const uint32_t off = slot == kNoRow ? 0xFFFFFFF0u : slot * R::BYTES + lcol[k];
         lds_dma16(rc, off, dst + uint32_t(k) * 4096);
+      }
+    } else if constexpr (RQ) {
+      // Row-quantized rows: every lane gathers its chunk's row through the
+      // block window (any page size; rows outside [t_begin, t_end) land as
+      // zeros), and the last wave loads the tile's 32 row scales behind the rows.
+      const int lower = t_begin > t0 ? t_begin - t0 : 0;
+      const int upper = t_end - t0 < kMlaTile ? t_end - t0 : kMlaTile;
+      if (((t0 + kMlaTile - 1) >> bs_log2) - wblk0 >= 64) {
+        wblk0 = t0 >> bs_log2;
+        load_window();
+      }
+      const u32x4 rc = raw_rsrc(p.cache, p.cache_bytes);
+      auto row_slot = [&](int r) {  // physical row of tile row r (all lanes take part)
+        const int pos = t0 + r;
+        const int blk = __shfl(lane_blocks, ((pos >> bs_log2) - wblk0) & 63, 64);
+        return uint32_t(blk) * uint32_t(bs) + uint32_t(pos & (bs - 1));
+      };
+#pragma unroll
+      for (int k = 0; k < R::NI; ++k) {
+        if (4 * k + w >= Cfg::LOADS) break;
+        const int r = int(lrow[k]);
+        const uint32_t srow = row_slot(r & 31);
+        const uint32_t off = r >= lower && r < upper ? srow * R::BYTES + lcol[k] : 0xFFFFFFF0u;
+        lds_dma16(rc, off, dst + uint32_t(k) * 4096);
+      }
+      if (w == 3) {
+        const uint32_t srow = row_slot(lane & 31);
+        const uint32_t off = lane < 32 && lane >= lower && lane < upper ? srow * 4u : 0xFFFFFFF0u;
+        lds_dma4(raw_rsrc(p.row_scales, p.scale_bytes), off,
+                 ring_base + uint32_t(ti % S) * Cfg::SLOT + uint32_t(Cfg::SCALES));
       }
     } else {
       const int lower = t_begin > t0 ? t_begin - t0 : 0;  // rows before the window start
@@ -693,10 +779,28 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       live = (upper >= 32 ? 0xFFFFFFFFu : ((1u << upper) - 1u)) & ~((1u << lower) - 1u);
     }
     // K operand: token 16mt + c, latent dims DPW w + 32s + 8g (+ rope dims 32(w&1) + 8g).
+    // Row-quantized keys become the bf16 values if_cache_dequantize writes,
+    // bf16(code * scale) (cache_quantization.cpp:39-57): a score depends on
+    // that rounding (a large-scale row moves by up to a percent without it),
+    // so the keys are scored exactly as the reference's dequantized cache.
     u32x4 k[2][KS + 1];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const uint32_t r = uint32_t(16 * mt + c);
+      if constexpr (RQ) {
+        const float rs = *reinterpret_cast<const float *>(tile + Cfg::SCALES + 4 * r);
+        auto codes = [&](uint32_t dim) {  // 8 codes of dims dim .. dim + 7
+          if constexpr (F == kFmtRq4)
+            return i4x8_to_i8x8(*reinterpret_cast<const uint32_t *>(tile + r * R::BYTES + dim / 2));
+          else
+            return *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + dim);
+        };
+#pragma unroll
+        for (int s = 0; s < KS; ++s) k[mt][s] = i8x8_dequant_bf16(codes(uint32_t(DPW * w + 32 * s + 8 * g)), rs);
+        k[mt][KS] = w < 2 ? i8x8_dequant_bf16(codes(uint32_t(512 + 32 * (w & 1) + 8 * g)), rs)
+                          : u32x4{0, 0, 0, 0};
+        continue;
+      }
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         if constexpr (C8) {
@@ -719,7 +823,18 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t r = uint32_t(mla_tile_token(g, j));
-      if constexpr (C8) {
+      if constexpr (RQ) {
+        static_assert(EPL == 8, "row-quantized V operands are 8 dims per lane");
+        if constexpr (F == kFmtRq4) {
+          const u32x2 x = i4x8_to_i8x8(
+              *reinterpret_cast<const uint32_t *>(tile + r * R::BYTES + (DPW * w + 8 * c) / 2));
+          v[j] = u32x4{x[0], x[1], 0u, 0u};
+        } else {
+          const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + DPW * w + 8 * c);
+          v[j] = u32x4{x[0], x[1], 0u, 0u};
+        }
+        sk[j] = *reinterpret_cast<const float *>(tile + Cfg::SCALES + 4 * r);
+      } else if constexpr (C8) {
         if constexpr (EPL == 8) {
           const u32x2 x = *reinterpret_cast<const u32x2 *>(tile + r * R::BYTES + DPW * w + 8 * c);
           v[j] = u32x4{x[0], x[1], 0u, 0u};
@@ -738,7 +853,8 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
       }
     }
 
-    mla_tile_scores<C8, NW>(k, sk, qv, xb, w, lane, k_corr, q_unscale);
+    // Row-quantized keys were dequantized above: bf16 scores, no scale.
+    mla_tile_scores<C8 && !RQ, NW>(k, sk, qv, xb, w, lane, k_corr, q_unscale);
   };
 
   // Ring: tile ti lives in slot ti % S; tiles 0..S-1 are issued up front. In
@@ -751,9 +867,11 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 #pragma unroll
   for (int i = 0; i < S; ++i)
     if (i < n_tiles) issue(i);
+  // Loads per wave per tile: NI, or NI - 1 for the waves past LOADS (the
+  // scale load brings the last wave of a row-quantized tile back to NI).
+  const bool full_loads = !Cfg::TIGHT || w < Cfg::FULL_WAVES || (RQ && w == 3);
   if (S - 1 < n_tiles) {  // tile 0; tiles 1 .. S-1 may stay in flight
-    // Loads per wave per tile: NI, or NI - 1 for the waves past LOADS.
-    if (!Cfg::TIGHT || w < Cfg::LOADS - 4 * (R::NI - 1))
+    if (full_loads)
       lds_dma_wait<(S - 1) * R::NI>();
     else
       lds_dma_wait<(S - 1) * (R::NI - 1)>();
@@ -768,7 +886,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
     uint32_t live;
     score(ring + (ti % S) * Cfg::SLOT, tile0 + ti * kMlaTile, v, sk, live, xb);
     if (ti + S - 1 < n_tiles) {  // tile ti+1; tiles ti+2 .. ti+S-1 may stay in flight
-      if (!Cfg::TIGHT || w < Cfg::LOADS - 4 * (R::NI - 1))
+      if (full_loads)
         lds_dma_wait<(S - 2) * R::NI>();
       else
         lds_dma_wait<(S - 2) * (R::NI - 1)>();
@@ -965,9 +1083,9 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
   __syncthreads();
 }
 
-template <bool C8, bool SPARSE, bool WIDE>
-__global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SPARSE, WIDE>::WGS)) void mla_attention_kernel(MlaParams p) {
-  using Cfg = MlaCfg<C8, SPARSE, WIDE>;
+template <int F, bool SPARSE, bool WIDE>
+__global__ __launch_bounds__(64 * (MlaCfg<F, SPARSE, WIDE>::NW), (MlaCfg<F, SPARSE, WIDE>::WGS)) void mla_attention_kernel(MlaParams p) {
+  using Cfg = MlaCfg<F, SPARSE, WIDE>;
   constexpr int NW = Cfg::NW;
   __shared__ __align__(16) uint8_t ring[Cfg::RING];
   __shared__ __align__(16) float xbuf[Cfg::XB * NW * 64][8];  // score exchange
@@ -1029,7 +1147,7 @@ __global__ __launch_bounds__(64 * (MlaCfg<C8, SPARSE, WIDE>::NW), (MlaCfg<C8, SP
       j1 = j1 < rw.tiles ? j1 : rw.tiles;
       if (j0 >= j1) continue;
       const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
-      mla_item<C8, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
+      mla_item<F, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
       __syncthreads();  // every wave is done with xbuf (and the ring)
     }
   }
@@ -1110,8 +1228,9 @@ __global__ __launch_bounds__(256) void mla_merge_kernel(MlaParams p) {
 namespace {
 
 struct MlaCall {
-  int c8;
+  int fmt;  // MlaFmt
   const void *q, *cache;
+  const float *row_scales;  // row-quantized formats
   const int32_t *block_tables;
   int32_t table_stride;
   const int32_t *cu_q, *kv_lens;
@@ -1187,19 +1306,24 @@ int32_t mla_run(const MlaCall &c, const char *what) {
     return fail(IFATTN_EINVAL, what, "1..16 heads, 1..2^20-1 rows and at least one sequence");
   if (!c.cu_q && c.num_rows != c.num_seqs)
     return fail(IFATTN_EINVAL, what, "without cu_seqlens_q every sequence has one row");
-  if (c.block_size < (c.c8 ? 32 : 16) || (c.block_size & (c.block_size - 1)))
-    return fail(IFATTN_EINVAL, what, "block_size must be a power of two >= 16 (bf16) or >= 32 (C8)");
+  const bool rq = c.fmt == kFmtRq8 || c.fmt == kFmtRq4;
+  if (c.block_size < (c.fmt == kFmtC8 ? 32 : 16) || (c.block_size & (c.block_size - 1)))
+    return fail(IFATTN_EINVAL, what,
+                "block_size must be a power of two >= 16 (bf16, row-quantized) or >= 32 (C8)");
   if (c.max_context <= 0 || c.num_blocks <= 0 || c.table_stride <= 0 ||
       int64_t(c.table_stride) * c.block_size < c.max_context)
     return fail(IFATTN_EINVAL, what, "table_stride * block_size must cover max_context");
   if (!aligned16(c.q) || !aligned16(c.out) || !aligned16(c.cache))
     return fail(IFATTN_EINVAL, what, "q, out and cache must be 16-byte aligned");
-  const uint64_t row_bytes = c.c8 ? 656 : 1152;
+  const uint64_t row_bytes = c.fmt == kFmtC8 ? 656 : (c.fmt == kFmtRq8 ? 576 : (c.fmt == kFmtRq4 ? 288 : 1152));
   if (uint64_t(c.block_size) * row_bytes > (1ull << 31))
     return fail(IFATTN_EINVAL, what, "block too large");
   const uint64_t cache_bytes = uint64_t(c.num_blocks) * c.block_size * row_bytes;
   if (sparse && (c.topk <= 0 || cache_bytes > 0xFFFFFFF0ull))
     return fail(IFATTN_EINVAL, what, "sparse attention needs topk > 0 and a cache below 4 GiB");
+  if (rq && (sparse || !c.row_scales || !aligned4(c.row_scales) || cache_bytes > 0xFFFFFFF0ull))
+    return fail(IFATTN_EINVAL, what,
+                "row-quantized rows: dense attention, 4-byte aligned scales, a cache below 4 GiB");
   if (c.window < 0) return fail(IFATTN_EINVAL, what, "window must be >= 0");
   if (c.n_sinks < 0 || c.n_sinks > kMaxSinks || (c.n_sinks > 0 && (!c.sink_k || !c.sink_v)) ||
       (c.n_sinks > 0 && (!aligned4(c.sink_k) || !aligned4(c.sink_v))))
@@ -1207,8 +1331,8 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   // Two-workgroup bf16 layout for large dense calls: at least kMlaWideKeys
   // keys possible over all rows.
   const int64_t span = (c.window > 0 && c.window < c.max_context) ? int64_t(c.window) + 31 : c.max_context;
-  const bool wide = !c.c8 && !sparse && int64_t(c.num_rows) * span >= kMlaWideKeys;
-  const int wgs = wgs_mla(c.c8, sparse, wide);
+  const bool wide = c.fmt == kFmtBf16 && !sparse && int64_t(c.num_rows) * span >= kMlaWideKeys;
+  const int wgs = wgs_mla(c.fmt, sparse, wide);
   const uint64_t need = mla_workspace(c.num_rows, c.heads, sparse, c.topk, c.n_sinks);
   if (!c.workspace || c.workspace_bytes < need || !aligned16(c.workspace))
     return fail(IFATTN_EWORKSPACE, what, "workspace missing, short or misaligned");
@@ -1225,7 +1349,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.sink_v = static_cast<const uint16_t *>(c.sink_v);
   p.out = static_cast<uint16_t *>(c.out);
   p.num_blocks = c.num_blocks;
-  p.cache_bytes = sparse ? uint32_t(cache_bytes) : 0u;
+  p.cache_bytes = (sparse || rq) ? uint32_t(cache_bytes) : 0u;
+  p.row_scales = rq ? c.row_scales : nullptr;
+  p.scale_bytes = rq ? uint32_t(uint64_t(c.num_blocks) * c.block_size * 4) : 0u;
   p.num_seqs = c.num_seqs;
   p.num_rows = c.num_rows;
   p.heads = c.heads;
@@ -1240,7 +1366,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.row_cost = mla_row_cost();
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
-  p.skew_pm = mla_skew_pm(c.c8 != 0, sparse);
+  p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse);
   p.max_workers = int(max_workers);
   p.grid = grid;
   // Self-planned calls: few rows, a variant with the LDS for the plan, and
@@ -1265,24 +1391,29 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.part_ml = reinterpret_cast<float *>(p.part_o + slots * c.heads * 512);
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   if (!p.self_plan) mla_plan_kernel<<<1, 1024, 0, s>>>(p);
-  if (c.c8) {
-    if (sparse) mla_attention_kernel<true, true, false><<<grid, 64 * MlaCfg<true, true>::NW, 0, s>>>(p);
-    else mla_attention_kernel<true, false, false><<<grid, 64 * MlaCfg<true, false>::NW, 0, s>>>(p);
+  constexpr int kThreads = 64 * kMlaWaves;
+  if (c.fmt == kFmtC8) {
+    if (sparse) mla_attention_kernel<kFmtC8, true, false><<<grid, kThreads, 0, s>>>(p);
+    else mla_attention_kernel<kFmtC8, false, false><<<grid, kThreads, 0, s>>>(p);
+  } else if (c.fmt == kFmtRq8) {
+    mla_attention_kernel<kFmtRq8, false, false><<<grid, kThreads, 0, s>>>(p);
+  } else if (c.fmt == kFmtRq4) {
+    mla_attention_kernel<kFmtRq4, false, false><<<grid, kThreads, 0, s>>>(p);
   } else {
-    if (sparse) mla_attention_kernel<false, true, false><<<grid, 64 * MlaCfg<false, true>::NW, 0, s>>>(p);
-    else if (wide) mla_attention_kernel<false, false, true><<<grid, 64 * MlaCfg<false, false, true>::NW, 0, s>>>(p);
-    else mla_attention_kernel<false, false, false><<<grid, 64 * MlaCfg<false, false>::NW, 0, s>>>(p);
+    if (sparse) mla_attention_kernel<kFmtBf16, true, false><<<grid, kThreads, 0, s>>>(p);
+    else if (wide) mla_attention_kernel<kFmtBf16, false, true><<<grid, kThreads, 0, s>>>(p);
+    else mla_attention_kernel<kFmtBf16, false, false><<<grid, kThreads, 0, s>>>(p);
   }
   mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
   return launch_status(what);
 }
 
-MlaCall decode_call(bool c8, const void *q, const void *cache, const int32_t *block_tables,
+MlaCall decode_call(int fmt, const void *q, const void *cache, const int32_t *block_tables,
                     int32_t table_stride, const int32_t *seq_lens, void *out, int32_t num_seqs,
                     int32_t heads, int32_t block_size, int64_t num_blocks, int32_t max_context,
                     float scale, void *workspace, uint64_t workspace_bytes, void *stream) {
   MlaCall c{};
-  c.c8 = c8;
+  c.fmt = fmt;
   c.q = q;
   c.cache = cache;
   c.block_tables = block_tables;
@@ -1320,7 +1451,7 @@ extern "C" int32_t ifattn_mla_decode_bf16(const void *q, const void *cache,
                                           int32_t heads, int32_t block_size, int64_t num_blocks,
                                           int32_t max_context, float scale, void *workspace,
                                           uint64_t workspace_bytes, void *stream) {
-  return mla_run(decode_call(false, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
+  return mla_run(decode_call(kFmtBf16, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
                              heads, block_size, num_blocks, max_context, scale, workspace,
                              workspace_bytes, stream),
                  "mla decode");
@@ -1332,7 +1463,7 @@ extern "C" int32_t ifattn_mla_decode_c8(const void *q, const void *cache,
                                         int32_t heads, int32_t block_size, int64_t num_blocks,
                                         int32_t max_context, float scale, void *workspace,
                                         uint64_t workspace_bytes, void *stream) {
-  return mla_run(decode_call(true, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
+  return mla_run(decode_call(kFmtC8, q, cache, block_tables, table_stride, seq_lens, out, num_seqs,
                              heads, block_size, num_blocks, max_context, scale, workspace,
                              workspace_bytes, stream),
                  "mla decode c8");
@@ -1355,7 +1486,7 @@ extern "C" int32_t ifattn_mla_window_attention_bf16(
     int32_t window, const void *sink_keys, const void *sink_values, int32_t n_sinks, void *out,
     int32_t heads, int32_t block_size, int64_t num_blocks, int32_t max_context, float scale,
     void *workspace, uint64_t workspace_bytes, void *stream) {
-  MlaCall c = decode_call(false, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
+  MlaCall c = decode_call(kFmtBf16, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
                           heads, block_size, num_blocks, max_context, scale, workspace,
                           workspace_bytes, stream);
   c.cu_q = cu_seqlens_q;
@@ -1375,7 +1506,7 @@ extern "C" int32_t ifattn_mla_sparse_attention_c8(
     int64_t num_blocks, int32_t max_context, float scale, void *workspace,
     uint64_t workspace_bytes, void *stream) {
   if (!indices) return fail(IFATTN_EINVAL, "mla sparse attention: null indices");
-  MlaCall c = decode_call(true, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
+  MlaCall c = decode_call(kFmtC8, q, cache, block_tables, table_stride, kv_lens, out, num_seqs,
                           heads, block_size, num_blocks, max_context, scale, workspace,
                           workspace_bytes, stream);
   c.cu_q = cu_seqlens_q;
@@ -1386,4 +1517,25 @@ extern "C" int32_t ifattn_mla_sparse_attention_c8(
   c.sink_v = sink_values;
   c.n_sinks = n_sinks;
   return mla_run(c, "mla sparse attention");
+}
+
+extern "C" int32_t ifattn_mla_window_attention_rowq(
+    const void *q, const void *cache, const float *row_scales, int32_t bits,
+    const int32_t *block_tables, int32_t table_stride, const int32_t *cu_seqlens_q,
+    const int32_t *kv_lens, int32_t num_seqs, int32_t num_rows, int32_t window,
+    const void *sink_keys, const void *sink_values, int32_t n_sinks, void *out, int32_t heads,
+    int32_t block_size, int64_t num_blocks, int32_t max_context, float scale, void *workspace,
+    uint64_t workspace_bytes, void *stream) {
+  if (bits != 8 && bits != 4) return fail(IFATTN_EINVAL, "mla row-quantized attention: bits 8 or 4");
+  MlaCall c = decode_call(bits == 8 ? kFmtRq8 : kFmtRq4, q, cache, block_tables, table_stride,
+                          kv_lens, out, num_seqs, heads, block_size, num_blocks, max_context,
+                          scale, workspace, workspace_bytes, stream);
+  c.row_scales = row_scales;
+  c.cu_q = cu_seqlens_q;
+  c.num_rows = num_rows;
+  c.window = window;
+  c.sink_k = sink_keys;
+  c.sink_v = sink_values;
+  c.n_sinks = n_sinks;
+  return mla_run(c, "mla row-quantized attention");
 }

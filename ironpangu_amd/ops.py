@@ -349,23 +349,34 @@ def mla_decode(q, cache, block_tables, seq_lens, max_context, scale=None, out=No
 
 def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None, indices=None,
                   window=0, sink_keys=None, sink_values=None, scale=None, out=None,
-                  workspace=None, stream=None):
+                  workspace=None, stream=None, row_scales=None, bits=8):
     """Packed-MLA attention over query rows.
 
     q [rows, heads, 576] bf16; rows per sequence from cu_seqlens int32 [seqs+1]
     (None: one row per sequence); kv_lens int32 [seqs]. bf16 caches
     [blocks, bs, 576] take the window path (``window`` 0 = all keys); packed C8
     caches uint8 [blocks, bs, 656] take the sparse path with ``indices`` int32
-    [rows, topk]. sink_keys [n, 576] / sink_values [n, 512] bf16 (n <= 128) are
+    [rows, topk]; row-quantized caches uint8 [blocks, bs, 576 * bits / 8] with
+    ``row_scales`` fp32 [blocks * bs] take the window path, dequantized in
+    registers. sink_keys [n, 576] / sink_values [n, 512] bf16 (n <= 128) are
     optional. Returns out [rows, heads, 512] bf16.
     """
-    c8 = cache.dtype == torch.uint8
-    _dev(q, cache, block_tables, kv_lens, cu_seqlens, indices, sink_keys, sink_values, out, workspace)
+    rowq = row_scales is not None
+    c8 = cache.dtype == torch.uint8 and not rowq
+    _dev(q, cache, block_tables, kv_lens, cu_seqlens, indices, sink_keys, sink_values, out, workspace,
+         row_scales)
     _req(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == 576, "q: bf16 [rows, heads, 576]")
     rows, h, _ = q.shape
-    _req(cache.dim() == 3 and cache.shape[2] == (656 if c8 else 576)
-         and cache.dtype in (torch.uint8, torch.bfloat16), "cache: bf16 [.., 576] or uint8 [.., 656]")
-    _req(c8 == (indices is not None), "C8 caches take index lists, bf16 caches take windows")
+    if rowq:
+        _req(bits in (8, 4) and cache.dtype == torch.uint8 and cache.dim() == 3
+             and cache.shape[2] == 576 * bits // 8, "row-quantized cache: uint8 [.., 576 * bits / 8]")
+        _req(row_scales.dtype == torch.float32 and row_scales.numel() == cache.shape[0] * cache.shape[1],
+             "row_scales: fp32 [blocks * block_size]")
+        _req(indices is None, "row-quantized caches take windows")
+    else:
+        _req(cache.dim() == 3 and cache.shape[2] == (656 if c8 else 576)
+             and cache.dtype in (torch.uint8, torch.bfloat16), "cache: bf16 [.., 576] or uint8 [.., 656]")
+        _req(c8 == (indices is not None), "C8 caches take index lists, bf16 caches take windows")
     nb, bs, _ = cache.shape
     seqs = rows if cu_seqlens is None else cu_seqlens.numel() - 1
     _req(cu_seqlens is None or (cu_seqlens.dtype == torch.int32 and seqs >= 1),
@@ -390,7 +401,13 @@ def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None,
     if workspace is None:
         n = lib().ifattn_mla_attention_workspace_size(rows, h, max_context, int(window), topk, ns, bs)
         workspace = torch.empty(max(int(n), 16), dtype=torch.uint8, device=q.device)
-    if c8:
+    if rowq:
+        st = lib().ifattn_mla_window_attention_rowq(
+            _ptr(q), _ptr(cache), _ptr(row_scales), int(bits), _ptr(block_tables),
+            block_tables.shape[1], _ptr(cu_seqlens), _ptr(kv_lens), seqs, rows, int(window),
+            _ptr(sink_keys), _ptr(sink_values), ns, _ptr(out), h, bs, nb, max_context, float(scale),
+            _ptr(workspace), workspace.numel(), _stream(stream))
+    elif c8:
         st = lib().ifattn_mla_sparse_attention_c8(
             _ptr(q), _ptr(cache), _ptr(indices), topk, _ptr(block_tables), block_tables.shape[1],
             _ptr(cu_seqlens), _ptr(kv_lens), seqs, rows, _ptr(sink_keys), _ptr(sink_values), ns,

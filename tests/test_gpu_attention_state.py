@@ -87,10 +87,3 @@ def test_state_attend_matches_direct_and_oracle(packed):
                                page, 1.0 / np.sqrt(192.0), c8=packed, indices=idx, window=window,
                                sink_k=sk, sink_v=sv)
     assert_close(bf16_host(out), exp)
-
-
-def test_state_rejects_row_quant_attend():
-    from ironpangu_amd.host import AttentionState, MetadataError
-    s = AttentionState(8, 512, False, 1, False, 0, 6)
-    with pytest.raises(MetadataError):
-        s.attend()
