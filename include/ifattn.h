@@ -265,6 +265,15 @@ int32_t ifattn_page_reset(void *field, uint64_t field_bytes, const uint64_t *spa
  * ranges outside the field are skipped. */
 int32_t ifattn_state_copy(void *field, uint64_t field_bytes, const uint64_t *ranges,
                           uint64_t count, void *stream);
+/* Checked forms: the whole plan is validated on the device first, with the
+ * reference's rule for every span (native/src/prepared_execution.h:346-354: not
+ * empty, inside the field, and for copies source and destination apart). An
+ * invalid plan moves no byte. *status (device int32) receives 0, or 1 + the
+ * index of the first invalid span; read it after the stream completes. */
+int32_t ifattn_page_reset_checked(void *field, uint64_t field_bytes, const uint64_t *spans,
+                                  uint64_t count, int32_t *status, void *stream);
+int32_t ifattn_state_copy_checked(void *field, uint64_t field_bytes, const uint64_t *ranges,
+                                  uint64_t count, int32_t *status, void *stream);
 
 /* ---- packed-MLA attention over query rows (windows, sparse lists, sinks) ----- */
 

@@ -76,6 +76,8 @@ SIGNATURES = {
                                              i32, vp, i32, i32, i64, i32, f32, vp, u64, vp]),
     "ifattn_page_reset": (i32, [vp, u64, vp, u64, vp]),
     "ifattn_state_copy": (i32, [vp, u64, vp, u64, vp]),
+    "ifattn_page_reset_checked": (i32, [vp, u64, vp, u64, vp, vp]),
+    "ifattn_state_copy_checked": (i32, [vp, u64, vp, u64, vp, vp]),
     "if_cache_quantize": (None, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "if_cache_dequantize": (None, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "if_packed_attention_metadata": (None, [vp, vp, vp, u32, vp]),

@@ -9,7 +9,11 @@
 // (nontemporal loads and stores: the bytes are not read again soon; the
 // loads measured copy 381 -> 368 us per GiB). Spans whose offset, size or base
 // are not 16-byte aligned fall back to a byte loop; spans outside the field
-// and copy ranges whose source and destination overlap are skipped. The span
+// and copy ranges whose source and destination overlap are skipped. The
+// checked entry points validate the whole plan first, in a one-workgroup
+// kernel, as the reference validates every copy before issuing it
+// (native/src/prepared_execution.h:346-354): an invalid plan moves no byte and
+// leaves the 1-based index of its first bad span in a device status word. The span
 // sizes live on the device, so the second grid dimension is sized from the
 // field's average share per span: a plan mixing one small span into a large
 // field launches idle workgroups for it, which exit at once.
@@ -22,11 +26,43 @@ namespace ifattn {
 // spans: {offset, bytes} pairs (reset) or {source, destination, bytes} triples
 // (copy). Workgroup (i, j) takes span i and every gridDim.y-th 4 KiB piece of
 // it starting at piece j (eight pieces per pass).
+// A span the reference rejects: empty, outside the field, or (copies) with
+// overlapping source and destination.
+template <bool COPY>
+__device__ __forceinline__ bool span_bad(uint64_t src, uint64_t dst, uint64_t bytes,
+                                         uint64_t field_bytes) {
+  return bytes == 0 || src > field_bytes || bytes > field_bytes - src || dst > field_bytes ||
+         bytes > field_bytes - dst || (COPY && src < dst + bytes && dst < src + bytes);
+}
+
+// Plan check of the checked entry points: *status = 1 + index of the first
+// bad span, or 0.
+template <bool COPY>
+__global__ __launch_bounds__(1024) void state_plan_check_kernel(uint64_t field_bytes,
+                                                                const uint64_t *__restrict__ spans,
+                                                                uint64_t count, int32_t *status) {
+  constexpr int W = COPY ? 3 : 2;
+  __shared__ unsigned long long first;
+  if (threadIdx.x == 0) first = ~0ull;
+  __syncthreads();
+  for (uint64_t i = threadIdx.x; i < count; i += blockDim.x) {
+    const uint64_t src = spans[W * i], dst = COPY ? spans[W * i + 1] : src;
+    if (span_bad<COPY>(src, dst, spans[W * i + W - 1], field_bytes)) {
+      atomicMin(&first, (unsigned long long)i);
+      break;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *status = first == ~0ull ? 0 : int32_t(first + 1);
+}
+
 template <bool COPY>
 __global__ __launch_bounds__(256) void state_span_kernel(uint8_t *__restrict__ field,
                                                          uint64_t field_bytes,
-                                                         const uint64_t *__restrict__ spans) {
+                                                         const uint64_t *__restrict__ spans,
+                                                         const int32_t *__restrict__ status) {
   constexpr int W = COPY ? 3 : 2;
+  if (status && *status != 0) return;  // checked call with an invalid plan: nothing moves
   const uint64_t i = blockIdx.x;
   const uint64_t src = spans[W * i];
   const uint64_t dst = COPY ? spans[W * i + 1] : src;
@@ -65,13 +101,17 @@ __global__ __launch_bounds__(256) void state_span_kernel(uint8_t *__restrict__ f
 
 namespace {
 int32_t run_spans(bool copy, void *field, uint64_t field_bytes, const uint64_t *spans,
-                  uint64_t count, void *stream, const char *what) {
+                  uint64_t count, int32_t *status, void *stream, const char *what) {
   if (!field || (!spans && count) || field_bytes == 0)
     return fail(IFATTN_EINVAL, what, "null field or plan");
-  if (!aligned8(spans)) return fail(IFATTN_EINVAL, what, "plan must be 8-byte aligned");
-  if (count == 0) return IFATTN_OK;
+  if (!aligned8(spans) || !aligned4(status)) return fail(IFATTN_EINVAL, what, "misaligned plan or status");
   if (count >= (1ull << 31)) return fail(IFATTN_EINVAL, what, "more than 2^31-1 spans");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (status) {
+    if (copy) state_plan_check_kernel<true><<<1, 1024, 0, s>>>(field_bytes, spans, count, status);
+    else state_plan_check_kernel<false><<<1, 1024, 0, s>>>(field_bytes, spans, count, status);
+  }
+  if (count == 0) return status ? launch_status(what) : IFATTN_OK;
   // Span sizes live on the device: size the second grid dimension for the
   // average span (one workgroup per 64 KiB of it, up to 1024). Fewer, fuller
   // workgroups measured faster than one per 4 KiB (1 GiB of 20992-B pages:
@@ -80,9 +120,9 @@ int32_t run_spans(bool copy, void *field, uint64_t field_bytes, const uint64_t *
   const unsigned split = unsigned(avg / 65536 + 1 < 1024 ? avg / 65536 + 1 : 1024);
   const dim3 grid(unsigned(count), split);
   if (copy)
-    state_span_kernel<true><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans);
+    state_span_kernel<true><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans, status);
   else
-    state_span_kernel<false><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans);
+    state_span_kernel<false><<<grid, 256, 0, s>>>(static_cast<uint8_t *>(field), field_bytes, spans, status);
   return launch_status(what);
 }
 }  // namespace
@@ -92,10 +132,23 @@ using namespace ifattn;
 
 extern "C" int32_t ifattn_page_reset(void *field, uint64_t field_bytes, const uint64_t *spans,
                                      uint64_t count, void *stream) {
-  return run_spans(false, field, field_bytes, spans, count, stream, "page reset");
+  return run_spans(false, field, field_bytes, spans, count, nullptr, stream, "page reset");
 }
 
 extern "C" int32_t ifattn_state_copy(void *field, uint64_t field_bytes, const uint64_t *ranges,
                                      uint64_t count, void *stream) {
-  return run_spans(true, field, field_bytes, ranges, count, stream, "state copy");
+  return run_spans(true, field, field_bytes, ranges, count, nullptr, stream, "state copy");
+}
+
+extern "C" int32_t ifattn_page_reset_checked(void *field, uint64_t field_bytes, const uint64_t *spans,
+                                             uint64_t count, int32_t *status, void *stream) {
+  if (!status) return fail(IFATTN_EINVAL, "page reset: null status");
+  return run_spans(false, field, field_bytes, spans, count, status, stream, "page reset");
+}
+
+extern "C" int32_t ifattn_state_copy_checked(void *field, uint64_t field_bytes,
+                                             const uint64_t *ranges, uint64_t count,
+                                             int32_t *status, void *stream) {
+  if (!status) return fail(IFATTN_EINVAL, "state copy: null status");
+  return run_spans(true, field, field_bytes, ranges, count, status, stream, "state copy");
 }

@@ -425,24 +425,40 @@ def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None,
 
 # ---------------------------------------------------------------- slot reuse
 
-def page_reset(field, spans, stream=None):
+def page_reset(field, spans, stream=None, status=None):
     """Zero the {offset, bytes} spans (uint64 [count, 2] on the device, e.g. from
-    host.page_spans) of a device state tensor, viewed as bytes."""
-    _dev(field, spans)
+    host.page_spans) of a device state tensor, viewed as bytes. With ``status``
+    (int32 [1] on the device) the plan is validated first and an invalid plan
+    zeroes nothing (status = 1 + first bad span)."""
+    _dev(field, spans, status)
     _req(spans.dtype in (torch.int64, torch.uint64) and spans.dim() == 2 and spans.shape[1] == 2,
          "spans: uint64/int64 [count, 2]")
-    check(lib().ifattn_page_reset(_ptr(field), field.numel() * field.element_size(), _ptr(spans),
-                                  spans.shape[0], _stream(stream)), "ifattn_page_reset")
+    nbytes = field.numel() * field.element_size()
+    if status is None:
+        st = lib().ifattn_page_reset(_ptr(field), nbytes, _ptr(spans), spans.shape[0], _stream(stream))
+    else:
+        _req(status.dtype == torch.int32 and status.numel() == 1, "status: int32 [1]")
+        st = lib().ifattn_page_reset_checked(_ptr(field), nbytes, _ptr(spans), spans.shape[0],
+                                             _ptr(status), _stream(stream))
+    check(st, "ifattn_page_reset")
 
 
-def state_copy(field, ranges, stream=None):
+def state_copy(field, ranges, stream=None, status=None):
     """Copy the {source, destination, bytes} ranges (uint64 [count, 3] on the
-    device, e.g. from ResidentPages.copy_plan) inside one device state tensor."""
-    _dev(field, ranges)
+    device, e.g. from ResidentPages.copy_plan) inside one device state tensor.
+    With ``status`` (int32 [1] on the device) the plan is validated first and an
+    invalid plan copies nothing (status = 1 + first bad range)."""
+    _dev(field, ranges, status)
     _req(ranges.dtype in (torch.int64, torch.uint64) and ranges.dim() == 2 and ranges.shape[1] == 3,
          "ranges: uint64/int64 [count, 3]")
-    check(lib().ifattn_state_copy(_ptr(field), field.numel() * field.element_size(), _ptr(ranges),
-                                  ranges.shape[0], _stream(stream)), "ifattn_state_copy")
+    nbytes = field.numel() * field.element_size()
+    if status is None:
+        st = lib().ifattn_state_copy(_ptr(field), nbytes, _ptr(ranges), ranges.shape[0], _stream(stream))
+    else:
+        _req(status.dtype == torch.int32 and status.numel() == 1, "status: int32 [1]")
+        st = lib().ifattn_state_copy_checked(_ptr(field), nbytes, _ptr(ranges), ranges.shape[0],
+                                             _ptr(status), _stream(stream))
+    check(st, "ifattn_state_copy")
 
 
 # ---------------------------------------------------------------- legacy launchers

@@ -104,3 +104,49 @@ def test_overlapping_copy_range_is_skipped():
     ops.state_copy(t, dev(plan.view(np.int64)))
     torch.cuda.synchronize()
     assert np.array_equal(t.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("bad", ["overlap", "outside", "empty", "none"])
+def test_checked_copy_is_all_or_nothing(bad):
+    """The checked entry point validates the whole plan with the reference's rule
+    (prepared_execution.h:346-354): one bad range and no byte moves, the status
+    names it (1-based); a valid plan copies as the unchecked call."""
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(4)
+    field = rng.integers(0, 256, 1 << 16, dtype=np.uint8)
+    plan = [[0, 16384, 4096], [32768, 49152, 4096], [4096, 20480, 4096]]
+    third = {"overlap": [8192, 9216, 4096], "outside": [60000, 4096, 8192],
+             "empty": [0, 4096, 0], "none": [12288, 28672, 4096]}[bad]
+    plan.insert(2, third)
+    t = dev(field)
+    status = torch.full((1,), -7, dtype=torch.int32, device="cuda")
+    ops.state_copy(t, dev(np.array(plan, np.int64)), status=status)
+    torch.cuda.synchronize()
+    got = t.cpu().numpy()
+    if bad == "none":
+        exp = field.copy()
+        for s, d, n in plan:
+            exp[d:d + n] = field[s:s + n]
+        assert status.item() == 0
+        assert np.array_equal(got, exp)
+    else:
+        assert status.item() == 3
+        assert np.array_equal(got, field)
+
+
+def test_checked_reset_is_all_or_nothing():
+    import torch
+    from ironpangu_amd import ops
+    field = np.full(1 << 14, 9, np.uint8)
+    t = dev(field)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.page_reset(t, dev(np.array([[0, 4096], [16000, 4096]], np.int64)), status=status)
+    torch.cuda.synchronize()
+    assert status.item() == 2 and np.array_equal(t.cpu().numpy(), field)
+    ops.page_reset(t, dev(np.array([[0, 4096], [8192, 4096]], np.int64)), status=status)
+    torch.cuda.synchronize()
+    exp = field.copy()
+    exp[0:4096] = 0
+    exp[8192:12288] = 0
+    assert status.item() == 0 and np.array_equal(t.cpu().numpy(), exp)

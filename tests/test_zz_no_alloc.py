@@ -67,3 +67,45 @@ def test_noalloc_step_rejects_calls_beyond_the_scratch():
     st = l.ifattn_paged_decode_step_bf16_noalloc(a, a, a, a, a, a, 5, 64, a, 32, a, a, 64,
                                                  128, 8, 256, 128, 1 << 20, 4096, 0.1, None)
     assert st == -1 and b"32 MiB" in l.ifattn_last_error()
+
+
+def test_noalloc_step_under_graph_capture():
+    """The entry point recorded into a HIP graph (after one eager warm-up call,
+    which also looks up the scratch address) and replayed three times, with
+    eager work and synchronisation between replays: every replay equals the
+    workspace entry point's eager result bit for bit."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd._native import check, lib
+    case = W.decode_host_case(9, num_seqs=32, lo=1, hi=9000, dist="loguniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=128,
+                              pool_blocks=32 * ((9000 + 127) // 128) + 4)
+    h = case.host
+    shape = (case.pool_blocks, 128, 2, 128)
+    k_ref, v_ref = to_dev(h["k_pool"]).view(shape), to_dev(h["v_pool"]).view(shape)
+    k_g, v_g = k_ref.clone(), v_ref.clone()
+    o_ref = torch.empty((32, 16, 128), dtype=torch.bfloat16, device="cuda")
+    _step(False, case, h, k_ref, v_ref, o_ref)
+    q, kn, vn = to_dev(h["q"]), to_dev(h["k_new"]), to_dev(h["v_new"])
+    slots = to_dev(case.slot_mapping.astype(np.int64))
+    tables, lens = to_dev(case.block_tables), to_dev(case.seq_lens)
+    out = torch.empty_like(o_ref)
+    args = [q.data_ptr(), kn.data_ptr(), vn.data_ptr(), k_g.data_ptr(), v_g.data_ptr(),
+            slots.data_ptr(), 5, 32, tables.data_ptr(), tables.shape[1], lens.data_ptr(),
+            out.data_ptr(), 32, 16, 2, 128, 128, case.pool_blocks, case.max_context, case.scale]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        check(lib().ifattn_paged_decode_step_bf16_noalloc(*args, s.cuda_stream), "warm-up")
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            check(lib().ifattn_paged_decode_step_bf16_noalloc(*args, s.cuda_stream), "capture")
+    for rep in range(3):
+        out.fill_(0)                      # eager work between replays
+        scratch_user = torch.empty_like(o_ref)
+        _step(True, case, h, k_g.clone(), v_g.clone(), scratch_user)  # eager call reuses the scratch
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, o_ref), f"replay {rep}: outputs differ"
+        assert torch.equal(k_g, k_ref) and torch.equal(v_g, v_ref), f"replay {rep}: caches differ"
