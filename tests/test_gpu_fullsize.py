@@ -198,8 +198,9 @@ def test_config5_mla_decode_full_size(c8):
 def test_config3_mixed_prefill_decode_full_size():
     """Config 3: 8 prefill chunks U[64, 2048] after U[0, 8192] cached tokens plus
     192 decode rows U[256, 16384], one packed varlen call after the slot write of
-    every new row. Every decode row is checked, and per chunk its first and last
-    rows and every 31st row; a sampled chunk row t sees kv_len - count + t + 1
+    every new row. Every decode row is checked, every row of the two longest
+    chunks, and of the other chunks the first and last rows and every 31st row;
+    a chunk row t sees kv_len - count + t + 1
     keys (native/src/openpangu_attention_metadata.h:20-22), so the oracle checks
     it as a one-row query over that prefix."""
     import torch
@@ -229,9 +230,12 @@ def test_config3_mixed_prefill_decode_full_size():
     oracle.kv_write(bits_host(kn), k_ref, case.slot_mapping)
     oracle.kv_write(bits_host(vn), v_ref, case.slot_mapping)
     rows, seqs, vis = [], [], []
+    # every row of the two longest chunks (all eight waves of each of their
+    # query tiles), sampled rows of the others
+    longest = set(np.argsort(-np.asarray(case.q_lens))[:2].tolist())
     for s in range(len(case.q_lens)):
         start, count, kv = int(case.cu_seqlens[s]), int(case.q_lens[s]), int(case.kv_lens[s])
-        ts = {0, count - 1} | set(range(0, count, 31))
+        ts = set(range(count)) if s in longest else {0, count - 1} | set(range(0, count, 31))
         for t in sorted(ts):
             rows.append(start + t)
             seqs.append(s)
@@ -242,4 +246,4 @@ def test_config3_mixed_prefill_decode_full_size():
                               threads=THREADS)
     assert_rel_l2(bf16_host(out)[rows], exp, what="config-3 sampled rows")
     assert_close(bf16_host(out)[rows], exp, what="config-3 sampled rows")
-    assert len(rows) > 192 + 8 * 3
+    assert len(rows) > 192 + 8 * 3 + sum(sorted(case.q_lens)[-2:])
