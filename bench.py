@@ -401,6 +401,74 @@ def bench_mla(seed, steps, warmup):
     return res
 
 
+def mla_step_pair(case, seed, steps, warmup, graph=False):
+    """ms of (fused, separate) decode steps over an MlaCase: each sequence's new
+    latent row normalized, roped and written at its last position, then the
+    decode. Fused: one ifattn_mla_decode_step; separate: the writer launch, then
+    the decode launch."""
+    import torch
+    from ironpangu_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 5)
+    n = case.num_seqs
+    cache = torch.empty((case.pool_blocks, case.block_size, 576), dtype=torch.bfloat16, device=dev)
+    fill_randn(cache, g, std=0.5)
+    q = (torch.randn((n, case.heads, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    x = torch.randn((n, 576), generator=g, device=dev).to(torch.bfloat16)
+    gamma = (torch.rand((512,), generator=g, device=dev) + 0.5).to(torch.bfloat16)
+    ang = torch.rand((n, 32), generator=g, device=dev) * 6.28
+    cos = torch.cat([ang.cos(), ang.cos()], 1).to(torch.bfloat16)
+    sin = torch.cat([ang.sin(), ang.sin()], 1).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    last = case.seq_lens.astype(np.int64) - 1
+    slots = torch.from_numpy(case.block_tables[np.arange(n), last // case.block_size].astype(np.int64)
+                             * case.block_size + last % case.block_size).to(dev)
+    ws = ops.mla_workspace(n, case.heads, case.max_context, case.block_size)
+    out = torch.empty((n, case.heads, 512), dtype=torch.bfloat16, device=dev)
+
+    def fused():
+        ops.mla_decode_step(q, x, gamma, cos, sin, cache, tables, lens, case.max_context,
+                            scale=case.scale, out=out, workspace=ws)
+
+    def separate():
+        ops.mla_norm_rope_cache_write(x, gamma, cos, sin, cache, slots)
+        ops.mla_decode(q, cache, tables, lens, case.max_context, case.scale, out=out, workspace=ws)
+
+    ms = (timed(fused, steps, warmup, graph=graph), timed(separate, steps, warmup, graph=graph))
+    del cache
+    torch.cuda.empty_cache()
+    return ms
+
+
+def bench_mla_step(seed, steps, warmup):
+    """Config 5 as a whole decode step (fused writer + decode in one launch,
+    against the two launches), and the same comparison on a small batch
+    replayed from a HIP graph, where the saved launch shows."""
+    from ironpangu_amd import workloads as W
+    case = W.mla_meta(seed)
+    ms_fused, ms_sep = mla_step_pair(case, seed, steps, warmup)
+    small = W.mla_meta(seed, num_seqs=16, lo=256, hi=4096)
+    sm_fused, sm_sep = mla_step_pair(small, seed, max(steps, 50), warmup, graph=True)
+    n = case.num_seqs
+    L = case.seq_lens.astype(np.int64)
+    nbytes = int(L.sum()) * 1152 + n * case.heads * (576 + 512) * 2 + int(((L + 63) // 64).sum()) * 4 + \
+        n * 4 + n * (1152 + 256 + 1152) + 1024
+    res = {"workload": "fused MLA decode step: cache writer (RMSNorm + RoPE) + latent decode, "
+                       "config-5 rows and lengths (bf16 rows)",
+           "value": round(nbytes / ms_fused / 1e6, 2), "unit": "GB/s",
+           "ms_per_step": round(ms_fused, 5), "ms_separate_launches": round(ms_sep, 5),
+           "small_batch": {"workload": "16 sequences of 256..4096 keys, graph replay",
+                           "ms_fused": round(sm_fused, 5), "ms_separate_launches": round(sm_sep, 5)},
+           "roofline": {"bound": "hbm", "kernel": "mla decode step operator (one launch: rows + attention; "
+                                                  "merge)",
+                        "achieved": round(nbytes / ms_fused / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(nbytes / ms_fused / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms_fused, 5), "algorithmic_bytes": nbytes}}
+    return res
+
+
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 
@@ -660,6 +728,7 @@ SECONDARY = {
     "c8_decode": bench_c8,
     "mla_decode": bench_mla,
     "mla_decode_c8": bench_mla_c8,
+    "mla_decode_step": bench_mla_step,
     "gqa_decode_hd256": bench_decode_hd256,
     "gqa_decode_page16": bench_decode_page16,
     "mixed_prefill_decode": bench_mixed,

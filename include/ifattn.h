@@ -275,6 +275,28 @@ int32_t ifattn_page_reset_checked(void *field, uint64_t field_bytes, const uint6
 int32_t ifattn_state_copy_checked(void *field, uint64_t field_bytes, const uint64_t *ranges,
                                   uint64_t count, int32_t *status, void *stream);
 
+/* The fused MLA decode step: the cache writer of ifattn_mla_norm_rope_cache_write
+ * and the decode attention of ifattn_mla_decode_bf16 (packed = 0, bf16 rows) or
+ * ifattn_mla_decode_c8 (packed = 1, 656-byte rows) in one launch. For each
+ * sequence s the step's latent row x_new[s] ([num_seqs, 576] bf16: 512 latent +
+ * 64 rope, with cos/sin [num_seqs, 64] bf16 and gamma [512] bf16) is normalized,
+ * roped and stored at the sequence's last position seq_lens[s] - 1 (the slot
+ * block_tables[s][(len-1)/block_size] * block_size + (len-1) % block_size;
+ * sequences with seq_lens[s] = 0 write nothing), then attended over with the
+ * other cached keys. Rows and outputs are bit-identical to the writer followed
+ * by the decode entry point (the same code writes the row); the writer's
+ * separate launch disappears. Replaces resident::normalized_cache_append
+ * followed by attend_packed / attend (native/src/resident_cache_writer.h:5-20,
+ * token_executor.h:841-906) for a decode step. Workspace as
+ * ifattn_mla_decode_workspace_size. */
+int32_t ifattn_mla_decode_step(const void *q, const void *x_new, const void *gamma,
+                               const void *cos, const void *sin, float eps, void *cache,
+                               int32_t packed, const int32_t *block_tables, int32_t table_stride,
+                               const int32_t *seq_lens, void *out, int32_t num_seqs, int32_t heads,
+                               int32_t block_size, int64_t num_blocks, int32_t max_context,
+                               float scale, void *workspace, uint64_t workspace_bytes,
+                               void *stream);
+
 /* ---- packed-MLA attention over query rows (windows, sparse lists, sinks) ----- */
 
 /* Rows: sequence s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) (NULL:

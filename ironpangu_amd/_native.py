@@ -67,6 +67,8 @@ SIGNATURES = {
                                      u64, vp]),
     "ifattn_mla_decode_c8": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, i64, i32, f32, vp, u64,
                                    vp]),
+    "ifattn_mla_decode_step": (i32, [vp, vp, vp, vp, vp, f32, vp, i32, vp, i32, vp, vp, i32, i32, i32,
+                                     i64, i32, f32, vp, u64, vp]),
     "ifattn_mla_attention_workspace_size": (u64, [i32, i32, i32, i32, i32, i32, i32]),
     "ifattn_mla_window_attention_bf16": (i32, [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp, vp, i32,
                                                vp, i32, i32, i64, i32, f32, vp, u64, vp]),

@@ -47,6 +47,7 @@
 // on the variant (MlaCfg).
 #include "common.h"
 #include "ifattn_internal.h"
+#include "mla_row_write.h"
 #include "split_k.h"
 
 namespace ifattn {
@@ -89,6 +90,16 @@ struct MlaParams {
   int grid;         // persistent attention workgroups
   int self_plan;    // the attention workgroups plan the call themselves (no plan launch)
   float scale_log2;
+};
+
+// Fused decode step (ifattn_mla_decode_step): the step's new latent rows x
+// [rows, 576] bf16, normalized and roped into the cache at each sequence's last
+// position by the workgroup that reads that position. A kernel argument of its
+// own: in MlaParams it cost the plain C8 kernel two spilled registers.
+struct MlaStep {
+  const uint16_t *x, *gamma, *cos, *sin;
+  uint8_t *cache;
+  float eps;
 };
 
 // Keys of one row: [lo, hi) are positions (dense) or index-list slots
@@ -1083,8 +1094,10 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
   __syncthreads();
 }
 
-template <int F, bool SPARSE, bool WIDE>
-__global__ __launch_bounds__(64 * (MlaCfg<F, SPARSE, WIDE>::NW), (MlaCfg<F, SPARSE, WIDE>::WGS)) void mla_attention_kernel(MlaParams p) {
+// STEP: the fused decode step (mla_step_kernel); the plain calls run kernels
+// without its row writes and its kernel argument.
+template <int F, bool SPARSE, bool WIDE, bool STEP>
+__device__ __forceinline__ void mla_attention_body(const MlaParams &p, const MlaStep &st) {
   using Cfg = MlaCfg<F, SPARSE, WIDE>;
   constexpr int NW = Cfg::NW;
   __shared__ __align__(16) uint8_t ring[Cfg::RING];
@@ -1125,6 +1138,54 @@ __global__ __launch_bounds__(64 * (MlaCfg<F, SPARSE, WIDE>::NW), (MlaCfg<F, SPAR
   };
   // Workgroup b walks the shares b, b + grid, ... row by row: a row's sink
   // block is one event at its first unit, its tiles j at first + 32 j.
+  if constexpr (STEP) {
+    static_assert(!SPARSE && !mla_rq(F), "the fused step is a dense bf16 / C8 decode");
+    // Fused decode step: before any tile is loaded, the workgroup writes the
+    // step's row of every sequence whose last tile (the one holding its last
+    // position) lies in one of its shares; no other workgroup reads that tile.
+    // One thread per sequence finds them (in parallel: a serial walk of the
+    // rows put a chain of dependent loads ahead of the first tile); each wave
+    // then writes the rows its lanes found, one row at a time. The decode
+    // rows are one per sequence, without window or sinks, so tile 0 of row r
+    // sits at unit row_pos[r] + row_cost.
+    const Shares sh = mla_shares(p, share);
+    for (int base = 0; base < p.num_rows; base += NW * 64) {
+      const int row = base + int(threadIdx.x);
+      bool mine = false;
+      int last = 0;
+      if (row < p.num_rows) {
+        const int64_t pos = self ? int64_t(s_pos[row]) : p.row_pos[row];
+        int kv = p.kv_lens[row];
+        kv = kv > p.max_context ? p.max_context : kv;
+        if (kv > 0) {
+          const int tiles = (kv + kMlaTile - 1) / kMlaTile;
+          const int wb = sh.worker(pos + p.row_cost + int64_t(kMlaTile) * (tiles - 1));
+          mine = wb < workers && wb % int(gridDim.x) == int(blockIdx.x);
+          last = kv - 1;
+        }
+      }
+      uint64_t todo = __ballot(mine);
+      while (todo) {
+        const int bit = __builtin_ctzll(todo);
+        todo &= todo - 1;
+        const int r = base + w * 64 + bit;
+        const int lr = __shfl(last, bit, 64);
+        int blk = ld_const(p.block_tables + int64_t(r) * p.table_stride + lr / p.block_size);
+        blk = blk < 0 ? 0 : (blk >= p.num_blocks ? int(p.num_blocks - 1) : blk);
+        const int64_t slot_w = int64_t(blk) * p.block_size + (lr & (p.block_size - 1));
+        mla_norm_rope_row<F == kFmtC8>(st.x + int64_t(r) * 576, st.gamma, st.cos + int64_t(r) * 64,
+                                       st.sin + int64_t(r) * 64, st.eps,
+                                       st.cache + slot_w * MlaRow<F>::BYTES, lane);
+      }
+    }
+    // The stores must have reached L2 before any wave loads the tile: a wait
+    // on this wave's stores suffices, because only this workgroup reads the row
+    // and its lines are not in the CU's L1 (tile boundaries are whole 128-B
+    // lines apart, and the L1 starts the kernel invalidated). A device-scope
+    // fence here wrote back the XCD's L2 and cost 50 us a call.
+    lds_dma_wait<0>();
+    __syncthreads();
+  }
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const Shares sh = mla_shares(p, share);
@@ -1151,6 +1212,16 @@ __global__ __launch_bounds__(64 * (MlaCfg<F, SPARSE, WIDE>::NW), (MlaCfg<F, SPAR
       __syncthreads();  // every wave is done with xbuf (and the ring)
     }
   }
+}
+
+template <int F, bool SPARSE, bool WIDE>
+__global__ __launch_bounds__(64 * (MlaCfg<F, SPARSE, WIDE>::NW), (MlaCfg<F, SPARSE, WIDE>::WGS)) void mla_attention_kernel(MlaParams p) {
+  mla_attention_body<F, SPARSE, WIDE, false>(p, MlaStep{});
+}
+
+template <int F, bool WIDE>
+__global__ __launch_bounds__(64 * (MlaCfg<F, false, WIDE>::NW), (MlaCfg<F, false, WIDE>::WGS)) void mla_step_kernel(MlaParams p, MlaStep st) {
+  mla_attention_body<F, false, WIDE, true>(p, st);
 }
 
 // Combine one (row, head): the row's partials (the sink partial first, when
@@ -1229,6 +1300,8 @@ namespace {
 
 struct MlaCall {
   int fmt;  // MlaFmt
+  const uint16_t *w_x = nullptr, *w_gamma = nullptr, *w_cos = nullptr, *w_sin = nullptr;
+  float w_eps = 0.0f;
   const void *q, *cache;
   const float *row_scales;  // row-quantized formats
   const int32_t *block_tables;
@@ -1392,8 +1465,14 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   hipStream_t s = static_cast<hipStream_t>(c.stream);
   if (!p.self_plan) mla_plan_kernel<<<1, 1024, 0, s>>>(p);
   constexpr int kThreads = 64 * kMlaWaves;
+  const bool step = c.w_x != nullptr;
+  MlaStep st{c.w_x, c.w_gamma, c.w_cos, c.w_sin,
+             const_cast<uint8_t *>(static_cast<const uint8_t *>(c.cache)), c.w_eps};
+  if (step && (sparse || rq || c.cu_q || c.window || c.n_sinks))
+    return fail(IFATTN_EINVAL, what, "the fused step is a plain decode");
   if (c.fmt == kFmtC8) {
     if (sparse) mla_attention_kernel<kFmtC8, true, false><<<grid, kThreads, 0, s>>>(p);
+    else if (step) mla_step_kernel<kFmtC8, false><<<grid, kThreads, 0, s>>>(p, st);
     else mla_attention_kernel<kFmtC8, false, false><<<grid, kThreads, 0, s>>>(p);
   } else if (c.fmt == kFmtRq8) {
     mla_attention_kernel<kFmtRq8, false, false><<<grid, kThreads, 0, s>>>(p);
@@ -1401,7 +1480,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
     mla_attention_kernel<kFmtRq4, false, false><<<grid, kThreads, 0, s>>>(p);
   } else {
     if (sparse) mla_attention_kernel<kFmtBf16, true, false><<<grid, kThreads, 0, s>>>(p);
+    else if (wide && step) mla_step_kernel<kFmtBf16, true><<<grid, kThreads, 0, s>>>(p, st);
     else if (wide) mla_attention_kernel<kFmtBf16, false, true><<<grid, kThreads, 0, s>>>(p);
+    else if (step) mla_step_kernel<kFmtBf16, false><<<grid, kThreads, 0, s>>>(p, st);
     else mla_attention_kernel<kFmtBf16, false, false><<<grid, kThreads, 0, s>>>(p);
   }
   mla_merge_kernel<<<dim3(c.num_rows, c.heads), 256, 0, s>>>(p);
@@ -1538,4 +1619,27 @@ extern "C" int32_t ifattn_mla_window_attention_rowq(
   c.sink_v = sink_values;
   c.n_sinks = n_sinks;
   return mla_run(c, "mla row-quantized attention");
+}
+
+extern "C" int32_t ifattn_mla_decode_step(const void *q, const void *x_new, const void *gamma,
+                                          const void *cos, const void *sin, float eps, void *cache,
+                                          int32_t packed, const int32_t *block_tables,
+                                          int32_t table_stride, const int32_t *seq_lens, void *out,
+                                          int32_t num_seqs, int32_t heads, int32_t block_size,
+                                          int64_t num_blocks, int32_t max_context, float scale,
+                                          void *workspace, uint64_t workspace_bytes, void *stream) {
+  if (!x_new || !gamma || !cos || !sin)
+    return fail(IFATTN_EINVAL, "mla decode step: null writer input");
+  if (!aligned16(x_new) || !aligned16(gamma) || !aligned4(cos) || !aligned4(sin))
+    return fail(IFATTN_EINVAL, "mla decode step: misaligned writer input");
+  if (!(eps >= 0.0f)) return fail(IFATTN_EINVAL, "mla decode step: eps must be >= 0");
+  MlaCall c = decode_call(packed ? kFmtC8 : kFmtBf16, q, cache, block_tables, table_stride, seq_lens,
+                          out, num_seqs, heads, block_size, num_blocks, max_context, scale, workspace,
+                          workspace_bytes, stream);
+  c.w_x = static_cast<const uint16_t *>(x_new);
+  c.w_gamma = static_cast<const uint16_t *>(gamma);
+  c.w_cos = static_cast<const uint16_t *>(cos);
+  c.w_sin = static_cast<const uint16_t *>(sin);
+  c.w_eps = eps;
+  return mla_run(c, "mla decode step");
 }

@@ -347,6 +347,40 @@ def mla_decode(q, cache, block_tables, seq_lens, max_context, scale=None, out=No
     return out
 
 
+def mla_decode_step(q, x_new, gamma, cos, sin, cache, block_tables, seq_lens, max_context,
+                    eps=1e-5, scale=None, out=None, workspace=None, stream=None):
+    """Fused MLA decode step: x_new [num_seqs, 576] bf16 rows are normalized
+    (gamma [512] bf16, eps), roped (cos/sin [num_seqs, 64] bf16) and stored at
+    each sequence's last position seq_lens[s] - 1, then attended over with
+    q [num_seqs, heads, 576]. cache bf16 [blocks, bs, 576] or uint8 [blocks, bs, 656]."""
+    c8 = cache.dtype == torch.uint8
+    _dev(q, x_new, gamma, cos, sin, cache, block_tables, seq_lens, out, workspace)
+    _req(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == 576,
+         "q: bf16 [num_seqs, heads, 576]")
+    ns, h, _ = q.shape
+    _req(x_new.dtype == torch.bfloat16 and tuple(x_new.shape) == (ns, 576), "x_new: bf16 [num_seqs, 576]")
+    _req(gamma.dtype == torch.bfloat16 and gamma.numel() == 512, "gamma: bf16 [512]")
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _req(t.dtype == torch.bfloat16 and tuple(t.shape) == (ns, 64), f"{n}: bf16 [num_seqs, 64]")
+    _req(cache.dim() == 3 and cache.shape[2] == (656 if c8 else 576)
+         and cache.dtype in (torch.uint8, torch.bfloat16), "cache: bf16 [.., 576] or uint8 [.., 656]")
+    nb, bs, _ = cache.shape
+    _check_tables(block_tables, seq_lens, ns, bs, max_context)
+    if scale is None:
+        scale = 1.0 / math.sqrt(192.0)
+    if out is None:
+        out = torch.empty((ns, h, 512), dtype=torch.bfloat16, device=q.device)
+    _req(tuple(out.shape) == (ns, h, 512) and out.dtype == torch.bfloat16, "out: bf16 [n, heads, 512]")
+    if workspace is None:
+        workspace = mla_workspace(ns, h, max_context, bs, q.device)
+    st = lib().ifattn_mla_decode_step(
+        _ptr(q), _ptr(x_new), _ptr(gamma), _ptr(cos), _ptr(sin), float(eps), _ptr(cache), int(c8),
+        _ptr(block_tables), block_tables.shape[1], _ptr(seq_lens), _ptr(out), ns, h, bs, nb,
+        max_context, float(scale), _ptr(workspace), workspace.numel(), _stream(stream))
+    check(st, "ifattn_mla_decode_step")
+    return out
+
+
 def mla_attention(q, cache, block_tables, kv_lens, max_context, cu_seqlens=None, indices=None,
                   window=0, sink_keys=None, sink_values=None, scale=None, out=None,
                   workspace=None, stream=None, row_scales=None, bits=8):
