@@ -35,9 +35,11 @@
 //    share writes bf16 output directly.
 //  * a register ring of decode_stages() tiles keeps the next tiles' loads in
 //    flight while the current tile is reduced.
-// C8: K/V int8 with an fp32 scale per (token, kv head). int8 -> bf16 is exact,
-// so QK^T runs on the integer codes and the K scale multiplies the score; the
-// V scale is folded into the probability before the PV MFMA.
+// C8: K/V int8 with an fp32 scale per (token, kv head). QK^T runs on the
+// integer codes as fp16 (biased by kI8Bias, exact; q scaled into fp16 range
+// and kI8Bias * sum(q) subtracted from each score) and the K scale multiplies
+// the score; V codes become exact bf16 and the V scale is folded into the
+// probability before the PV MFMA.
 #include <cstdlib>
 #include <mutex>
 
@@ -239,13 +241,6 @@ __device__ __forceinline__ uint32_t i8pair_to_bf16x2(int a, int b) {
   // high half of the fp32 pattern is the bf16 value.
   return perm_b32(__float_as_uint(float(b)), __float_as_uint(float(a)), 0x07060302u);
 }
-__device__ __forceinline__ u32x4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  const int32_t l = int32_t(lo), h = int32_t(hi);
-  return u32x4{i8pair_to_bf16x2((l << 24) >> 24, (l << 16) >> 24),
-               i8pair_to_bf16x2((l << 8) >> 24, l >> 24),
-               i8pair_to_bf16x2((h << 24) >> 24, (h << 16) >> 24),
-               i8pair_to_bf16x2((h << 8) >> 24, h >> 24)};
-}
 __device__ __forceinline__ int i8_at(uint32_t w, int b) {
   return (int32_t(w) << (24 - 8 * b)) >> 24;
 }
@@ -277,6 +272,22 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
       const int d0 = k_lines<D, C8>() ? 32 * s + 8 * g : (D / 4) * g + 8 * s;
       qv[s] = buf_load_x4(rq, qoff + uint32_t(d0) * 2);
     }
+  }
+  // C8 keys: QK^T runs in fp16 on the codes biased by kI8Bias (exact, three
+  // VALU ops per four codes against a convert per code), q scaled per head by
+  // a power of two into fp16 range; kI8Bias * sum(q) leaves each score.
+  float k_corr = 0.0f, sl2 = p.scale_log2;
+  if constexpr (C8) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) amax = fmaxf(amax, bf16x8_absmax(qv[s]));
+    amax = max_xor32(max_xor16(amax));
+    const float qs = f16_range_scale(amax);
+    float qsum = 0.0f;
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s) qv[s] = bf16x8_to_f16(qv[s], qs, &qsum);
+    sl2 = p.scale_log2 / qs;
+    k_corr = kI8Bias * sum_xor32(sum_xor16(qsum)) * sl2;
   }
 
   LaneOffsets o;
@@ -351,15 +362,16 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, int seq, int 
         } else if constexpr (!C8)
           a = t.k[mt][s];
         else
-          a = i8x8_to_bf16x8(t.k[mt][s][0], t.k[mt][s][1]);
-        sacc[mt] = mfma16x16x32(a, qv[s], sacc[mt]);
+          a = i8x8_to_f16_biased(t.k[mt][s][0], t.k[mt][s][1]);
+        sacc[mt] = C8 ? mfma16x16x32_f16(a, qv[s], sacc[mt]) : mfma16x16x32(a, qv[s], sacc[mt]);
       }
     }
     float x[TPL];
 #pragma unroll
     for (int mt = 0; mt < TR::MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[4 * mt + r] = sacc[mt][r] * p.scale_log2;
+      for (int r = 0; r < 4; ++r)
+        x[4 * mt + r] = C8 ? __builtin_fmaf(sacc[mt][r], sl2, -k_corr) : sacc[mt][r] * sl2;
     if constexpr (C8) {
 #pragma unroll
       for (int j = 0; j < TPL; ++j) x[j] *= t.ks[j];
