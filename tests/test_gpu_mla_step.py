@@ -83,3 +83,48 @@ def test_fused_step_equals_writer_then_decode(packed, seed, lens, bs):
     ref_cache = host if packed else host.view(np.uint16).reshape(-1, 576)
     exp = oracle.mla_decode(q, ref_cache, table, lens, 16, bs, 1.0 / np.sqrt(192.0), c8=packed)
     assert_close(bf16_host(o2), exp)
+
+
+@pytest.mark.parametrize("packed", [False, True], ids=["bf16", "c8"])
+def test_fused_step_graph_replay(packed):
+    """The fused step captured into a HIP graph: three replays, each with new
+    latent rows copied into the captured input and the cache restored, with
+    eager calls between them; every replay equals the eager call on the same
+    inputs bit for bit (outputs and caches)."""
+    import torch
+    from ironpangu_amd import ops
+    print(f"mla step graph packed={packed}", flush=True)
+    lens = list(np.random.default_rng(11).integers(1, 9000, 40)) + [0, 1]
+    q, x, gamma, cos, sin, cache, table, lens, slots, maxc = case(21, lens, 64, packed)
+    bfv = lambda t: t.view(torch.bfloat16)
+    dq, dx, dg, dc, ds = (to_dev(a) for a in (q, x, gamma, cos, sin))
+    dt, dl = to_dev(table), to_dev(lens)
+    c0 = to_dev(cache) if packed else to_dev(cache).view(torch.bfloat16)
+    cg = c0.clone()
+    ws = ops.mla_workspace(len(lens), 16, maxc, 64)
+    out = torch.empty((len(lens), 16, 512), dtype=torch.bfloat16, device="cuda")
+
+    def step(c, o, xin):
+        ops.mla_decode_step(bfv(dq), bfv(xin), bfv(dg), bfv(dc), bfv(ds), c, dt, dl, maxc,
+                            out=o, workspace=ws)
+
+    step(cg, out, dx)  # first call on the device before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step(cg, out, dx)
+    rng = np.random.default_rng(5)
+    for r in range(3):
+        xr = to_dev(bf(rng.standard_normal((len(lens), 576)).astype(f32)))
+        dx.copy_(xr)
+        cg.copy_(c0)
+        g.replay()
+        torch.cuda.synchronize()
+        ce = c0.clone()
+        oe = torch.empty_like(out)
+        ws_e = ops.mla_workspace(len(lens), 16, maxc, 64)
+        ops.mla_decode_step(bfv(dq), bfv(xr), bfv(dg), bfv(dc), bfv(ds), ce, dt, dl, maxc,
+                            out=oe, workspace=ws_e)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), oe.view(torch.int16)), f"replay {r}: outputs differ"
+        assert torch.equal(cg.view(torch.uint8), ce.view(torch.uint8)), f"replay {r}: caches differ"
