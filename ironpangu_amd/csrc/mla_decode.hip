@@ -1324,7 +1324,9 @@ struct MlaCall {
 
 // Share skew (permille) of dense bf16 calls, as for the GQA decode: odd
 // workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
-// 0.4225 ms with 3%; 0.4307 ms with the opposite skew). C8 calls keep equal
+// 0.4225 ms with 3%, 0.4165-0.4181 ms with 6% against 0.4211-0.4216 at 3% on
+// one box, 4.5%: 0.4185, 8%: 0.4172-0.4191, 10%: 0.4200-0.4214; 0.4307 ms
+// with the opposite skew). C8 calls keep equal
 // shares (3% and 6% measured 0.5-1.5% slower), and so do sparse calls (their
 // shares are capped by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides
 // the default of dense calls.
@@ -1334,7 +1336,7 @@ inline int mla_skew_pm(bool c8, bool sparse) {
     const int x = e ? atoi(e) : 1000;
     return (x >= 0 && x <= 200) ? x : 1000;
   }();
-  return sparse ? 0 : (v != 1000 ? v : (c8 ? 0 : 30));
+  return sparse ? 0 : (v != 1000 ? v : (c8 ? 0 : 60));
 }
 // Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
 // share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)

@@ -663,6 +663,7 @@ template <int D, bool C8>
 void launch_decode(const DecodeParams &p0, const RowWrite &wr, hipStream_t s) {
   const int waves = p0.kv_heads < max_decode_waves(D) ? p0.kv_heads : max_decode_waves(D);
   DecodeParams p = p0;
+  p.seq_cost = decode_seq_cost(C8);
   p.self_plan = decode_self_plan(p, 64 * waves) ? 1 : 0;
   p.skew_pm = decode_skew_pm(C8, D);
   launch_prologue(p, wr, s);

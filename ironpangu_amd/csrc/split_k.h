@@ -392,14 +392,16 @@ inline int wgs_per_cu() {
 
 // Work units charged per sequence on top of its tokens: the item start of a
 // decode workgroup (q and block-id loads, the first tiles' latency) costs about
-// as much as streaming this many tokens. IFATTN_DECODE_SEQ_COST overrides it.
-inline int decode_seq_cost() {
+// as much as streaming this many tokens: 64 for bf16 caches, 192 for C8, whose
+// tokens stream twice as fast (config 4: 0.2080 -> 0.2050 ms; 128: 0.2055,
+// 256: 0.2061). IFATTN_DECODE_SEQ_COST overrides both.
+inline int decode_seq_cost(bool c8 = false) {
   static int v = [] {
     const char *e = getenv("IFATTN_DECODE_SEQ_COST");
     const int x = e ? atoi(e) : -1;
-    return (x >= 0 && x <= 65536) ? x : 64;
+    return (x >= 0 && x <= 65536) ? x : -1;
   }();
-  return v;
+  return v >= 0 ? v : (c8 ? 192 : 64);
 }
 // Share skew (permille) of bf16 decode at head_dim <= 128: workgroups are
 // dispatched round-robin over the 8 XCDs, so odd workers run on odd XCDs,
