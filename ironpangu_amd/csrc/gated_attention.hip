@@ -359,20 +359,30 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
 // eight partials ((m, l) with O, lane l owning dims 4l .. 4l + 3) costs one
 // memory round trip. A partition whose rows were all out of range has m = -inf,
 // weight 0 and zero O. The waves' (m, l, O) meet in LDS.
+// Nothing waits for the live count before loading: the first 64 list entries
+// of each wave and the gate are loaded with it (entries past the count are
+// in the request's list row, their ids clamped, their partials loaded and then
+// given weight 0), so a request of up to 64 * kMergeWaves live partitions
+// costs two dependent memory round trips instead of four.
 constexpr int kMergeWaves = 16;
 __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedParams p) {
   __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
   __shared__ f32x4 s_o[kMergeWaves][64];
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int n = p.live_count[b];
   const int32_t *parts = p.live_parts + int64_t(b) * p.parts;
+  const int64_t o_out = (int64_t(b) * kHeads + h) * kD + 4 * lane;
+  const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o_out);
+  int my_part = w + kMergeWaves * lane < p.parts ? parts[w + kMergeWaves * lane] : 0;
+  const int n = p.live_count[b];
   const int64_t base = int64_t(b) * p.parts * kHeads + h;
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
   constexpr int U = 8;
   for (int k0 = w; k0 < n; k0 += kMergeWaves * 64) {
-    const int kk = k0 + kMergeWaves * lane;
-    const int my_part = kk < n ? parts[kk] : 0;
+    if (k0 != w) {
+      const int kk = k0 + kMergeWaves * lane;
+      my_part = kk < p.parts ? parts[kk] : 0;
+    }
     const int cnt = (n - k0 + kMergeWaves - 1) / kMergeWaves < 64 ? (n - k0 + kMergeWaves - 1) / kMergeWaves : 64;
     for (int u0 = 0; u0 < cnt; u0 += U) {
       float2 ml[U];
@@ -380,9 +390,15 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = u0 + u;
-        const int64_t r = base + int64_t(__builtin_amdgcn_readlane(my_part, i < 64 ? i : 63)) * kHeads;
-        ml[u] = i < cnt ? *reinterpret_cast<const float2 *>(p.part_ml + r * 2) : make_float2(-INFINITY, 0.0f);
-        o[u] = i < cnt ? *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane) : f32x4{0, 0, 0, 0};
+        int part = __builtin_amdgcn_readlane(my_part, i < 64 ? i : 63);
+        part = part < 0 ? 0 : (part >= p.parts ? p.parts - 1 : part);
+        const int64_t r = base + int64_t(part) * kHeads;
+        ml[u] = *reinterpret_cast<const float2 *>(p.part_ml + r * 2);
+        o[u] = *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane);
+        if (i >= cnt) {
+          ml[u] = make_float2(-INFINITY, 0.0f);
+          o[u] = f32x4{0, 0, 0, 0};
+        }
       }
       float mx = m_run;
 #pragma unroll
@@ -421,9 +437,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
     }
   }
   const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  const int64_t o = (int64_t(b) * kHeads + h) * kD + 4 * lane;
-  const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o);
-  *reinterpret_cast<u32x2 *>(p.out + o) =
+  *reinterpret_cast<u32x2 *>(p.out + o_out) =
       u32x2{pack_bf16x2(acc[0] * inv * bf16_bits_to_f32(gw[0] & 0xffffu),
                         acc[1] * inv * bf16_bits_to_f32(gw[0] >> 16)),
             pack_bf16x2(acc[2] * inv * bf16_bits_to_f32(gw[1] & 0xffffu),
