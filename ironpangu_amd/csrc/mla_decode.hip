@@ -955,7 +955,7 @@ __device__ __forceinline__ void mla_item(const MlaParams &p, uint8_t *ring, floa
 // cache keys, four waves per row, heads in the MFMA N dimension. The (m, l, O)
 // partial of the sinks alone goes to the row's first partial slot. Runs as the
 // event at the start of the row's work units, in the share that holds it.
-template <int NW>
+template <int NW, bool DB>
 __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[8], int row, int slot0,
                                               int w, int lane) {
   using Geo = MlaGeo<NW>;
@@ -975,12 +975,16 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
   for (int i = 0; i < EPL; ++i) acc.o[i] = f32x4{0, 0, 0, 0};
   acc.m = -INFINITY;
   acc.l = 0.0f;
-  for (int t0 = 0; t0 < n; t0 += kMlaTile) {
+  // DB (the one-workgroup-per-CU variant, which has the registers): tile
+  // t + 1's rows are loaded (from L2: every row reads the same sinks) while
+  // tile t is computed, two register sets alternating. The variants with
+  // several workgroups per CU spilled with the second set and load one tile at
+  // a time.
+  auto load = [&](int t0, u32x4 (&k)[2][KS + 1], u32x4 (&v)[8]) {
     const int live_n = n - t0 < kMlaTile ? n - t0 : kMlaTile;
     // Rows past the last sink read as zero (buffer extent).
     const auto rk = make_rsrc(p.sink_k + int64_t(t0) * 576, uint32_t(live_n) * 1152u);
     const auto rv = make_rsrc(p.sink_v + int64_t(t0) * 512, uint32_t(live_n) * 1024u);
-    u32x4 k[2][KS + 1], v[8];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
       const uint32_t r = uint32_t(16 * mt + c) * 1152u;
@@ -998,9 +1002,29 @@ __device__ __forceinline__ void mla_sink_item(const MlaParams &p, float (*xbuf)[
         v[j] = u32x4{x[0], x[1], 0u, 0u};
       }
     }
+  };
+  auto math = [&](int t0, const u32x4 (&k)[2][KS + 1], const u32x4 (&v)[8]) {
+    const int live_n = n - t0 < kMlaTile ? n - t0 : kMlaTile;
     const uint32_t live = live_n >= 32 ? 0xFFFFFFFFu : ((1u << live_n) - 1u);
     mla_tile_math<false, NW>(acc, k, v, nullptr, qv, xbuf, live, p.scale_log2, w, lane);
     __syncthreads();  // xbuf is rewritten by the next tile
+  };
+  if constexpr (DB) {
+    u32x4 ka[2][KS + 1], va[8], kb[2][KS + 1], vb[8];
+    if (n > 0) load(0, ka, va);
+    for (int t0 = 0; t0 < n; t0 += 2 * kMlaTile) {
+      if (t0 + kMlaTile < n) load(t0 + kMlaTile, kb, vb);
+      math(t0, ka, va);
+      if (t0 + kMlaTile >= n) break;
+      if (t0 + 2 * kMlaTile < n) load(t0 + 2 * kMlaTile, ka, va);
+      math(t0 + kMlaTile, kb, vb);
+    }
+  } else {
+    for (int t0 = 0; t0 < n; t0 += kMlaTile) {
+      u32x4 k[2][KS + 1], v[8];
+      load(t0, k, v);
+      math(t0, k, v);
+    }
   }
   float l_tot = sum_xor16(acc.l);
   l_tot = sum_xor32(l_tot);
@@ -1195,7 +1219,7 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
       if (pos >= hi) break;
       const int slot0 = self ? mla_se_slot(s_se[row]) : ld_const(&p.row_slot[row].x);
       if (sinks && pos >= lo) {
-        mla_sink_item<NW>(p, xbuf, row, slot0, w, lane);
+        mla_sink_item<NW, Cfg::WGS == 1>(p, xbuf, row, slot0, w, lane);
         __syncthreads();  // every wave is done with xbuf
       }
       const int seq = !p.cu_q ? row : (self ? mla_seq_of(p, row) : ld_const(p.row_seq + row));
