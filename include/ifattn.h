@@ -287,8 +287,11 @@ int32_t ifattn_state_copy_checked(void *field, uint64_t field_bytes, const uint6
  * by the decode entry point (the same code writes the row); the writer's
  * separate launch disappears. Replaces resident::normalized_cache_append
  * followed by attend_packed / attend (native/src/resident_cache_writer.h:5-20,
- * token_executor.h:841-906) for a decode step. Workspace as
- * ifattn_mla_decode_workspace_size. */
+ * token_executor.h:841-906) for a decode step. The block holding a sequence's
+ * last position must belong to that sequence alone in this call (as a decode
+ * step's tail block does): only the workgroup that reads a sequence's last tile
+ * waits for its row, so another sequence reading the same block could see the
+ * row before or after the write. Workspace as ifattn_mla_decode_workspace_size. */
 int32_t ifattn_mla_decode_step(const void *q, const void *x_new, const void *gamma,
                                const void *cos, const void *sin, float eps, void *cache,
                                int32_t packed, const int32_t *block_tables, int32_t table_stride,

@@ -352,7 +352,9 @@ def mla_decode_step(q, x_new, gamma, cos, sin, cache, block_tables, seq_lens, ma
     """Fused MLA decode step: x_new [num_seqs, 576] bf16 rows are normalized
     (gamma [512] bf16, eps), roped (cos/sin [num_seqs, 64] bf16) and stored at
     each sequence's last position seq_lens[s] - 1, then attended over with
-    q [num_seqs, heads, 576]. cache bf16 [blocks, bs, 576] or uint8 [blocks, bs, 656]."""
+    q [num_seqs, heads, 576]. cache bf16 [blocks, bs, 576] or uint8 [blocks, bs, 656].
+    The block holding each sequence's last position must not be shared with
+    another sequence of the call."""
     c8 = cache.dtype == torch.uint8
     _dev(q, x_new, gamma, cos, sin, cache, block_tables, seq_lens, out, workspace)
     _req(q.dtype == torch.bfloat16 and q.dim() == 3 and q.shape[2] == 576,
