@@ -174,11 +174,13 @@ __device__ __forceinline__ float bf16x8_absmax(u32x4 v) {
     m = fmaxf(m, fmaxf(fabsf(bf16_bits_to_f32(v[i] & 0xFFFFu)), fabsf(bf16_bits_to_f32(v[i] >> 16))));
   return m;
 }
-// Power of two 2^-e (e >= 0) that brings amax below 2^15, inside fp16's range
-// with room for the biased product sums.
+// Power of two 2^-e that brings amax into [2^14, 2^15): inside fp16's range
+// with room for the biased product sums, and away from fp16's subnormals, so
+// small q keep their 11 significant bits (e is clamped to [-100, 127]; a zero
+// or subnormal amax gets 2^100).
 __device__ __forceinline__ float f16_range_scale(float amax) {
   int e = int((__float_as_uint(amax) >> 23) & 0xFFu) - 127 - 14;
-  e = e > 0 ? e : 0;
+  e = e < -100 ? -100 : (e > 127 ? 127 : e);
   return __uint_as_float(uint32_t(127 - e) << 23);
 }
 

@@ -158,3 +158,30 @@ def test_packed_attention_metadata():
         exp = np.where(np.arange(512) <= pos, np.arange(512), -1)
         assert np.array_equal(i[r], exp)
     assert list(lens.cpu().numpy()) == [1, 32, 33, 512, 601]
+
+
+@pytest.mark.parametrize("q_scale", [1e-4, 300.0, 3e4])
+def test_c8_decode_q_range(q_scale):
+    """C8 keys are scored with the fp16 MFMA (q scaled per head by a power of
+    two into fp16 range, codes biased by 1152): q far from unit size, small
+    enough that fp16 would lose it or large enough to overflow without the
+    scale, still gives the oracle's output. Heads mix magnitudes (every other
+    head 1/8 of the scale) so the per-head scale is exercised."""
+    import torch
+    from ironpangu_amd import ops
+    print(f"c8 q range {q_scale}", flush=True)
+    case = W.decode_host_case(12, num_seqs=6, lo=1, hi=1500, dist="uniform", q_heads=16,
+                              kv_heads=2, head_dim=128, block_size=64,
+                              pool_blocks=6 * 24 + 2, c8=True)
+    kc, vc, ks, vs = _quantize_pool_on_gpu(case)
+    qf = W.bf16_to_f32(case.host["q"]) * np.float32(q_scale / 64.0)
+    qf[:, 1::2] *= np.float32(0.125)
+    q = W.bf16_bits(qf)
+    scale = 1.0 / (q_scale * 0.5)  # keeps the softmax neither flat nor one-hot
+    out = ops.paged_decode(to_dev(q), kc, vc, to_dev(case.block_tables), to_dev(case.seq_lens),
+                           case.max_context, scale, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    exp = oracle.paged_decode(q, kc.cpu().numpy(), vc.cpu().numpy(), case.block_tables,
+                              case.seq_lens, 16, 2, 128, 64, scale,
+                              k_scale=ks.cpu().numpy(), v_scale=vs.cpu().numpy())
+    assert_close(bf16_host(out), exp)
