@@ -276,21 +276,35 @@ __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
   }
   for (int i = tid; i < p.parts; i += 1024) s_flag[i] = 0u;
   __syncthreads();
-  // Unconditional buffer loads (zeros past the row; the position test comes
-  // after the load), so all U loads of a thread are in flight together.
+  // Unconditional 16-byte buffer loads, four positions a lane (zeros past the
+  // row; the position test comes after the load), so all U loads of a thread
+  // are in flight together: a quarter of the load instructions of one
+  // position a lane.
   const auto rm = make_rsrc(p.mask + int64_t(b) * p.context, uint32_t(p.context) * 4u);
-  constexpr int U = 32;
-  for (int t0 = 0; t0 < p.context; t0 += U * 1024) {
-    float x[U];
+  constexpr int U = 8;
+  const int lanes_per_part = p.part >> 2;  // 16, 32 or 64 lanes cover a partition
+  for (int t0 = 0; t0 < p.context; t0 += U * 4096) {
+    u32x4 x[U];
 #pragma unroll
-    for (int e = 0; e < U; ++e) x[e] = buf_load_f32(rm, uint32_t(t0 + e * 1024 + tid) * 4u);
-    // A wave's 64 positions lie in one partition (partitions are 64-aligned
-    // multiples of 64): one flag store per wave, not one per lane (same-address
-    // LDS stores from many lanes serialise).
+    for (int e = 0; e < U; ++e) x[e] = buf_load_x4(rm, uint32_t(t0 + e * 4096 + tid * 4) * 4u);
+    // A wave's 256 positions hold 256 / part whole partitions (partitions are
+    // 64-aligned multiples of 64): lane 0 stores their flags from the ballot,
+    // not one store per lane (same-address LDS stores from many lanes
+    // serialise).
 #pragma unroll
     for (int e = 0; e < U; ++e) {
-      const int t = t0 + e * 1024 + tid;
-      if (__ballot(t < p.context && x[e] != -INFINITY) != 0 && lane == 0) s_flag[t >> p.part_shift] = 1u;
+      const int tb = t0 + e * 4096 + tid * 4;
+      bool live = false;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) live |= tb + j < p.context && __uint_as_float(x[e][j]) != -INFINITY;
+      const uint64_t bal = __ballot(live);
+      if (lane == 0 && bal != 0) {
+        const int wbase = t0 + e * 4096 + w * 256;
+        for (int q = 0; q < 64; q += lanes_per_part) {
+          const uint64_t m = lanes_per_part == 64 ? ~uint64_t(0) : ((uint64_t(1) << lanes_per_part) - 1) << q;
+          if (bal & m) s_flag[(wbase + 4 * q) >> p.part_shift] = 1u;
+        }
+      }
     }
   }
   __syncthreads();
