@@ -354,6 +354,51 @@ def bench_mla_c8(seed, steps, warmup):
     return res
 
 
+def bench_mla_rowq(seed, steps, warmup, bits):
+    """Config 5's rows and lengths over row-quantized latent rows (the
+    reference's integer cache: int8 or int4 codes of all 576 dims, one fp32
+    scale per row), attended directly with in-register dequantization. Codes
+    and scales are drawn at random (the kernel's cost does not depend on how
+    they were produced)."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd import workloads as W
+    case = W.mla_meta(seed)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 8 + bits)
+    row_bytes = 576 * bits // 8
+    cache = torch.randint(0, 256, (case.pool_blocks, case.block_size, row_bytes), generator=g,
+                          device=dev, dtype=torch.uint8)
+    scales = torch.rand(case.pool_blocks * case.block_size, generator=g, device=dev) * 0.01 + 0.001
+    q = (torch.randn((case.num_seqs, case.heads, 576), generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    tables = torch.from_numpy(case.block_tables).to(dev)
+    lens = torch.from_numpy(case.seq_lens).to(dev)
+    n = ops.lib().ifattn_mla_attention_workspace_size(case.num_seqs, case.heads, case.max_context, 0, 0, 0,
+                                                      case.block_size)
+    ws = torch.empty(max(int(n), 16), dtype=torch.uint8, device=dev)
+    out = torch.empty((case.num_seqs, case.heads, 512), dtype=torch.bfloat16, device=dev)
+
+    def attn():
+        ops.mla_attention(q, cache, tables, lens, case.max_context, scale=case.scale, out=out,
+                          workspace=ws, row_scales=scales, bits=bits)
+
+    ms = timed(attn, steps, warmup)
+    L = case.seq_lens.astype(np.int64)
+    nbytes = int(L.sum()) * (row_bytes + 4) + case.num_seqs * case.heads * (576 + 512) * 2 + \
+        int(((L + 63) // 64).sum()) * 4 + case.num_seqs * 4
+    res = {"workload": f"packed-MLA latent decode over row-quantized int{bits} rows (+ fp32 row "
+                       f"scale), config-5 rows and lengths",
+           "value": round(nbytes / ms / 1e6, 2), "unit": "GB/s", "ms_per_call": round(ms, 5),
+           "roofline": {"bound": "hbm", "kernel": f"mla_attention rowq{bits} operator",
+                        "achieved": round(nbytes / ms / 1e6, 2), "peak": HBM_PEAK_GBPS,
+                        "unit": "GB/s", "frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBPS, 4),
+                        "avg_ms": round(ms, 5), "algorithmic_bytes": nbytes}}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_mla(seed, steps, warmup):
     """Config 5: packed-MLA latent decode, 128 seqs, L log-uniform [1024,65536],
     16 heads, 576-wide bf16 rows, block 64, N(0,0.5)."""
@@ -739,6 +784,8 @@ SECONDARY = {
     "c8_decode": bench_c8,
     "mla_decode": bench_mla,
     "mla_decode_c8": bench_mla_c8,
+    "mla_decode_rowq8": lambda seed, steps, warmup: bench_mla_rowq(seed, steps, warmup, 8),
+    "mla_decode_rowq4": lambda seed, steps, warmup: bench_mla_rowq(seed, steps, warmup, 4),
     "mla_decode_step": bench_mla_step,
     "gqa_decode_hd256": bench_decode_hd256,
     "gqa_decode_page16": bench_decode_page16,

@@ -348,10 +348,13 @@ struct MlaCfg {
   // -> 489-491 us. Small calls keep one workgroup with a 4-slot ring (window
   // 2048 over 128 rows: 79 against 83 us with two).
   static constexpr bool B2 = !C8 && !SPARSE && WIDE;
-  // Row-quantized tiles run two workgroups with 3-slot rings: their gather
-  // addressing and the rope codes' extra MFMAs need more than the 168
-  // registers of three workgroups (they spilled there).
-  static constexpr int WGS = mla_rq(F) ? 2 : (C8 ? ((TIGHT && !SPARSE) ? 3 : 2) : (B2 ? 2 : 1));
+  // Row-quantized int8 tiles run two workgroups with 3-slot rings: their
+  // gather addressing, bf16 dequantization and the rope codes' extra MFMAs
+  // need more than the 168 registers of three workgroups (they spilled 17 and
+  // ran 0.514-0.520 against 0.488-0.490 ms on config-5 rows). Int4 tiles (9 KB)
+  // run three with 2-slot rings: 0.438-0.441 against 0.471-0.472 ms despite 8
+  // spilled registers.
+  static constexpr int WGS = F == kFmtRq8 ? 2 : (F == kFmtRq4 ? 3 : (C8 ? ((TIGHT && !SPARSE) ? 3 : 2) : (B2 ? 2 : 1)));
   // Waves per workgroup. Eight waves with 64-dim slices measured slower for
   // bf16 (612 against 532 us on 128 rows of log-uniform [1024, 65536] keys):
   // the score exchange then sums eight partials per tile.
@@ -362,7 +365,7 @@ struct MlaCfg {
 #ifndef IFATTN_MLA_BF16_XB
 #define IFATTN_MLA_BF16_XB 1
 #endif
-  static constexpr int STAGES = mla_rq(F) ? 3 : (C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : IFATTN_MLA_BF16_STAGES)));
+  static constexpr int STAGES = F == kFmtRq8 ? 3 : F == kFmtRq4 ? 2 : (C8 ? 2 : (SPARSE ? 3 : (B2 ? 2 : IFATTN_MLA_BF16_STAGES)));
   // 1-KiB loads per tile
   static constexpr int LOADS = TIGHT ? int((32 * MlaRow<F>::BYTES + 1023) / 1024) : 4 * MlaRow<F>::NI;
   static constexpr int SCALES = mla_rq(F) ? LOADS * 1024 : 0;  // LDS byte of the row scales
@@ -382,12 +385,12 @@ struct MlaCfg {
 // Persistent workgroups per CU of the kernel variant a call runs (the grid is
 // that many per CU, all resident at once).
 inline int wgs_mla(int fmt, bool sparse, bool wide) {
-  if (mla_rq(fmt)) return MlaCfg<kFmtRq8, false>::WGS;
+  if (fmt == kFmtRq8) return MlaCfg<kFmtRq8, false>::WGS;
+  if (fmt == kFmtRq4) return MlaCfg<kFmtRq4, false>::WGS;
   if (fmt != kFmtBf16) return sparse ? MlaCfg<kFmtC8, true>::WGS : MlaCfg<kFmtC8, false>::WGS;
   return sparse ? MlaCfg<kFmtBf16, true>::WGS
                 : (wide ? MlaCfg<kFmtBf16, false, true>::WGS : MlaCfg<kFmtBf16, false>::WGS);
 }
-static_assert(MlaCfg<kFmtRq8, false>::WGS == MlaCfg<kFmtRq4, false>::WGS, "one grid per format");
 constexpr int kMlaWgsMax = 3;  // most persistent workgroups per CU of any variant
 constexpr int64_t kMlaWideKeys = int64_t(1) << 21;
 // Wave geometry of a workgroup of NW waves: wave w owns the latent dims
