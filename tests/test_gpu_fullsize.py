@@ -1,4 +1,4 @@
-"""GPU parity at the benchmark's full sizes, on the same
+"""GPU parity at the benchmark's full sizes (and config 5 over row-quantized rows), on the same
 seeded metadata bench.py times (seed 0 of ironpangu_amd.workloads).
 
 Each test builds the whole pool on the GPU, runs the HIP path through the C
@@ -193,6 +193,41 @@ def test_config5_mla_decode_full_size(c8):
                             bs, case.scale, c8=c8, threads=THREADS)
     assert_rel_l2(bf16_host(out), exp, what=f"config-5 MLA decode ({'c8' if c8 else 'bf16'})")
     assert_close(bf16_host(out), exp, what=f"config-5 MLA decode ({'c8' if c8 else 'bf16'})")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_config5_rowq_full_size(bits):
+    """Config 5's rows and lengths over row-quantized rows (int8 or int4 codes of
+    all 576 dims, one fp32 scale per row; the bench's mla_decode_rowq lines):
+    every row against the oracle's attention over the bf16 rows
+    oracle_dequant_legacy gives for the referenced blocks (the reference's
+    dequantize-then-attend path). Codes are uniform over the whole code range
+    and scales vary per row, so every code value and a range of scales occur."""
+    import torch
+    from ironpangu_amd import ops
+    case = W.mla_meta(0)
+    nb, bs, heads = case.pool_blocks, case.block_size, case.heads
+    row_bytes = 576 * bits // 8
+    print(f"config5 rowq{bits}: {case.num_seqs} seqs, {int(case.seq_lens.sum())} tokens", flush=True)
+    g = _gen(700 + bits)
+    cache = torch.randint(0, 256, (nb, bs, row_bytes), generator=g, device="cuda", dtype=torch.uint8)
+    if bits == 8:
+        cache[cache == 128] = 129  # -128 is outside the quantizer's [-127, 127]
+    scales = torch.rand(nb * bs, generator=g, device="cuda") * 0.01 + 0.001
+    q = _randn(g, (case.num_seqs, heads, 576), std=0.5)
+    out = ops.mla_attention(q, cache, to_dev(case.block_tables), to_dev(case.seq_lens), case.max_context,
+                            scale=case.scale, row_scales=scales, bits=bits)
+    torch.cuda.synchronize()
+    used, ctab = compact_blocks(case.block_tables, case.seq_lens, bs)
+    codes = _gather_host(cache, used).reshape(-1)
+    sc = scales.view(nb, bs).index_select(0, torch.from_numpy(used).cuda()).cpu().numpy().reshape(-1)
+    del cache
+    rows = sc.size
+    deq = oracle.dequant_legacy(codes, sc, rows - 1, 576, bits).reshape(rows, 576)
+    exp = oracle.mla_attention(bits_host(q), deq, ctab, case.seq_lens, heads, bs, case.scale,
+                               threads=THREADS)
+    assert_rel_l2(bf16_host(out), exp, what=f"config-5 MLA decode (rowq{bits})")
+    assert_close(bf16_host(out), exp, what=f"config-5 MLA decode (rowq{bits})")
 
 
 def test_config3_mixed_prefill_decode_full_size():
