@@ -230,6 +230,70 @@ def test_config5_rowq_full_size(bits):
     assert_close(bf16_host(out), exp, what=f"config-5 MLA decode (rowq{bits})")
 
 
+@pytest.mark.parametrize("sparse", [False, True], ids=["window2048", "sparse2048"])
+def test_mla_sinks_bench_size(sparse):
+    """The bench's small-call MLA workloads at their size: 128 decode rows over
+    contexts U[4096, 65536], 16 heads, 128 learned sinks; bf16 rows behind a
+    2048-token window on 16-token ring pages, or packed C8 rows behind random
+    top-2048 causal candidate lists on 32-token pages. Every row against the
+    oracle; the sparse case hands the oracle a compact pool of exactly the
+    referenced rows (one row per block) with the tables remapped onto it."""
+    import torch
+    from ironpangu_amd import ops
+    from ironpangu_amd.host import WindowLayout
+    rng = np.random.default_rng(41)
+    n, heads, topk, window, ctx = 128, 16, 2048, 2048, 65536
+    bs = 32 if sparse else 16
+    lens = rng.integers(4096, 65537, n).astype(np.int32)
+    print(f"mla sinks bench size sparse={sparse}", flush=True)
+    if sparse:
+        need = (lens.astype(np.int64) + bs - 1) // bs
+        pool = int(need.sum())
+        table = W.block_tables_for(rng, lens, bs, pool, ctx // bs)
+    else:
+        lay = WindowLayout(ctx, window, 1, bs)
+        pool = n * lay.physical_pages
+        table = np.stack([lay.table(np.arange(lay.physical_pages) + s * lay.physical_pages)
+                          for s in range(n)]).astype(np.int32)
+    g = _gen(900 + int(sparse))
+    if sparse:
+        cache = torch.empty((pool, bs, 656), dtype=torch.uint8, device="cuda")
+        for r0 in range(0, pool * bs, 1 << 16):
+            m = min(1 << 16, pool * bs - r0)
+            ops.mla_cache_write_c8(_randn(g, (m, 576), std=0.5), cache,
+                                   torch.arange(r0, r0 + m, dtype=torch.int64, device="cuda"))
+        idx = np.stack([rng.permutation(int(lens[i]))[:topk] for i in range(n)]).astype(np.int32)
+    else:
+        cache = torch.empty((pool, bs, 576), dtype=torch.bfloat16, device="cuda")
+        fill_randn(cache, g, std=0.5)
+        idx = None
+    q = _randn(g, (n, heads, 576), std=0.5)
+    sk = _randn(g, (128, 576), std=0.5)
+    sv = _randn(g, (128, 512), std=0.5)
+    out = ops.mla_attention(q, cache, to_dev(table), to_dev(lens), ctx,
+                            indices=None if idx is None else to_dev(idx),
+                            window=0 if sparse else window, sink_keys=sk, sink_values=sv)
+    torch.cuda.synchronize()
+    if sparse:
+        # physical row of every candidate, then a pool of those rows alone
+        phys = table[np.arange(n)[:, None], idx // bs].astype(np.int64) * bs + idx % bs
+        rows, inv = np.unique(phys, return_inverse=True)
+        host = cache.view(-1, 656).index_select(0, torch.from_numpy(rows).cuda()).cpu().numpy()
+        ctab = np.zeros((n, ctx), np.int32)
+        ctab[np.arange(n)[:, None], idx] = inv.reshape(n, topk).astype(np.int32)
+        exp = oracle.mla_attention(bits_host(q), host, ctab, lens, heads, 1, 1.0 / np.sqrt(192.0),
+                                   c8=True, indices=idx, sink_k=bits_host(sk), sink_v=bits_host(sv),
+                                   threads=THREADS)
+    else:
+        host = bits_host(cache).reshape(-1, 576)
+        exp = oracle.mla_attention(bits_host(q), host, table, lens, heads, bs, 1.0 / np.sqrt(192.0),
+                                   window=window, sink_k=bits_host(sk), sink_v=bits_host(sv),
+                                   threads=THREADS)
+    what = "sparse top-2048" if sparse else "window 2048"
+    assert_rel_l2(bf16_host(out), exp, what=what)
+    assert_close(bf16_host(out), exp, what=what)
+
+
 def test_config3_mixed_prefill_decode_full_size():
     """Config 3: 8 prefill chunks U[64, 2048] after U[0, 8192] cached tokens plus
     192 decode rows U[256, 16384], one packed varlen call after the slot write of
