@@ -106,6 +106,20 @@ def test_gated_attention_long_context():
     _run(42, 4, 65536, (1 << 18) + 3)
 
 
+def test_gated_attention_bench_size():
+    """The bench's gated workload at its size: 64 requests over a
+    32768-position table, live lengths log-uniform [128, 32768] (mask -inf
+    beyond), rows drawn at random, with repeats, from a 2^20-row pool."""
+    print("gated bench size", flush=True)
+    rng = np.random.default_rng(77)
+    batch, context, slots = 64, 32768, 1 << 20
+    lens = W.lengths(rng, batch, 128, context, "loguniform")
+    rows = rng.integers(0, slots, (batch, context)).astype(np.int64)
+    mask = np.where(np.arange(context)[None, :] < lens[:, None], 0.0, -np.inf).astype(np.float32)
+    append = rows[np.arange(batch), lens - 1].copy()
+    _check(rng, rows, mask, append, slots)
+
+
 def test_gated_attention_all_masked_request_is_zero():
     import torch
     from ironpangu_amd import ops
