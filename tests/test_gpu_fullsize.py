@@ -294,6 +294,40 @@ def test_mla_sinks_bench_size(sparse):
     assert_close(bf16_host(out), exp, what=what)
 
 
+@pytest.mark.parametrize("shape", ["hd256", "page16"])
+def test_decode_bench_shapes_full_size(shape):
+    """The bench's other GQA decode lines at their size, every sequence against
+    the oracle: the Qwen head shape (8 q / 2 kv heads, head_dim 256, block 128)
+    and config 2's heads on the reference's 16-token bf16 pages, both over
+    config 2's 256 ragged lengths (log-uniform [128, 32768])."""
+    import torch
+    from ironpangu_amd import ops
+    lens = W.decode_meta(0, **W.CONFIGS["decode"]).seq_lens
+    if shape == "hd256":
+        hq, hd, bs = 8, 256, 128
+    else:
+        hq, hd, bs = 16, 128, 16
+    need = int(((lens.astype(np.int64) + bs - 1) // bs).sum())
+    case = W.decode_meta(0, num_seqs=256, lo=128, hi=32768, dist="loguniform", q_heads=hq, kv_heads=2,
+                         head_dim=hd, block_size=bs, pool_blocks=need + 64)
+    print(f"decode {shape}: {int(case.seq_lens.sum())} tokens", flush=True)
+    g = _gen(1100 + hd + bs)
+    kc = torch.empty((case.pool_blocks, bs, 2, hd), dtype=torch.bfloat16, device="cuda")
+    vc = torch.empty_like(kc)
+    fill_randn(kc, g)
+    fill_randn(vc, g)
+    q = _randn(g, (256, hq, hd))
+    scale = 1.0 / np.sqrt(hd)
+    out = ops.paged_decode(q, kc, vc, to_dev(case.block_tables), to_dev(case.seq_lens),
+                           case.max_context, scale)
+    torch.cuda.synchronize()
+    used, ctab = compact_blocks(case.block_tables, case.seq_lens, bs)
+    exp = oracle.paged_decode(bits_host(q), _gather_host(kc, used), _gather_host(vc, used), ctab,
+                              case.seq_lens, hq, 2, hd, bs, scale, threads=THREADS)
+    assert_rel_l2(bf16_host(out), exp, what=f"decode {shape}")
+    assert_close(bf16_host(out), exp, what=f"decode {shape}")
+
+
 def test_config3_mixed_prefill_decode_full_size():
     """Config 3: 8 prefill chunks U[64, 2048] after U[0, 8192] cached tokens plus
     192 decode rows U[256, 16384], one packed varlen call after the slot write of
