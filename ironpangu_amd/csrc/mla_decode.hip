@@ -144,8 +144,8 @@ __device__ __forceinline__ int mla_tiles(const MlaSpan &s) {
   return s.hi > s.lo ? (s.hi - s.base + kMlaTile - 1) / kMlaTile : 0;
 }
 // Work of row r in units: [row_pos, + sink_units) is its sink block (one
-// event at row_pos), then row_cost units of start, then its tiles, tile j at
-// unit first = row_pos + sink_units + row_cost + 32 j.
+// event, see mla_sink_mid), then row_cost units of start, then its tiles, tile
+// j at unit first = row_pos + sink_units + row_cost + 32 j.
 struct MlaRowWork {
   int tiles, wa, wb;  // tiles; workers of the first and last tile
   int64_t first;      // unit of tile 0
@@ -153,6 +153,14 @@ struct MlaRowWork {
 };
 __device__ __forceinline__ Shares mla_shares(const MlaParams &p, int64_t share) {
   return Shares{share, share * p.skew_pm / 1000};
+}
+// The sink block is one event, run by the worker whose share holds its middle
+// unit: a share boundary inside the block then moves at most half of its cost
+// to the neighbouring share. (Run at its first unit, a row start a few units
+// before a boundary put the whole block, about six tiles of time, on the
+// worker before it: window-2048 calls ended 8 us later on odd workers.)
+__device__ __forceinline__ int64_t mla_sink_mid(const MlaParams &p, int64_t pos) {
+  return pos + p.sink_units / 2;
 }
 __device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const MlaSpan &sp, int64_t pos,
                                                    int64_t share) {
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
       cnt = rw.slots;
       // Worker of the row's last event (its last tile, or its sink block).
       if (rw.tiles > 0) e = rw.wb;
-      else if (p.sink_units > 0) e = mla_shares(p, share).worker(pos);
+      else if (p.sink_units > 0) e = mla_shares(p, share).worker(mla_sink_mid(p, pos));
     }
     int tot;
     const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
@@ -1101,7 +1109,7 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
     const MlaRowWork rw = mla_row_work(p, sp, pos, share);
     cnt = rw.slots;
     if (rw.tiles > 0) e = rw.wb;
-    else if (p.sink_units > 0) e = mla_shares(p, share).worker(pos);
+    else if (p.sink_units > 0) e = mla_shares(p, share).worker(mla_sink_mid(p, pos));
   }
   int nslots;
   const int slot = wg_scan<false>(cnt, s_wt, &nslots) - cnt;
@@ -1164,7 +1172,7 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
     return a;
   };
   // Workgroup b walks the shares b, b + grid, ... row by row: a row's sink
-  // block is one event at its first unit, its tiles j at first + 32 j.
+  // block is one event at its middle unit, its tiles j at first + 32 j.
   if constexpr (STEP) {
     static_assert(!SPARSE && !mla_rq(F), "the fused step is a dense bf16 / C8 decode");
     // Fused decode step: before any tile is loaded, the workgroup writes the
@@ -1221,7 +1229,7 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
       const int64_t pos = self ? int64_t(s_pos[row]) : ld_const(p.row_pos + row);
       if (pos >= hi) break;
       const int slot0 = self ? mla_se_slot(s_se[row]) : ld_const(&p.row_slot[row].x);
-      if (sinks && pos >= lo) {
+      if (sinks && mla_sink_mid(p, pos) >= lo && mla_sink_mid(p, pos) < hi) {
         mla_sink_item<NW, Cfg::WGS == 1>(p, xbuf, row, slot0, w, lane);
         __syncthreads();  // every wave is done with xbuf
       }
@@ -1353,17 +1361,21 @@ struct MlaCall {
 // workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
 // 0.4225 ms with 3%, 0.4165-0.4181 ms with 6% against 0.4211-0.4216 at 3% on
 // one box, 4.5%: 0.4185, 8%: 0.4172-0.4191, 10%: 0.4200-0.4214; 0.4307 ms
-// with the opposite skew). C8 calls keep equal
-// shares (3% and 6% measured 0.5-1.5% slower), and so do sparse calls (their
-// shares are capped by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides
-// the default of dense calls.
-inline int mla_skew_pm(bool c8, bool sparse) {
+// with the opposite skew). Only the wide variant (large bf16 calls, two
+// workgroups per CU) is skewed: the one-workgroup variant of small calls runs
+// tiles at the same rate on both parities (window-2048 calls: 1.497 against
+// 1.507 us per tile), and the skew only unbalanced them (0.071-0.072 ms
+// without, 0.074-0.075 ms with). C8 calls keep equal shares (3% and 6%
+// measured 0.5-1.5% slower), and so do sparse calls (their shares are capped
+// by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides the default of
+// dense calls.
+inline int mla_skew_pm(bool c8, bool sparse, bool wide) {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_XCD_SKEW");
     const int x = e ? atoi(e) : 1000;
     return (x >= 0 && x <= 200) ? x : 1000;
   }();
-  return sparse ? 0 : (v != 1000 ? v : (c8 ? 0 : 60));
+  return sparse ? 0 : (v != 1000 ? v : (c8 || !wide ? 0 : 60));
 }
 // Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
 // share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
@@ -1377,8 +1389,10 @@ inline int mla_row_cost() {
   return v;
 }
 constexpr int kMlaSparseShare = kSparsePart - 2 * kMlaTile;
+// Units of a sink block: its tiles plus a start (the sink rows come from L2).
+constexpr int kMlaSinkStart = 64;
 inline int mla_sink_units(int n_sinks) {
-  return n_sinks > 0 ? kMlaTile * ((n_sinks + kMlaTile - 1) / kMlaTile) + mla_row_cost() : 0;
+  return n_sinks > 0 ? kMlaTile * ((n_sinks + kMlaTile - 1) / kMlaTile) + kMlaSinkStart : 0;
 }
 // Workers the workspace holds: the largest persistent grid, or for sparse
 // calls enough capped shares for rows of topk entries.
@@ -1468,7 +1482,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.row_cost = mla_row_cost();
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
-  p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse);
+  p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse, wide);
   p.max_workers = int(max_workers);
   p.grid = grid;
   // Self-planned calls: few rows, a variant with the LDS for the plan, and
