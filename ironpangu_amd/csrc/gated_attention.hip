@@ -51,7 +51,11 @@ constexpr int kPolicy = 2;
 constexpr int kKPolicy = 0;
 // Growth of a head's running max (log2 units) tolerated before rescaling.
 constexpr float kRescaleSlack = 8.0f;
-// Persistent decode waves per CU (two per SIMD: the kernel's register use).
+// Decode waves per CU in the grid. At the kernel's 267 registers one wave per
+// SIMD is resident, so four run at a time and the others start as they end;
+// a grid of four per CU (all resident) measured the same (0.1355 ms per call
+// at 64 requests over 32768 positions): the decode streams at about 6.6 TB/s
+// either way.
 constexpr int kWavesPerCu = 8;
 
 struct GatedParams {
