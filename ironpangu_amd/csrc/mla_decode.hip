@@ -45,6 +45,8 @@
 // shares, and rows with sinks, write (m, l, O) partials; a merge kernel
 // combines them with the sink partial. How many workgroups share a CU depends
 // on the variant (MlaCfg).
+#include <array>
+
 #include "common.h"
 #include "ifattn_internal.h"
 #include "mla_row_write.h"
@@ -53,6 +55,7 @@
 namespace ifattn {
 
 constexpr int kMlaWaves = 4;
+constexpr int kMlaSlotsMax = 3;  // most workgroups of one variant per CU
 constexpr int kMlaTile = 32;
 constexpr int kSparsePart = 1024;  // index-list entries per sparse partition
 
@@ -69,7 +72,7 @@ struct MlaParams {
   const uint16_t *sink_k;       // [n_sinks, 576] bf16 or null
   const uint16_t *sink_v;       // [n_sinks, 512] bf16
   uint16_t *out;                // [rows, heads, 512]
-  // Plan outputs: plan[0] = workers, plan[2..3] = share (int64 work units).
+  // Plan outputs: plan[0] = workers, plan[2..3] = total work units (int64).
   int32_t *plan;
   int64_t *row_pos;             // [rows] first work unit of each row
   int32_t *row_seq;             // [rows] sequence of each row
@@ -85,7 +88,10 @@ struct MlaParams {
   int row_cost;     // work units charged per row start
   int sink_units;   // work units of a row's sink block (0 without sinks)
   int max_share;    // largest share: sparse segments fit the kSparsePart slot list
-  int skew_pm;      // share skew between odd and even workers (Shares), permille
+  int skew_pm;      // share skew between odd and even workers (MlaShares), permille
+  int slot_n;       // dispatch slots with their own share weight (MlaShares), 1: equal shares
+  int slot_c;       // workers per dispatch slot (the CUs)
+  int slot_w[kMlaSlotsMax];  // share weight of each dispatch slot, permille
   int max_workers;  // workers the workspace holds
   int grid;         // persistent attention workgroups
   int self_plan;    // the attention workgroups plan the call themselves (no plan launch)
@@ -151,9 +157,75 @@ struct MlaRowWork {
   int64_t first;      // unit of tile 0
   int slots;          // partial slots: 1 for the sinks, then one per share the tiles touch
 };
-__device__ __forceinline__ Shares mla_shares(const MlaParams &p, int64_t share) {
-  return Shares{share, share * p.skew_pm / 1000};
+// Contiguous shares of a call's work units, one per worker, in worker order.
+// Worker v runs on workgroup v % grid; workgroups [k C, (k + 1) C) are the
+// k-th workgroup dispatched to each CU (dispatch slot k). Co-resident
+// workgroups do not progress at the same rate: the older waves of a CU win
+// instruction issue, so on the VALU-bound integer tiles a CU's first
+// workgroup ran 2.1, its second 2.5 and its third 3.0 us per tile (C8
+// config-5 rows, three per CU), and equal shares ended a third of the way
+// apart. When the workers fill the slots exactly, the workers of slot k get
+// shares in proportion to its weight; otherwise all shares are equal. Within a
+// slot, odd workers (odd XCDs) are d = s * skew_pm / 1000 units shorter than
+// even ones. The slots' shares live in a small LDS table (kMlaShareTab
+// int64s, written by one thread): kept in registers they pushed the dense C8
+// kernel's scalar registers into spills.
+constexpr int kMlaShareTab = 2 * kMlaSlotsMax + 3;  // s[3], b[4], c, ns
+__device__ __forceinline__ void mla_shares_fill(const MlaParams &p, int64_t total, int workers,
+                                                int64_t *tab) {
+  const int64_t eq = total > 0 ? (total + workers - 1) / workers : 1;
+  // Host-checked: no weight exceeds twice the mean, so a weighted share is at
+  // most 2 eq + 1 (sparse shares must fit the slot list).
+  if (p.slot_n > 1 && workers == p.slot_n * p.slot_c && 2 * eq + 1 <= p.max_share) {
+    int wsum = 0;
+    for (int k = 0; k < p.slot_n; ++k) wsum += p.slot_w[k];
+    const int64_t den = int64_t(p.slot_c) * wsum;
+    int64_t b = 0;
+    for (int k = 0; k < p.slot_n; ++k) {
+      const int64_t sk = (total * p.slot_w[k] + den - 1) / den;
+      tab[k] = sk < 1 ? 1 : sk;
+      tab[kMlaSlotsMax + k] = b;
+      b += int64_t(p.slot_c) * tab[k];
+    }
+    tab[kMlaSlotsMax + p.slot_n] = b;
+    tab[2 * kMlaSlotsMax + 1] = p.slot_c;
+    tab[2 * kMlaSlotsMax + 2] = p.slot_n;
+  } else {
+    tab[0] = eq;
+    tab[kMlaSlotsMax] = 0;
+    tab[2 * kMlaSlotsMax + 1] = workers + 1;  // one slot: lo(workers) ends the last share
+    tab[2 * kMlaSlotsMax + 2] = 1;
+  }
 }
+// TAB false: equal shares of s0 units without the table (the wide variant,
+// whose LDS is full; the host gives it no weights).
+template <bool TAB = true>
+struct MlaShares {
+  const int64_t *tab;
+  int64_t s0;
+  int skew_pm;
+  __device__ int64_t lo(int v) const {
+    if (!TAB) return int64_t(v) * s0 + ((v & 1) ? s0 * skew_pm / 1000 : 0);
+    const int c = int(tab[2 * kMlaSlotsMax + 1]);
+    const int k = v / c, i = v - k * c;
+    const int64_t s = tab[k];
+    return tab[kMlaSlotsMax + k] + int64_t(i) * s + ((i & 1) ? s * skew_pm / 1000 : 0);
+  }
+  __device__ int worker(int64_t u) const {  // the worker whose share holds unit u
+    int k = 0, c = 0;
+    int64_t s = s0, b = 0;
+    if (TAB) {
+      const int ns = int(tab[2 * kMlaSlotsMax + 2]);
+      for (int t = 1; t < ns; ++t)
+        if (u >= tab[kMlaSlotsMax + t]) k = t;
+      s = tab[k];
+      b = tab[kMlaSlotsMax + k];
+      c = int(tab[2 * kMlaSlotsMax + 1]);
+    }
+    const int64_t d = s * skew_pm / 1000, q = u - b, pair = q / (2 * s);
+    return k * c + int(2 * pair + (q - 2 * s * pair >= s + d ? 1 : 0));
+  }
+};
 // The sink block is one event, run by the worker whose share holds its middle
 // unit: a share boundary inside the block then moves at most half of its cost
 // to the neighbouring share. (Run at its first unit, a row start a few units
@@ -162,9 +234,9 @@ __device__ __forceinline__ Shares mla_shares(const MlaParams &p, int64_t share) 
 __device__ __forceinline__ int64_t mla_sink_mid(const MlaParams &p, int64_t pos) {
   return pos + p.sink_units / 2;
 }
+template <bool TAB>
 __device__ __forceinline__ MlaRowWork mla_row_work(const MlaParams &p, const MlaSpan &sp, int64_t pos,
-                                                   int64_t share) {
-  const Shares sh = mla_shares(p, share);
+                                                   const MlaShares<TAB> &sh) {
   MlaRowWork r;
   r.tiles = mla_tiles(sp);
   r.first = pos + p.sink_units + p.row_cost;
@@ -184,18 +256,16 @@ __device__ __forceinline__ int64_t mla_row_weight(const MlaParams &p, const MlaS
   const int tiles = mla_tiles(sp);
   return (tiles > 0 ? int64_t(p.row_cost) + int64_t(kMlaTile) * tiles : 0) + p.sink_units;
 }
-// Workers and share of a call of `total` units: the grid, fewer for small
-// calls (at least kMinShareUnits each), more for sparse calls whose shares
-// must fit the slot list, at most the workspace's max_workers.
-__device__ __forceinline__ void mla_split(const MlaParams &p, int64_t total, int &workers,
-                                          int64_t &share) {
+// Workers of a call of `total` units: the grid, fewer for small calls (at
+// least kMinShareUnits each), more for sparse calls whose shares must fit the
+// slot list, at most the workspace's max_workers.
+__device__ __forceinline__ int mla_split(const MlaParams &p, int64_t total) {
   const int64_t small = (total + kMinShareUnits - 1) / kMinShareUnits;
   int64_t wk = small < p.grid ? small : p.grid;
   const int64_t bound = (total + p.max_share - 1) / p.max_share;  // sparse share cap
   wk = bound > wk ? bound : wk;
   wk = wk < 1 ? 1 : (wk > p.max_workers ? p.max_workers : wk);
-  workers = int(wk);
-  share = total > 0 ? (total + wk - 1) / wk : 1;
+  return int(wk);
 }
 
 // Work split on the device (graph-safe: lengths are read at run time), the
@@ -213,7 +283,8 @@ __device__ __forceinline__ void mla_split(const MlaParams &p, int64_t total, int
 __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
   __shared__ long long s_tot64[16];
   __shared__ int s_tot32[16];
-  __shared__ long long s_pos, s_share;
+  __shared__ long long s_pos;
+  __shared__ int64_t s_tab[kMlaShareTab];
   __shared__ int s_slot, s_emax, s_workers;
   __shared__ int s_incl[1024];
   const int tid = threadIdx.x;
@@ -250,27 +321,25 @@ __global__ __launch_bounds__(1024) void mla_plan_kernel(MlaParams p) {
     __syncthreads();
   }
   if (tid == 0) {
-    int workers;
-    int64_t share;
-    mla_split(p, s_pos, workers, share);
+    const int workers = mla_split(p, s_pos);
     s_workers = workers;
-    s_share = share;
     p.plan[0] = workers;
-    *reinterpret_cast<int64_t *>(p.plan + 2) = share;
+    *reinterpret_cast<int64_t *>(p.plan + 2) = s_pos;
+    mla_shares_fill(p, s_pos, workers, s_tab);
   }
   __syncthreads();
-  const long long share = s_share;
+  const MlaShares<> sh{s_tab, 0, p.skew_pm};
   for (int base = 0; base < p.num_rows; base += 1024) {
     const int row = base + tid;
     int cnt = 0, e = -1;
     if (row < p.num_rows) {
       const int64_t pos = base == 0 ? first_pos : p.row_pos[row];
       const MlaRowWork rw =
-          mla_row_work(p, base == 0 ? first_span : mla_span(p, row, p.row_seq[row]), pos, share);
+          mla_row_work(p, base == 0 ? first_span : mla_span(p, row, p.row_seq[row]), pos, sh);
       cnt = rw.slots;
       // Worker of the row's last event (its last tile, or its sink block).
       if (rw.tiles > 0) e = rw.wb;
-      else if (p.sink_units > 0) e = mla_shares(p, share).worker(mla_sink_mid(p, pos));
+      else if (p.sink_units > 0) e = sh.worker(mla_sink_mid(p, pos));
     }
     int tot;
     const int incl = block_scan<int, false>(cnt, s_tot32, &tot);
@@ -1092,7 +1161,7 @@ __device__ __forceinline__ int wg_scan(int x, int *wt, int *total) {
 __device__ __forceinline__ int mla_se_slot(int se) { return (se >> 16) - 1; }
 __device__ __forceinline__ int mla_se_e(int se) { return (se & 0xFFFF) - 1; }
 __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, int *s_se, int *s_wt,
-                                              int &workers, int64_t &share) {
+                                              int64_t *s_tab, int &workers, int64_t &total_units) {
   const int row = threadIdx.x;
   const bool live = row < p.num_rows;
   MlaSpan sp{0, 0, 0, 0};
@@ -1103,13 +1172,17 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
   }
   int total;
   const int pos = wg_scan<false>(w, s_wt, &total) - w;
-  mla_split(p, total, workers, share);
+  workers = mla_split(p, total);
+  total_units = total;
+  if (threadIdx.x == 0) mla_shares_fill(p, total, workers, s_tab);
+  __syncthreads();
+  const MlaShares<> sh{s_tab, 0, p.skew_pm};
   int cnt = 0, e = -1;
   if (live) {
-    const MlaRowWork rw = mla_row_work(p, sp, pos, share);
+    const MlaRowWork rw = mla_row_work(p, sp, pos, sh);
     cnt = rw.slots;
     if (rw.tiles > 0) e = rw.wb;
-    else if (p.sink_units > 0) e = mla_shares(p, share).worker(mla_sink_mid(p, pos));
+    else if (p.sink_units > 0) e = sh.worker(mla_sink_mid(p, pos));
   }
   int nslots;
   const int slot = wg_scan<false>(cnt, s_wt, &nslots) - cnt;
@@ -1151,17 +1224,27 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
   static_assert(NW * 64 == kMlaSelfPlanRows, "one planned row per thread");
   constexpr int SPR = Cfg::B2 ? 1 : kMlaSelfPlanRows;
   __shared__ int s_pos[SPR], s_se[SPR], s_wt[NW];
+  __shared__ int64_t s_tab[Cfg::B2 ? 1 : kMlaShareTab];
   int workers;
-  int64_t share;
+  int64_t s0 = 0;
   const bool self = !Cfg::B2 && p.self_plan;
   if (self) {
-    mla_self_plan(p, s_pos, s_se, s_wt, workers, share);
+    int64_t total;
+    mla_self_plan(p, s_pos, s_se, s_wt, s_tab, workers, total);
   } else {
     // Plan entries through scalar loads (ld_const): vector loads here each
     // waited behind the previous item's output stores.
     workers = ld_const(p.plan);
-    share = ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
+    const int64_t total = ld_const(reinterpret_cast<const int64_t *>(p.plan + 2));
+    if constexpr (Cfg::B2) {
+      s0 = total > 0 ? (total + workers - 1) / workers : 1;
+    } else {
+      if (threadIdx.x == 0) mla_shares_fill(p, total, workers, s_tab);
+      __syncthreads();
+    }
   }
+  workers = uniform(workers);  // scalar (the self plan's scans leave it in a vector register)
+  const MlaShares<!Cfg::B2> sh{s_tab, s0, p.skew_pm};
   auto start_row = [&](int v) {
     if (!self) return int(ld_const(p.start_row + v));
     int a = 0, b = p.num_rows;  // first row whose running last-event worker reaches v
@@ -1183,7 +1266,6 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
     // then writes the rows its lanes found, one row at a time. The decode
     // rows are one per sequence, without window or sinks, so tile 0 of row r
     // sits at unit row_pos[r] + row_cost.
-    const Shares sh = mla_shares(p, share);
     for (int base = 0; base < p.num_rows; base += NW * 64) {
       const int row = base + int(threadIdx.x);
       bool mine = false;
@@ -1223,8 +1305,7 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
   }
   const int sinks = p.n_sinks > 0 ? 1 : 0;
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
-    const Shares sh = mla_shares(p, share);
-    const int64_t lo = sh.lo(v), hi = sh.lo(v + 1);
+    const int64_t lo = uniform(sh.lo(v)), hi = uniform(sh.lo(v + 1));
     for (int row = start_row(v); row < p.num_rows; ++row) {
       const int64_t pos = self ? int64_t(s_pos[row]) : ld_const(p.row_pos + row);
       if (pos >= hi) break;
@@ -1235,14 +1316,14 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
       }
       const int seq = !p.cu_q ? row : (self ? mla_seq_of(p, row) : ld_const(p.row_seq + row));
       const MlaSpan sp = mla_span(p, row, seq);
-      const MlaRowWork rw = mla_row_work(p, sp, pos, share);
+      const MlaRowWork rw = mla_row_work(p, sp, pos, sh);
       if (rw.tiles == 0) continue;
       const int64_t a = lo - rw.first, b = hi - rw.first;
-      const int j0 = a <= 0 ? 0 : int((a + kMlaTile - 1) / kMlaTile);
+      const int j0 = uniform(a <= 0 ? 0 : int((a + kMlaTile - 1) / kMlaTile));
       int j1 = b <= 0 ? 0 : int((b + kMlaTile - 1) / kMlaTile);
-      j1 = j1 < rw.tiles ? j1 : rw.tiles;
+      j1 = uniform(j1 < rw.tiles ? j1 : rw.tiles);
       if (j0 >= j1) continue;
-      const int slot = slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1;
+      const int slot = uniform(slot0 >= 0 ? slot0 + sinks + (v - rw.wa) : -1);
       mla_item<F, SPARSE, WIDE>(p, ring, xbuf, slot_list, row, sp, j0, j1, slot, w, lane);
       __syncthreads();  // every wave is done with xbuf (and the ring)
     }
@@ -1377,6 +1458,49 @@ inline int mla_skew_pm(bool c8, bool sparse, bool wide) {
   }();
   return sparse ? 0 : (v != 1000 ? v : (c8 || !wide ? 0 : 60));
 }
+// Share weights of the dispatch slots (MlaShares), permille: the k-th
+// workgroup of a CU gets a share in proportion to weight k. Dense integer
+// tiles (C8, row-quantized), measured on config-5 rows against equal shares
+// on the same box: C8 0.346-0.353 -> 0.332-0.335 ms, int4 rows 0.450-0.451 ->
+// 0.419-0.420 ms at 1400/1000/600 (1300/1000/700 and 1100/1000/900 gained
+// less); int8 rows (two per CU) 0.497-0.501 -> 0.486-0.487 ms at 1300/1000
+// and 1400/1000. Sparse calls (two per CU) showed no gain and keep equal
+// shares; the wide bf16 variant (no LDS for the table) always does.
+// IFATTN_MLA_SLOT_WEIGHTS ("w0,w1[,w2]") overrides the weights of every
+// variant but the wide one.
+inline void mla_slot_weights(MlaParams &p, int wgs, int fmt, bool sparse, bool wide) {
+  static const std::array<int, kMlaSlotsMax> env = [] {
+    std::array<int, kMlaSlotsMax> w{0, 0, 0};
+    if (const char *e = getenv("IFATTN_MLA_SLOT_WEIGHTS")) {
+      for (int k = 0; k < kMlaSlotsMax && *e; ++k) {
+        w[k] = atoi(e);
+        while (*e && *e != ',') ++e;
+        if (*e == ',') ++e;
+      }
+    }
+    return w;
+  }();
+  p.slot_n = 1;
+  p.slot_c = device_cus();
+  for (int k = 0; k < kMlaSlotsMax; ++k) p.slot_w[k] = 1000;
+  if (wgs < 2 || wgs > kMlaSlotsMax || wide) return;
+  std::array<int, kMlaSlotsMax> w{1000, 1000, 1000};
+  if (env[0] > 0)
+    w = env;
+  else if (fmt == kFmtBf16 || sparse)
+    return;
+  else
+    w = wgs == 3 ? std::array<int, kMlaSlotsMax>{1400, 1000, 600}
+                 : std::array<int, kMlaSlotsMax>{1300, 1000, 0};
+  // Malformed weights, or one above twice the mean (mla_shares_fill relies
+  // on that bound): equal shares.
+  int wsum = 0;
+  for (int k = 0; k < wgs; ++k) wsum += w[k];
+  for (int k = 0; k < wgs; ++k)
+    if (w[k] < 100 || w[k] > 10000 || int64_t(w[k]) * wgs > 2 * int64_t(wsum)) return;
+  p.slot_n = wgs;
+  for (int k = 0; k < wgs; ++k) p.slot_w[k] = w[k];
+}
 // Work units charged per row start (tunable: IFATTN_MLA_ROW_COST), and the
 // share cap of sparse calls: a share's tiles (at most share/32 + 1 of them)
 // keep their index entries within the kSparsePart slot list.
@@ -1483,6 +1607,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
   p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse, wide);
+  mla_slot_weights(p, wgs, c.fmt, sparse, wide);
   p.max_workers = int(max_workers);
   p.grid = grid;
   // Self-planned calls: few rows, a variant with the LDS for the plan, and
