@@ -173,29 +173,30 @@ struct MlaRowWork {
 constexpr int kMlaShareTab = 2 * kMlaSlotsMax + 3;  // s[3], b[4], c, ns
 __device__ __forceinline__ void mla_shares_fill(const MlaParams &p, int64_t total, int workers,
                                                 int64_t *tab) {
-  const int64_t eq = total > 0 ? (total + workers - 1) / workers : 1;
-  // Host-checked: no weight exceeds twice the mean, so a weighted share is at
-  // most 2 eq + 1 (sparse shares must fit the slot list).
-  if (p.slot_n > 1 && workers == p.slot_n * p.slot_c && 2 * eq + 1 <= p.max_share) {
+  if (p.slot_n > 1 && workers == p.slot_n * p.slot_c) {
     int wsum = 0;
     for (int k = 0; k < p.slot_n; ++k) wsum += p.slot_w[k];
     const int64_t den = int64_t(p.slot_c) * wsum;
     int64_t b = 0;
+    bool fits = true;  // sparse shares must fit the slot list
     for (int k = 0; k < p.slot_n; ++k) {
       const int64_t sk = (total * p.slot_w[k] + den - 1) / den;
       tab[k] = sk < 1 ? 1 : sk;
+      fits = fits && tab[k] <= p.max_share;
       tab[kMlaSlotsMax + k] = b;
       b += int64_t(p.slot_c) * tab[k];
     }
-    tab[kMlaSlotsMax + p.slot_n] = b;
-    tab[2 * kMlaSlotsMax + 1] = p.slot_c;
-    tab[2 * kMlaSlotsMax + 2] = p.slot_n;
-  } else {
-    tab[0] = eq;
-    tab[kMlaSlotsMax] = 0;
-    tab[2 * kMlaSlotsMax + 1] = workers + 1;  // one slot: lo(workers) ends the last share
-    tab[2 * kMlaSlotsMax + 2] = 1;
+    if (fits) {
+      tab[kMlaSlotsMax + p.slot_n] = b;
+      tab[2 * kMlaSlotsMax + 1] = p.slot_c;
+      tab[2 * kMlaSlotsMax + 2] = p.slot_n;
+      return;
+    }
   }
+  tab[0] = total > 0 ? (total + workers - 1) / workers : 1;
+  tab[kMlaSlotsMax] = 0;
+  tab[2 * kMlaSlotsMax + 1] = workers + 1;  // one slot: lo(workers) ends the last share
+  tab[2 * kMlaSlotsMax + 2] = 1;
 }
 // TAB false: equal shares of s0 units without the table (the wide variant,
 // whose LDS is full; the host gives it no weights).
@@ -1492,8 +1493,7 @@ inline void mla_slot_weights(MlaParams &p, int wgs, int fmt, bool sparse, bool w
   else
     w = wgs == 3 ? std::array<int, kMlaSlotsMax>{1400, 1000, 600}
                  : std::array<int, kMlaSlotsMax>{1300, 1000, 0};
-  // Malformed weights, or one above twice the mean (mla_shares_fill relies
-  // on that bound): equal shares.
+  // Malformed weights: equal shares.
   int wsum = 0;
   for (int k = 0; k < wgs; ++k) wsum += w[k];
   for (int k = 0; k < wgs; ++k)
