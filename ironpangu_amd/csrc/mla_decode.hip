@@ -1446,8 +1446,8 @@ struct MlaCall {
 // with the opposite skew). Only the wide variant (large bf16 calls, two
 // workgroups per CU) is skewed: the one-workgroup variant of small calls runs
 // tiles at the same rate on both parities (window-2048 calls: 1.497 against
-// 1.507 us per tile), and the skew only unbalanced them (0.071-0.072 ms
-// without, 0.074-0.075 ms with). C8 calls keep equal shares (3% and 6%
+// 1.507 us per tile), and the skew only unbalanced them (0.073-0.074 ms
+// without, 0.078-0.079 ms with, on one box). C8 calls keep equal shares (3% and 6%
 // measured 0.5-1.5% slower), and so do sparse calls (their shares are capped
 // by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides the default of
 // dense calls.
@@ -1462,11 +1462,12 @@ inline int mla_skew_pm(bool c8, bool sparse, bool wide) {
 // Share weights of the dispatch slots (MlaShares), permille: the k-th
 // workgroup of a CU gets a share in proportion to weight k. Dense integer
 // tiles (C8, row-quantized), measured on config-5 rows against equal shares
-// on the same box: C8 0.346-0.353 -> 0.332-0.335 ms, int4 rows 0.450-0.451 ->
-// 0.419-0.420 ms at 1400/1000/600 (1300/1000/700 and 1100/1000/900 gained
-// less); int8 rows (two per CU) 0.497-0.501 -> 0.486-0.487 ms at 1300/1000
-// and 1400/1000. Sparse calls (two per CU) showed no gain and keep equal
-// shares; the wide bf16 variant (no LDS for the table) always does.
+// on the same box: C8 0.334-0.335 -> 0.320-0.326 ms and int4 rows
+// 0.435-0.439 -> 0.399-0.402 ms at 1400/1000/600 (1300/1000/700 and
+// 1100/1000/900 gained less); int8 rows (two per CU) 0.480-0.503 ->
+// 0.464-0.470 ms at 1300/1000. Sparse calls (two per CU) were 2-6% slower
+// with weights and keep equal shares; the wide bf16 variant (no LDS for the
+// table) always does.
 // IFATTN_MLA_SLOT_WEIGHTS ("w0,w1[,w2]") overrides the weights of every
 // variant but the wide one.
 inline void mla_slot_weights(MlaParams &p, int wgs, int fmt, bool sparse, bool wide) {
