@@ -227,3 +227,28 @@ def test_merge_partial_counts(c8, with_sinks):
         else:
             got, exp = run(q, cache, table, kvs, maxc, cu=cu, sk=sk, sv=sv)
         assert_close(got, exp, what=f"kv {kv}")
+
+
+@pytest.mark.parametrize("rows", [300, 130])
+def test_dense_c8_weighted_shares(rows):
+    """Dense C8 decode calls large enough for the full persistent grid, where
+    each CU's three workgroups take shares weighted by dispatch order: 300 rows
+    plan through the plan launch, 130 inside the workgroups. The rows' tables
+    reuse a small pool of physical blocks (reads only), so the call is large
+    while the cache stays small; lengths straddle share boundaries at random."""
+    import torch
+    from ironpangu_amd import ops
+    print(f"dense c8 weighted shares rows={rows}", flush=True)
+    rng = np.random.default_rng(41 + rows)
+    bs, pool, heads = 64, 192, 16
+    kv = rng.integers(2000, 8000 if rows < 256 else 4000, rows).astype(np.int32)
+    kv[::17] = rng.integers(1, 300, len(kv[::17]))  # short rows inside one share
+    stride = int((kv.max() + bs - 1) // bs) + 1
+    table = rng.integers(0, pool, (rows, stride)).astype(np.int32)
+    lat = bf(rng.standard_normal((pool * bs, 576)).astype(f32) * f32(0.5))
+    cache = oracle.mla_pack_c8(lat).reshape(pool, bs, 656)
+    q = bf(rng.standard_normal((rows, heads, 576)).astype(f32) * f32(0.5))
+    out = ops.mla_decode(to_dev(q), to_dev(cache), to_dev(table), to_dev(kv), stride * bs)
+    torch.cuda.synchronize()
+    exp = oracle.mla_decode(q, cache.reshape(-1, 656), table, kv, heads, bs, SCALE, c8=True)
+    assert_close(bf16_host(out), exp)
