@@ -5,7 +5,9 @@ even ones (IFATTN_DECODE_XCD_SKEW / IFATTN_MLA_XCD_SKEW, permille of the
 share, read once per process). At the extreme setting, and with one or three
 workgroups per CU (even and odd persistent grids), every unit must still
 belong to exactly one worker, so the decode and MLA parity cases of the other
-test files are rerun in a child process with those settings.
+test files are rerun in a child process with those settings. The MLA shares
+of a CU's co-resident workgroups are also weighted by dispatch order
+(IFATTN_MLA_SLOT_WEIGHTS); one run uses the most uneven weights accepted.
 """
 import os
 import subprocess
@@ -39,14 +41,21 @@ for args in [(0, 64, False), (37, 64, True), (2500, 128, True)]:
     m.test_window_batches(*args)
 m.test_many_rows(False, True, 300)
 m.test_self_plan_row_limit(257, False)
+m.test_dense_c8_weighted_shares(300)
+m.test_dense_c8_weighted_shares(130)
+m.test_sparse_batches(2048, 32, 128)
 print("skew cases passed", flush=True)
 """
 
 
-@pytest.mark.parametrize("wgs", ["1", "3"])
-def test_extreme_skew(wgs):
+@pytest.mark.parametrize("wgs,weights", [("1", ""), ("3", ""), ("2", "1900,1000,100")])
+def test_extreme_skew(wgs, weights):
+    """The last case also gives the MLA dispatch slots the most uneven share
+    weights accepted (none above twice the mean)."""
     env = dict(os.environ, IFATTN_DECODE_XCD_SKEW="200", IFATTN_MLA_XCD_SKEW="200",
                IFATTN_DECODE_WGS_PER_CU=wgs)
+    if weights:
+        env["IFATTN_MLA_SLOT_WEIGHTS"] = weights
     r = subprocess.run([sys.executable, "-c", CASES.format(tests=str(TESTS))], env=env,
                        capture_output=True, text=True, timeout=200)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
