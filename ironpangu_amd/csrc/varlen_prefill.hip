@@ -19,9 +19,9 @@
 //    columns, so all G heads of a kv head reuse every K/V tile. Each wave owns
 //    2 column blocks of 16 (1 for head_dim 256).
 //  * K/V 32-token tiles are copied HBM -> LDS with direct-to-LDS buffer loads
-//    into a ring of 3 steps of two tiles each (16-B chunks XOR-swizzled by a
-//    row key), two steps ahead; a loop step waits, synchronises and runs the
-//    softmax bookkeeping once per 64 keys. QK^T runs transposed (tokens in M,
+//    into a ring of steps of four tiles (16-B chunks XOR-swizzled by a row
+//    key; two steps at head_dim 128, one in flight); a loop step waits,
+//    synchronises and runs the softmax bookkeeping once per 128 keys. QK^T runs transposed (tokens in M,
 //    columns in N) so the score tile is already the B operand of the PV MFMA;
 //    V^T operands come from transposing LDS reads. The two waves of a SIMD
 //    overlap one's MFMAs with the other's softmax.
@@ -130,13 +130,16 @@ __device__ __forceinline__ int pf_tile_token(int g, int j) {
 #define IFATTN_PF_STAGES 3
 #endif
 // 32-key tiles per loop step: the per-step costs (wait, barrier, row max,
-// rescale check) are paid once per 64 keys where the ring has room for it.
+// rescale check) are paid once per 128 keys. At head_dim 128 the ring then
+// holds two steps (one being read, one in flight, 128 KiB): config-3 chunks
+// 0.2951-0.2989 -> 0.2839-0.2890 ms against two tiles per step in three
+// steps (three tiles in two steps: 0.2871-0.2880 ms).
 #ifndef IFATTN_PF_KT
-#define IFATTN_PF_KT 2
+#define IFATTN_PF_KT 4
 #endif
 constexpr int prefill_kt(int d) { return d <= 128 ? IFATTN_PF_KT : 1; }
 // Ring depth in steps: up to 128 KiB of staged tiles (16 KiB per tile at
-// head_dim 128). Three steps (one being read, two in flight) measured best.
+// head_dim 128), at most three steps (one being read, two in flight).
 constexpr int prefill_stages(int d) {
   return IFATTN_PF_STAGES * prefill_kt(d) * 4 * 32 * d <= 131072
              ? IFATTN_PF_STAGES
