@@ -1462,10 +1462,13 @@ inline int mla_skew_pm(bool c8, bool sparse, bool wide) {
 // Share weights of the dispatch slots (MlaShares), permille: the k-th
 // workgroup of a CU gets a share in proportion to weight k. Dense integer
 // tiles (C8, row-quantized), measured on config-5 rows against equal shares
-// on the same box: C8 0.334-0.335 -> 0.320-0.326 ms and int4 rows
-// 0.435-0.439 -> 0.399-0.402 ms at 1400/1000/600 (1300/1000/700 and
-// 1100/1000/900 gained less); int8 rows (two per CU) 0.480-0.503 ->
-// 0.464-0.470 ms at 1300/1000. Sparse calls (two per CU) were 2-6% slower
+// on the same box: C8 0.334-0.335 -> 0.320-0.326 ms at 1400/1000/600
+// (1100/1000/900 and 1300/1000/700 gained less; 1500/1000/500 and
+// 1600/1000/400 measured 0.334-0.343 against 0.328 ms on a later box), int4
+// rows 0.435-0.439 -> 0.399-0.402 ms at 1400/1000/600, and 0.409-0.411 ->
+// 0.400-0.402 ms from 1400/1000/600 to 1500/1000/500 on the later box; int8
+// rows (two per CU) 0.480-0.503 -> 0.464-0.470 ms at 1300/1000, and
+// 0.469-0.479 -> 0.467-0.468 ms at 1500/1000 on the later box. Sparse calls (two per CU) were 2-6% slower
 // with weights and keep equal shares; the wide bf16 variant (no LDS for the
 // table) always does.
 // IFATTN_MLA_SLOT_WEIGHTS ("w0,w1[,w2]") overrides the weights of every
@@ -1491,9 +1494,11 @@ inline void mla_slot_weights(MlaParams &p, int wgs, int fmt, bool sparse, bool w
     w = env;
   else if (fmt == kFmtBf16 || sparse)
     return;
+  else if (fmt == kFmtC8)
+    w = std::array<int, kMlaSlotsMax>{1400, 1000, 600};
   else
-    w = wgs == 3 ? std::array<int, kMlaSlotsMax>{1400, 1000, 600}
-                 : std::array<int, kMlaSlotsMax>{1300, 1000, 0};
+    w = wgs == 3 ? std::array<int, kMlaSlotsMax>{1500, 1000, 500}
+                 : std::array<int, kMlaSlotsMax>{1500, 1000, 0};
   // Malformed weights: equal shares.
   int wsum = 0;
   for (int k = 0; k < wgs; ++k) wsum += w[k];
