@@ -421,10 +421,12 @@ struct MlaCfg {
   // one score buffer 74 us. Row-quantized slots end with the tile's 32 row
   // scales (256 bytes: the direct-to-LDS scale load writes a dword per lane).
   static constexpr bool TIGHT = C8 && !SPARSE;
-  // Large dense bf16 calls (WIDE) run two workgroups per CU, each with a
-  // 2-slot ring and one score buffer (exactly 160 KiB): config-5 decode 507-510
-  // -> 489-491 us. Small calls keep one workgroup with a 4-slot ring (window
-  // 2048 over 128 rows: 79 against 83 us with two).
+  // Dense bf16 calls of at least 2^18 keys (WIDE) run two workgroups per CU,
+  // each with a 2-slot ring and one score buffer (exactly 160 KiB): config-5
+  // decode 507-510 -> 489-491 us; window 2048 over 128 rows (sinks included:
+  // while one workgroup runs a sink block, the other keeps streaming)
+  // 0.0735-0.0773 -> 0.0716-0.0753 ms. Smaller calls keep one workgroup with a
+  // 4-slot ring and plan for themselves.
   static constexpr bool B2 = !C8 && !SPARSE && WIDE;
   // Row-quantized int8 tiles run two workgroups with 3-slot rings: their
   // gather addressing, bf16 dequantization and the rope codes' extra MFMAs
@@ -470,7 +472,7 @@ inline int wgs_mla(int fmt, bool sparse, bool wide) {
                 : (wide ? MlaCfg<kFmtBf16, false, true>::WGS : MlaCfg<kFmtBf16, false>::WGS);
 }
 constexpr int kMlaWgsMax = 3;  // most persistent workgroups per CU of any variant
-constexpr int64_t kMlaWideKeys = int64_t(1) << 21;
+constexpr int64_t kMlaWideKeys = int64_t(1) << 18;
 // Wave geometry of a workgroup of NW waves: wave w owns the latent dims
 // [DPW w, DPW w + DPW) for QK^T and PV (KS k-steps of 32), waves 0 and 1 add
 // 32 rope dims each; a lane holds EPL dims of each of its eight V tokens and
@@ -1443,21 +1445,23 @@ struct MlaCall {
 // workers run on odd XCDs, whose tiles are slower (config-5 rows 0.4257 ->
 // 0.4225 ms with 3%, 0.4165-0.4181 ms with 6% against 0.4211-0.4216 at 3% on
 // one box, 4.5%: 0.4185, 8%: 0.4172-0.4191, 10%: 0.4200-0.4214; 0.4307 ms
-// with the opposite skew). Only the wide variant (large bf16 calls, two
-// workgroups per CU) is skewed: the one-workgroup variant of small calls runs
+// with the opposite skew). Only the wide variant (two workgroups per CU)
+// without sinks is skewed: the one-workgroup variant of small calls runs
 // tiles at the same rate on both parities (window-2048 calls: 1.497 against
 // 1.507 us per tile), and the skew only unbalanced them (0.073-0.074 ms
-// without, 0.078-0.079 ms with, on one box). C8 calls keep equal shares (3% and 6%
+// without, 0.078-0.079 ms with, on one box); with sinks the even workers also
+// hold the sink blocks (window 2048 in the wide variant: 0.0701-0.0713 ms at
+// 0 and 3%, 0.0737-0.0751 ms at 6%). C8 calls keep equal shares (3% and 6%
 // measured 0.5-1.5% slower), and so do sparse calls (their shares are capped
 // by the slot list). IFATTN_MLA_XCD_SKEW (0..200) overrides the default of
 // dense calls.
-inline int mla_skew_pm(bool c8, bool sparse, bool wide) {
+inline int mla_skew_pm(bool c8, bool sparse, bool wide, bool sinks) {
   static const int v = [] {
     const char *e = getenv("IFATTN_MLA_XCD_SKEW");
     const int x = e ? atoi(e) : 1000;
     return (x >= 0 && x <= 200) ? x : 1000;
   }();
-  return sparse ? 0 : (v != 1000 ? v : (c8 || !wide ? 0 : 60));
+  return sparse ? 0 : (v != 1000 ? v : (c8 || !wide || sinks ? 0 : 60));
 }
 // Share weights of the dispatch slots (MlaShares), permille: the k-th
 // workgroup of a CU gets a share in proportion to weight k. Dense integer
@@ -1612,7 +1616,7 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   p.row_cost = mla_row_cost();
   p.sink_units = mla_sink_units(c.n_sinks);
   p.max_share = sparse ? kMlaSparseShare : 0x7FFFFFFF;
-  p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse, wide);
+  p.skew_pm = mla_skew_pm(c.fmt != kFmtBf16, sparse, wide, c.n_sinks > 0);
   mla_slot_weights(p, wgs, c.fmt, sparse, wide);
   p.max_workers = int(max_workers);
   p.grid = grid;
