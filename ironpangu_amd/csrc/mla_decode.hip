@@ -1205,6 +1205,63 @@ __device__ __forceinline__ void mla_self_plan(const MlaParams &p, int *s_pos, in
   __syncthreads();
 }
 
+// The same plan for the wide layout, whose LDS holds no per-row arrays: every
+// workgroup computes it and stores each row's first unit and partial slots
+// into the plan arrays the plan launch would write (row_pos, row_slot). Every
+// workgroup writes the same values, and each reads them back only after its
+// own stores (program order and the workgroup barrier), so whichever store a
+// read returns carries this call's value. `scratch` (the score buffer, unused
+// until the first tile) holds the scans' wave totals, the rows' running
+// last-event workers and the start row of this workgroup's worker, which is
+// returned (workers <= grid for dense calls: one worker per workgroup).
+__device__ __forceinline__ int mla_self_plan_global(const MlaParams &p, int *scratch, int &workers,
+                                                    int64_t &total_units) {
+  int *s_wt = scratch, *s_e = scratch + 8, *s_start = scratch + 4;
+  const int row = threadIdx.x;
+  const bool live = row < p.num_rows;
+  MlaSpan sp{0, 0, 0, 0};
+  int w = 0;
+  if (live) {
+    sp = mla_span(p, row, mla_seq_of(p, row));
+    w = int(mla_row_weight(p, sp));
+  }
+  if (row == 0) *s_start = p.num_rows;
+  int total;
+  const int pos = wg_scan<false>(w, s_wt, &total) - w;
+  workers = mla_split(p, total);
+  total_units = total;
+  const MlaShares<false> sh{nullptr, total > 0 ? (int64_t(total) + workers - 1) / workers : 1, p.skew_pm};
+  int cnt = 0, e = -1;
+  if (live) {
+    const MlaRowWork rw = mla_row_work(p, sp, pos, sh);
+    cnt = rw.slots;
+    if (rw.tiles > 0) e = rw.wb;
+    else if (p.sink_units > 0) e = sh.worker(mla_sink_mid(p, pos));
+  }
+  int nslots;
+  const int slot = wg_scan<false>(cnt, s_wt, &nslots) - cnt;
+  int emax;
+  const int einc = wg_scan<true>(e, s_wt, &emax);
+  if (live) {
+    s_e[row] = einc;
+    p.row_pos[row] = pos;
+    p.row_slot[row] = make_int2(cnt > 0 ? slot : -1, cnt);
+    if (blockIdx.x == 0 && w == 0) {  // no keys and no sinks: defined zero output
+      uint16_t *o = p.out + int64_t(row) * p.heads * 512;
+      for (int i = 0; i < p.heads * 512; i += 8) store_u32x4(o + i, u32x4{0, 0, 0, 0});
+    }
+  }
+  __syncthreads();
+  // Start row of worker v = blockIdx.x: the first row whose running
+  // last-event worker reaches v.
+  const int v = int(blockIdx.x);
+  if (live && einc >= v && (row == 0 || s_e[row - 1] < v)) *s_start = row;
+  __syncthreads();
+  const int start = *s_start;
+  __syncthreads();  // the scratch is the score buffer from here on
+  return start;
+}
+
 // STEP: the fused decode step (mla_step_kernel); the plain calls run kernels
 // without its row writes and its kernel argument.
 template <int F, bool SPARSE, bool WIDE, bool STEP>
@@ -1231,9 +1288,14 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
   int workers;
   int64_t s0 = 0;
   const bool self = !Cfg::B2 && p.self_plan;
+  int g_start = 0;  // wide layout planned in the kernel: this workgroup's start row
   if (self) {
     int64_t total;
     mla_self_plan(p, s_pos, s_se, s_wt, s_tab, workers, total);
+  } else if (Cfg::B2 && p.self_plan) {
+    int64_t total;
+    g_start = mla_self_plan_global(p, reinterpret_cast<int *>(&xbuf[0][0]), workers, total);
+    s0 = total > 0 ? (total + workers - 1) / workers : 1;
   } else {
     // Plan entries through scalar loads (ld_const): vector loads here each
     // waited behind the previous item's output stores.
@@ -1248,7 +1310,11 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
   }
   workers = uniform(workers);  // scalar (the self plan's scans leave it in a vector register)
   const MlaShares<!Cfg::B2> sh{s_tab, s0, p.skew_pm};
+  // Plan arrays written by this kernel (the wide layout's in-kernel plan) are
+  // read with ordinary loads: the scalar constant path may not see them.
+  const bool gplan = Cfg::B2 && p.self_plan;
   auto start_row = [&](int v) {
+    if (gplan) return g_start;
     if (!self) return int(ld_const(p.start_row + v));
     int a = 0, b = p.num_rows;  // first row whose running last-event worker reaches v
     while (a < b) {
@@ -1310,14 +1376,15 @@ __device__ __forceinline__ void mla_attention_body(const MlaParams &p, const Mla
   for (int v = blockIdx.x; v < workers; v += gridDim.x) {
     const int64_t lo = uniform(sh.lo(v)), hi = uniform(sh.lo(v + 1));
     for (int row = start_row(v); row < p.num_rows; ++row) {
-      const int64_t pos = self ? int64_t(s_pos[row]) : ld_const(p.row_pos + row);
+      const int64_t pos = self ? int64_t(s_pos[row]) : (gplan ? p.row_pos[row] : ld_const(p.row_pos + row));
       if (pos >= hi) break;
-      const int slot0 = self ? mla_se_slot(s_se[row]) : ld_const(&p.row_slot[row].x);
+      const int slot0 =
+          self ? mla_se_slot(s_se[row]) : (gplan ? p.row_slot[row].x : ld_const(&p.row_slot[row].x));
       if (sinks && mla_sink_mid(p, pos) >= lo && mla_sink_mid(p, pos) < hi) {
         mla_sink_item<NW, Cfg::WGS == 1>(p, xbuf, row, slot0, w, lane);
         __syncthreads();  // every wave is done with xbuf
       }
-      const int seq = !p.cu_q ? row : (self ? mla_seq_of(p, row) : ld_const(p.row_seq + row));
+      const int seq = !p.cu_q ? row : (self || gplan ? mla_seq_of(p, row) : ld_const(p.row_seq + row));
       const MlaSpan sp = mla_span(p, row, seq);
       const MlaRowWork rw = mla_row_work(p, sp, pos, sh);
       if (rw.tiles == 0) continue;
@@ -1620,9 +1687,9 @@ int32_t mla_run(const MlaCall &c, const char *what) {
   mla_slot_weights(p, wgs, c.fmt, sparse, wide);
   p.max_workers = int(max_workers);
   p.grid = grid;
-  // Self-planned calls: few rows, a variant with the LDS for the plan, and
-  // every prefix of row units within 32 bits.
-  p.self_plan = !wide && c.num_rows <= kMlaSelfPlanRows &&
+  // Self-planned calls: few rows and every prefix of row units within 32
+  // bits (the wide layout plans into the plan arrays instead of LDS).
+  p.self_plan = c.num_rows <= kMlaSelfPlanRows &&
                 int64_t(c.num_rows) * (int64_t(c.max_context) + p.row_cost + p.sink_units + kMlaTile) <
                     (int64_t(1) << 31) &&
                 2 * max_workers + uint64_t(c.num_rows) < 0xFFFFu;
