@@ -21,10 +21,11 @@
 // sparse rows read the logical positions of their index list
 // (min(causal, topk) candidates, -1 padding; openpangu_attention_metadata.h:13-33).
 //
-// Decomposition: the plan kernel cuts the call's work (rows weighted by their
-// key tiles, a start cost and their sink block) into equal contiguous shares,
-// one per persistent workgroup of four waves, which walks its share row by
-// row. A share's 32-token tiles are copied HBM -> LDS once by direct-to-LDS
+// Decomposition: the plan (a plan launch, or for calls of at most 256 rows
+// every attention workgroup itself) cuts the call's work (rows weighted by
+// their key tiles, a start cost and their sink block) into contiguous shares,
+// one per persistent workgroup of four waves (equal, or weighted by the
+// workgroup's dispatch order on the CU), which walks its share row by row. A share's 32-token tiles are copied HBM -> LDS once by direct-to-LDS
 // loads (dense: 32 consecutive rows of one
 // block; sparse: a gather of 32 rows named by the index list) through a ring
 // of slots; wave w then owns latent dims [128w, 128w+128) for QK^T and PV (K
