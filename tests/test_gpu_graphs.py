@@ -85,6 +85,38 @@ def test_graph_mla_window_and_sparse():
                                                           indices=idx, sink_keys=sk, sink_values=sv))
 
 
+def test_graph_mla_wide_layout():
+    """A dense bf16 call with at least 2^18 possible keys (rows x max_context)
+    runs the two-workgroup layout, whose workgroups write the plan into the
+    workspace themselves: replays with new lengths equal eager calls."""
+    import torch
+    from ironpangu_amd import ops
+    rng = np.random.default_rng(37)
+    bs, nb, heads, maxc = 32, 96, 6, 65536
+    lens = np.array([700, 1500, 40], np.int32)
+    assert 5 * maxc >= 1 << 18
+    table = torch.from_numpy(rng.integers(0, nb, (3, maxc // bs)).astype(np.int32)).cuda()
+    cache = to_dev(W.bf16_randn(rng, (nb * bs, 576), std=0.5)).view(nb, bs, 576)
+    q = to_dev(W.bf16_randn(rng, (5, heads, 576), std=0.5))
+    cu = torch.tensor([0, 2, 4, 5], dtype=torch.int32, device="cuda")
+    kv = torch.from_numpy(lens).cuda()
+    sk, sv = to_dev(W.bf16_randn(rng, (128, 576))), to_dev(W.bf16_randn(rng, (128, 512)))
+
+    def set_meta(i):
+        kv.copy_(torch.from_numpy(lens + 301 * i))
+
+    ws = torch.empty(int(ops.lib().ifattn_mla_attention_workspace_size(5, heads, maxc, 0, 0, 128, bs)),
+                     dtype=torch.uint8, device="cuda")
+    out = torch.empty((5, heads, 512), dtype=torch.bfloat16, device="cuda")
+
+    def call():
+        return ops.mla_attention(q, cache, table, kv, maxc, cu_seqlens=cu, sink_keys=sk, sink_values=sv,
+                                 out=out, workspace=ws)
+
+    _replays(call, set_meta, lambda: ops.mla_attention(q, cache, table, kv, maxc, cu_seqlens=cu,
+                                                        sink_keys=sk, sink_values=sv))
+
+
 def test_graph_varlen_prefill():
     import torch
     from ironpangu_amd import ops
