@@ -256,3 +256,23 @@ def test_dense_c8_weighted_shares(rows):
     torch.cuda.synchronize()
     exp = oracle.mla_decode(q, cache.reshape(-1, 656), table, kv, heads, bs, SCALE, c8=True)
     assert_close(bf16_host(out), exp)
+
+
+@pytest.mark.parametrize("with_sinks", [False, True])
+def test_wide_layout_in_kernel_plan(with_sinks):
+    """Dense bf16 calls of at most 256 rows in the two-workgroup layout (rows x
+    max_context >= 2^18) plan inside the attention workgroups, into the plan
+    arrays: packed multi-row sequences, rows without keys, rows over several
+    shares, with and without sinks, against the oracle."""
+    print(f"wide in-kernel plan sinks={with_sinks}", flush=True)
+    rng = np.random.default_rng(53 + with_sinks)
+    counts = [1] * 30 + [3, 2, 4]
+    kv = rng.integers(0, 700, len(counts)).astype(np.int32)
+    kv[::7] = 0                                                   # rows without keys
+    kv[3::9] = rng.integers(4000, 7000, len(kv[3::9]))           # rows over several shares
+    kv[-3:] = [5000, 900, 6100]
+    q, cache, table, kv, cu, maxc = batch(61, counts, kv, 64, 16, False)
+    assert int(sum(counts)) * maxc >= 1 << 18 and int(sum(counts)) <= 256
+    sk, sv = sinks(128, 62) if with_sinks else (None, None)
+    got, exp = run(q, cache, table, kv, maxc, cu=cu, sk=sk, sv=sv)
+    assert_close(got, exp)
