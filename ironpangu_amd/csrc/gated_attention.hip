@@ -13,11 +13,12 @@
 // product. Accumulation is fp32 (scores, softmax, PV); the reference rounds
 // scores and probabilities to bf16 between its ACLNN calls.
 //
-// Launches (one stream): plan (one workgroup per request appends the step's
-// rows and lists the partitions of 64/128/256 positions holding a position
-// whose mask is not -inf); decode (persistent waves, eight per CU, take the live
-// (partition, kv head) items round-robin); merge (per request and head, the
-// live partitions' (m, l, O), normalised and gated). A one-partition context
+// Launches (one stream): plan (four workgroups per request, each over a
+// quarter of its partitions of 64/128/256 positions, list the partitions
+// holding a position whose mask is not -inf; the first also appends the step's
+// rows); decode (persistent waves, eight per CU, take the live (partition, kv
+// head) items round-robin); merge (per request and head, the live partitions'
+// (m, l, O), normalised and gated). A one-partition context
 // runs an append launch in place of the plan, and no merge.
 //
 // Decode item: the wave loads the partition's (mask, index) pairs and compacts
@@ -67,7 +68,7 @@ struct GatedParams {
   float *part_o;   // [batch, parts, heads, D]
   float *part_ml;  // [batch, parts, heads, 2]
   int32_t *live_parts;  // [batch, parts]: each request's partitions with a live position
-  int32_t *live_count;  // [batch]; both null for a one-partition context
+  int32_t *live_count;  // [batch, kPlanSplit] (per chunk of partitions); both null for a one-partition context
   // The step's rows (appended by the plan kernel when there is one).
   const uint8_t *k_new, *v_new;
   const int64_t *append;
@@ -85,9 +86,10 @@ __device__ __forceinline__ u32x4 row_ror8(u32x4 v) {
   return r;
 }
 
-// One (request b, kv head kvh, partition part) item; s_row / s_mask hold the
-// wave's list of live positions.
-__device__ __forceinline__ void gated_item(const GatedParams &p, int part, int kvh, int b,
+// One (request b, kv head kvh, partition part) item, whose partials go to row
+// `slot` of the request's partials (the partition's place in the request's
+// live list); s_row / s_mask hold the wave's list of live positions.
+__device__ __forceinline__ void gated_item(const GatedParams &p, int part, int slot, int kvh, int b,
                                            uint32_t *s_row, float *s_mask) {
   const int lane = threadIdx.x, c = lane & 15, g = lane >> 4;
   const bool head_live = c < kGroup;
@@ -246,7 +248,7 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int k
       }
     }
   } else {
-    const int64_t prow = (int64_t(b) * p.parts + part) * kHeads + head;
+    const int64_t prow = (int64_t(b) * p.parts + slot) * kHeads + head;
     if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
     // Written even without a live row (zeros, m = -inf): the merge loads every
     // listed partition's O alongside its (m, l).
@@ -260,50 +262,71 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int k
   }
 }
 
-// Live partitions of each request: workgroup b scans mask row b (1024 threads,
-// up to 32 positions each in flight) and lists, in order, the partitions with
-// at least one position whose mask is not -inf.
+// Live partitions of each request, in kPlanSplit chunks of pc = ceil(parts /
+// kPlanSplit) partitions: workgroup (b, c) scans chunk c of mask row b
+// (kPlanThreads threads, up to 32 positions each in flight) and lists, in
+// order, the chunk's partitions with at least one position whose mask is not
+// -inf at live_parts[b][c pc ..], their number at live_count[b][c]. Request
+// b's list is the concatenation of its chunks' lists. One workgroup per
+// request read its 128 KiB of mask at a CU's bandwidth: 6.7 us per call at 64
+// requests over 32768 positions.
+#ifndef IFATTN_GATED_PLAN_SPLIT
+#define IFATTN_GATED_PLAN_SPLIT 4
+#endif
+constexpr int kPlanSplit = IFATTN_GATED_PLAN_SPLIT;
+constexpr int kPlanThreads = 1024 / kPlanSplit;
 constexpr int kMaxParts = 262144 / kMinPart;
-__global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
-  __shared__ uint32_t s_flag[kMaxParts];
-  __shared__ int s_wave[16];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // Append request b's step row (K by threads 0-63, V by 64-127, 16 B each)
-  // before the decode launch reads the caches.
-  if (tid < 2 * (kRowBytes / 16)) {
+__host__ __device__ __forceinline__ int plan_chunk(int parts) {
+  return (parts + kPlanSplit - 1) / kPlanSplit;
+}
+__global__ __launch_bounds__(kPlanThreads) void gated_plan_kernel(GatedParams p) {
+  constexpr int NW = kPlanThreads / 64;
+  __shared__ uint32_t s_flag[kMaxParts / kPlanSplit + 1];
+  __shared__ int s_wave[NW];
+  const int b = blockIdx.x / kPlanSplit, c = blockIdx.x % kPlanSplit;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // Append request b's step row (K as 16-B pieces 0-63, V as 64-127) before
+  // the decode launch reads the caches.
+  for (int i = tid; c == 0 && i < 2 * (kRowBytes / 16); i += kPlanThreads) {
     const int64_t slot = p.append[b];
-    const bool val = tid >= kRowBytes / 16;
-    const int c = val ? tid - kRowBytes / 16 : tid;
+    const bool val = i >= kRowBytes / 16;
+    const int cc = val ? i - kRowBytes / 16 : i;
     if (slot >= 0 && slot < p.slots)
-      store_u32x4((val ? p.values_out : p.keys_out) + (slot * (kRowBytes / 16) + c) * 16,
-                  load_u32x4((val ? p.v_new : p.k_new) + (int64_t(b) * (kRowBytes / 16) + c) * 16));
+      store_u32x4((val ? p.values_out : p.keys_out) + (slot * (kRowBytes / 16) + cc) * 16,
+                  load_u32x4((val ? p.v_new : p.k_new) + (int64_t(b) * (kRowBytes / 16) + cc) * 16));
   }
-  for (int i = tid; i < p.parts; i += 1024) s_flag[i] = 0u;
+  const int pc = plan_chunk(p.parts);
+  const int p0 = c * pc;
+  const int np = p.parts - p0 < pc ? (p.parts - p0 > 0 ? p.parts - p0 : 0) : pc;
+  const int t_beg = p0 * p.part;
+  const int t_len = np == 0 ? 0 : (p.context - t_beg < np * p.part ? p.context - t_beg : np * p.part);
+  for (int i = tid; i < np; i += kPlanThreads) s_flag[i] = 0u;
   __syncthreads();
   // Unconditional 16-byte buffer loads, four positions a lane (zeros past the
-  // row; the position test comes after the load), so all U loads of a thread
-  // are in flight together: a quarter of the load instructions of one
+  // chunk; the position test comes after the load), so all U loads of a
+  // thread are in flight together: a quarter of the load instructions of one
   // position a lane.
-  const auto rm = make_rsrc(p.mask + int64_t(b) * p.context, uint32_t(p.context) * 4u);
+  const auto rm = make_rsrc(p.mask + int64_t(b) * p.context + t_beg, uint32_t(t_len) * 4u);
   constexpr int U = 8;
+  constexpr int kRound = kPlanThreads * 4;  // positions per load row
   const int lanes_per_part = p.part >> 2;  // 16, 32 or 64 lanes cover a partition
-  for (int t0 = 0; t0 < p.context; t0 += U * 4096) {
+  for (int t0 = 0; t0 < t_len; t0 += U * kRound) {
     u32x4 x[U];
 #pragma unroll
-    for (int e = 0; e < U; ++e) x[e] = buf_load_x4(rm, uint32_t(t0 + e * 4096 + tid * 4) * 4u);
-    // A wave's 256 positions hold 256 / part whole partitions (partitions are
-    // 64-aligned multiples of 64): lane 0 stores their flags from the ballot,
-    // not one store per lane (same-address LDS stores from many lanes
-    // serialise).
+    for (int e = 0; e < U; ++e) x[e] = buf_load_x4(rm, uint32_t(t0 + e * kRound + tid * 4) * 4u);
+    // A wave's 256 positions hold 256 / part whole partitions (chunks and
+    // partitions are 64-aligned multiples of 64): lane 0 stores their flags
+    // from the ballot, not one store per lane (same-address LDS stores from
+    // many lanes serialise).
 #pragma unroll
     for (int e = 0; e < U; ++e) {
-      const int tb = t0 + e * 4096 + tid * 4;
+      const int tb = t0 + e * kRound + tid * 4;
       bool live = false;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) live |= tb + j < p.context && __uint_as_float(x[e][j]) != -INFINITY;
+      for (int j = 0; j < 4; ++j) live |= tb + j < t_len && __uint_as_float(x[e][j]) != -INFINITY;
       const uint64_t bal = __ballot(live);
       if (lane == 0 && bal != 0) {
-        const int wbase = t0 + e * 4096 + w * 256;
+        const int wbase = t0 + e * kRound + w * 256;
         for (int q = 0; q < 64; q += lanes_per_part) {
           const uint64_t m = lanes_per_part == 64 ? ~uint64_t(0) : ((uint64_t(1) << lanes_per_part) - 1) << q;
           if (bal & m) s_flag[(wbase + 4 * q) >> p.part_shift] = 1u;
@@ -312,24 +335,38 @@ __global__ __launch_bounds__(1024) void gated_plan_kernel(GatedParams p) {
     }
   }
   __syncthreads();
-  // Compaction in partition order: wave w owns partitions 64w + 1024r + lane.
+  // Compaction in partition order: wave w owns chunk partitions 64w + kPlanThreads r + lane.
   int base = 0;
-  for (int r0 = 0; r0 < p.parts; r0 += 1024) {
+  int32_t *list = p.live_parts + int64_t(b) * p.parts + p0;
+  for (int r0 = 0; r0 < np; r0 += kPlanThreads) {
     const int i = r0 + tid;
-    const bool live = i < p.parts && s_flag[i] != 0u;
+    const bool live = i < np && s_flag[i] != 0u;
     const uint64_t ballot = __ballot(live);
     if (lane == 0) s_wave[w] = __popcll(ballot);
     __syncthreads();
     int before = base;
     for (int u = 0; u < w; ++u) before += s_wave[u];
     if (live)
-      p.live_parts[int64_t(b) * p.parts + before +
-                   __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
-                                             __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u))] = i;
-    for (int u = 0; u < 16; ++u) base += s_wave[u];
+      list[before + __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                              __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u))] = p0 + i;
+    for (int u = 0; u < NW; ++u) base += s_wave[u];
     __syncthreads();
   }
-  if (tid == 0) p.live_count[b] = base;
+  if (tid == 0) p.live_count[b * kPlanSplit + c] = base;
+}
+
+// Position in request b's list row of its k-th live partition, given its
+// chunks' counts n[0 .. kPlanSplit).
+__device__ __forceinline__ int live_slot(int k, const int *n, int pc) {
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < kPlanSplit - 1; ++u) {
+    if (k >= n[u] && c == u) {
+      k -= n[u];
+      c = u + 1;
+    }
+  }
+  return c * pc + k;
 }
 
 // Persistent waves (kWavesPerCu per CU) over the live items: item k is kv head
@@ -345,12 +382,19 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
   __shared__ uint32_t s_row[kPart];
   __shared__ float s_mask[kPart];
   if (!p.live_parts) {
-    gated_item(p, 0, int(blockIdx.x) % kKvHeads, int(blockIdx.x) / kKvHeads, s_row, s_mask);
+    gated_item(p, 0, 0, int(blockIdx.x) % kKvHeads, int(blockIdx.x) / kKvHeads, s_row, s_mask);
     return;
   }
   const int lane = threadIdx.x;
-  // Inclusive prefix of the live counts over requests (lane b = request b).
-  const int cnt = lane < p.batch ? p.live_count[lane] : 0;
+  // Inclusive prefix of the live counts over requests (lane b = request b,
+  // holding its chunks' counts).
+  int nc[kPlanSplit];
+#pragma unroll
+  for (int u = 0; u < kPlanSplit; ++u) nc[u] = lane < p.batch ? p.live_count[lane * kPlanSplit + u] : 0;
+  int cnt = 0;
+#pragma unroll
+  for (int u = 0; u < kPlanSplit; ++u) cnt += nc[u];
+  const int pc = plan_chunk(p.parts);
   int incl = cnt;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -362,8 +406,11 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
     const int idx = k / kKvHeads;  // live partition index over all requests
     const int b = __popcll(__ballot(incl <= idx));
     const int j = idx - (__builtin_amdgcn_readlane(incl, b) - __builtin_amdgcn_readlane(cnt, b));
-    const int part = p.live_parts[int64_t(b) * p.parts + j];
-    gated_item(p, part, k % kKvHeads, b, s_row, s_mask);
+    int nb[kPlanSplit];
+#pragma unroll
+    for (int u = 0; u < kPlanSplit; ++u) nb[u] = __builtin_amdgcn_readlane(nc[u], b);
+    const int part = p.live_parts[int64_t(b) * p.parts + live_slot(j, nb, pc)];
+    gated_item(p, part, j, k % kKvHeads, b, s_row, s_mask);
     // The next item rewrites the list this one read.
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -372,16 +419,12 @@ __global__ __launch_bounds__(64) void gated_decode_kernel(GatedParams p) {
 
 // One workgroup of kMergeWaves waves per (request, head): combine the live
 // partitions' (m, l, O) in one online pass, normalise, apply the gate. Wave w
-// takes list entries w, w + kMergeWaves, ...: their partition ids are loaded
-// 64 at a time, one per lane, and read back with v_readlane, so each round of
-// eight partials ((m, l) with O, lane l owning dims 4l .. 4l + 3) costs one
-// memory round trip. A partition whose rows were all out of range has m = -inf,
-// weight 0 and zero O. The waves' (m, l, O) meet in LDS.
-// Nothing waits for the live count before loading: the first 64 list entries
-// of each wave and the gate are loaded with it (entries past the count are
-// in the request's list row, their ids clamped, their partials loaded and then
-// given weight 0), so a request of up to 64 * kMergeWaves live partitions
-// costs two dependent memory round trips instead of four. Eight waves per
+// takes partial rows w, w + kMergeWaves, ... (the decode wrote the request's
+// live partitions' partials to rows 0 .. n-1 in partition order), so each
+// round of eight partials ((m, l) with O, lane l owning dims 4l .. 4l + 3)
+// costs one memory round trip, after the one that loads the chunk counts and
+// the gate. A partition whose rows were all out of range has m = -inf, weight
+// 0 and zero O. The waves' (m, l, O) meet in LDS. Eight waves per
 // workgroup (7.2 us per call) launched faster than sixteen (8.4 us) and four
 // (8.1 us) on the benchmark's 512 (request, head) pairs.
 constexpr int kMergeWaves = 8;
@@ -389,20 +432,16 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
   __shared__ float s_m[kMergeWaves], s_l[kMergeWaves];
   __shared__ f32x4 s_o[kMergeWaves][64];
   const int b = blockIdx.x, h = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int32_t *parts = p.live_parts + int64_t(b) * p.parts;
   const int64_t o_out = (int64_t(b) * kHeads + h) * kD + 4 * lane;
   const u32x2 gw = *reinterpret_cast<const u32x2 *>(p.gate + o_out);
-  int my_part = w + kMergeWaves * lane < p.parts ? parts[w + kMergeWaves * lane] : 0;
-  const int n = p.live_count[b];
+  int n = 0;
+#pragma unroll
+  for (int u = 0; u < kPlanSplit; ++u) n += p.live_count[b * kPlanSplit + u];
   const int64_t base = int64_t(b) * p.parts * kHeads + h;
   float m_run = -INFINITY, l_run = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
   constexpr int U = 8;
   for (int k0 = w; k0 < n; k0 += kMergeWaves * 64) {
-    if (k0 != w) {
-      const int kk = k0 + kMergeWaves * lane;
-      my_part = kk < p.parts ? parts[kk] : 0;
-    }
     const int cnt = (n - k0 + kMergeWaves - 1) / kMergeWaves < 64 ? (n - k0 + kMergeWaves - 1) / kMergeWaves : 64;
     for (int u0 = 0; u0 < cnt; u0 += U) {
       float2 ml[U];
@@ -410,9 +449,8 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = u0 + u;
-        int part = __builtin_amdgcn_readlane(my_part, i < 64 ? i : 63);
-        part = part < 0 ? 0 : (part >= p.parts ? p.parts - 1 : part);
-        const int64_t r = base + int64_t(part) * kHeads;
+        const int row = i < cnt ? k0 + kMergeWaves * i : 0;
+        const int64_t r = base + int64_t(row) * kHeads;
         ml[u] = *reinterpret_cast<const float2 *>(p.part_ml + r * 2);
         o[u] = *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane);
         if (i >= cnt) {
@@ -508,7 +546,7 @@ extern "C" uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, i
   if (parts == 1) return 16;
   // Partials (O, then (m, l)), the live partition lists and their counts.
   return uint64_t(batch) * parts * (kHeads * (kD + 2) * sizeof(float) + sizeof(int32_t)) +
-         align16(uint64_t(batch) * sizeof(int32_t));
+         align16(uint64_t(batch) * kPlanSplit * sizeof(int32_t));
 }
 
 extern "C" int32_t ifattn_gated_paged_attention_bf16(
@@ -544,7 +582,7 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
     p.part_o = static_cast<float *>(workspace);
     p.part_ml = p.part_o + uint64_t(batch) * p.parts * kHeads * kD;
     p.live_parts = reinterpret_cast<int32_t *>(p.part_ml + uint64_t(batch) * p.parts * kHeads * 2);
-    p.live_count = p.live_parts + uint64_t(batch) * p.parts;
+    p.live_count = p.live_parts + uint64_t(batch) * p.parts;  // [batch, kPlanSplit]
   }
   p.batch = int(batch);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -556,7 +594,7 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
   const int items = p.parts * kKvHeads * int(batch);
   const int waves = device_cus() * kWavesPerCu;
   if (p.live_parts) {
-    gated_plan_kernel<<<unsigned(batch), 1024, 0, s>>>(p);  // appends the step's rows too
+    gated_plan_kernel<<<unsigned(batch) * kPlanSplit, kPlanThreads, 0, s>>>(p);  // appends the step's rows too
   } else {
     const int vecs = int(batch) * (kRowBytes / 16) * 2;
     gated_append_kernel<<<(vecs + 255) / 256, 256, 0, s>>>(p.k_new, p.v_new, p.keys_out,
