@@ -101,6 +101,33 @@ def test_gated_attention_live_positions_after_dead_partitions():
     _check(rng, rows, mask, append, slots)
 
 
+@pytest.mark.parametrize("context", [100, 1100])
+def test_gated_attention_plan_chunk_edges(context):
+    """The plan lists each request's live partitions in four chunks of
+    ceil(parts / 4) partitions (two 64-position partitions at context 100:
+    chunks 2 and 3 empty; 18 at 1100: chunks of 5, 5, 5, 3). Live positions sit
+    only on the first and last position of chunks, and one request's only live
+    positions are in its last chunk."""
+    rng = np.random.default_rng(context)
+    batch = 5
+    slots = batch * context + 9
+    rows = rng.permutation(slots)[: batch * context].reshape(batch, context).astype(np.int64)
+    parts = (context + 63) // 64
+    pc = (parts + 3) // 4
+    edges = sorted({min(c * pc * 64, context - 1) for c in range(5)} |
+                   {min((c + 1) * pc * 64 - 1, context - 1) for c in range(4)})
+    live = np.zeros((batch, context), bool)
+    live[0, edges] = True
+    live[1, -1] = True                      # only the last position
+    live[2, :] = True
+    live[3, ::97] = True
+    live[4, min(3 * pc * 64, context - 1):] = True  # the last chunk only
+    mask = np.where(live, 0.0, -np.inf).astype(np.float32)
+    last = np.array([np.nonzero(r)[0][-1] for r in live])
+    append = rows[np.arange(batch), last].copy()
+    _check(rng, rows, mask, append, slots)
+
+
 def test_gated_attention_long_context():
     # 4 requests over 65536 positions (512 partitions of 128, merged), 2^18 + 3 slots
     _run(42, 4, 65536, (1 << 18) + 3)
