@@ -65,7 +65,7 @@ struct GatedParams {
   const int64_t *table;
   const float *mask;
   uint16_t *out;
-  float *part_o;   // [batch, parts, heads, D]
+  uint16_t *part_o;  // [batch, parts, heads, D] bf16 O / l
   float *part_ml;  // [batch, parts, heads, 2]
   int32_t *live_parts;  // [batch, parts]: each request's partitions with a live position
   int32_t *live_count;  // [batch, kPlanSplit] (per chunk of partitions); both null for a one-partition context
@@ -250,15 +250,21 @@ __device__ __forceinline__ void gated_item(const GatedParams &p, int part, int s
   } else {
     const int64_t prow = (int64_t(b) * p.parts + slot) * kHeads + head;
     if (g == 0) *reinterpret_cast<float2 *>(p.part_ml + prow * 2) = make_float2(m_run, l_tot);
+    // O / l in bf16 (half the partial bytes; the merge weighs it by l).
     // Written even without a live row (zeros, m = -inf): the merge loads every
     // listed partition's O alongside its (m, l).
-    float *po = p.part_o + prow * kD + 32 * g;
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    uint16_t *po = p.part_o + prow * kD + 32 * g;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        *reinterpret_cast<f32x4 *>(po + 128 * u + 4 * k) =
-            f32x4{elem(u, 4 * k), elem(u, 4 * k + 1), elem(u, 4 * k + 2), elem(u, 4 * k + 3)};
+      for (int k = 0; k < 4; ++k) {
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = pack_bf16x2(elem(u, 8 * k + 2 * i) * inv, elem(u, 8 * k + 2 * i + 1) * inv);
+        store_u32x4(po + 128 * u + 8 * k, w);
+      }
   }
 }
 
@@ -452,7 +458,9 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
         const int row = i < cnt ? k0 + kMergeWaves * i : 0;
         const int64_t r = base + int64_t(row) * kHeads;
         ml[u] = *reinterpret_cast<const float2 *>(p.part_ml + r * 2);
-        o[u] = *reinterpret_cast<const f32x4 *>(p.part_o + r * kD + 4 * lane);
+        const u32x2 ob = *reinterpret_cast<const u32x2 *>(p.part_o + r * kD + 4 * lane);
+        o[u] = f32x4{bf16_bits_to_f32(ob[0] & 0xffffu), bf16_bits_to_f32(ob[0] >> 16),
+                     bf16_bits_to_f32(ob[1] & 0xffffu), bf16_bits_to_f32(ob[1] >> 16)};
         if (i >= cnt) {
           ml[u] = make_float2(-INFINITY, 0.0f);
           o[u] = f32x4{0, 0, 0, 0};
@@ -470,7 +478,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void gated_merge_kernel(GatedPara
       for (int u = 0; u < U; ++u) {
         const float wt = ml[u].x == -INFINITY ? 0.0f : fast_exp2(ml[u].x - mx);
         l_run += wt * ml[u].y;
-        acc += wt * o[u];
+        acc += (wt * ml[u].y) * o[u];
       }
     }
   }
@@ -544,8 +552,8 @@ extern "C" uint64_t ifattn_gated_paged_attention_workspace_size(int64_t batch, i
   if (batch <= 0 || context <= 0) return 0;
   const uint64_t parts = uint64_t(parts_for(batch, context));
   if (parts == 1) return 16;
-  // Partials (O, then (m, l)), the live partition lists and their counts.
-  return uint64_t(batch) * parts * (kHeads * (kD + 2) * sizeof(float) + sizeof(int32_t)) +
+  // Partials (bf16 O / l, then fp32 (m, l)), the live partition lists and their counts.
+  return uint64_t(batch) * parts * (kHeads * (kD * sizeof(uint16_t) + 2 * sizeof(float)) + sizeof(int32_t)) +
          align16(uint64_t(batch) * kPlanSplit * sizeof(int32_t));
 }
 
@@ -579,8 +587,8 @@ extern "C" int32_t ifattn_gated_paged_attention_bf16(
   if (p.parts > 1) {
     if (!workspace || workspace_bytes < need || !aligned16(workspace))
       return fail(IFATTN_EWORKSPACE, "gated paged attention: workspace missing, short or misaligned");
-    p.part_o = static_cast<float *>(workspace);
-    p.part_ml = p.part_o + uint64_t(batch) * p.parts * kHeads * kD;
+    p.part_o = static_cast<uint16_t *>(workspace);
+    p.part_ml = reinterpret_cast<float *>(p.part_o + uint64_t(batch) * p.parts * kHeads * kD);
     p.live_parts = reinterpret_cast<int32_t *>(p.part_ml + uint64_t(batch) * p.parts * kHeads * 2);
     p.live_count = p.live_parts + uint64_t(batch) * p.parts;  // [batch, kPlanSplit]
   }
